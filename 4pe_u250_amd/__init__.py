@@ -1,0 +1,377 @@
+"""Python host mirror of the SwiftKV decode-attention stage (ctypes over libswiftkv.so).
+
+Mirrors the reference's local-PE attention entry
+    int4_swiftkv_attention_pe{0..3}(q, k, v, kv_cache, rope_lut_ddr,
+                                    activation_q, activation_scale,
+                                    layer_index, position)
+(kernel_HLS/swiftkv_attention.hpp:167-209) with the same argument meaning: the
+KV cache and the RoPE table are persistent device objects owned by the caller,
+`position` is the cached-token count (the step writes that token and attends
+[0, position]), and the outputs are the FP32 attention result plus the optional
+A14/E8M0 activation words for the O projection.  All 32 heads of a layer run on
+one GPU; a batch of sequences runs in one call.
+
+Follows the repo precedent of reaching native code through ctypes
+(run_autoround.py:5-21).  There is no CPU fallback: importing this module
+without the built library raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+from typing import Optional, Sequence
+
+import numpy as np
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+REPO_DIR = os.path.dirname(PKG_DIR)
+LIB_PATH = os.path.join(PKG_DIR, "libswiftkv.so")
+HEADER_PATH = os.path.join(REPO_DIR, "include", "swiftkv.h")
+
+HEADS = 32
+HEAD_DIM = 128
+MODEL_DIM = HEADS * HEAD_DIM
+GROUP = 32
+GROUPS_PER_HEAD = HEAD_DIM // GROUP
+REFERENCE_MAX_SEQ = 4096
+MAX_SEQ = 32768
+ROPE_LUT_BYTES_PER_POSITION = 512
+RECORD_BYTES = 320
+A14_WORD_BYTES = 56
+TOKEN_BYTES = 288          # algorithmic bytes per cached token-head: 2 x 128 codes + 8 FP32 scales
+
+OK, EINVAL, ERANGE, EHIP, ENOMEM, ESTATE = 0, -1, -2, -3, -4, -5
+DIST_NORMAL, DIST_STUDENT_T3 = 0, 1
+KERNEL_APPEND, KERNEL_ATTEND, KERNEL_COMBINE = 0, 1, 2
+_STATUS_NAMES = {EINVAL: "EINVAL", ERANGE: "ERANGE", EHIP: "EHIP", ENOMEM: "ENOMEM", ESTATE: "ESTATE"}
+
+
+class SwiftKVError(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(f"swiftkv error {code} ({_STATUS_NAMES.get(code, '?')}): {message}")
+        self.code = code
+
+
+_vp = C.c_void_p
+_i32 = C.c_int32
+_sz = C.c_size_t
+
+# name -> (restype, argtypes); every declaration of include/swiftkv.h.
+_SIGNATURES = {
+    "swiftkv_last_error": (C.c_char_p, []),
+    "swiftkv_version": (C.c_char_p, []),
+    "swiftkv_context_create": (C.c_int, [C.c_int, C.POINTER(_vp)]),
+    "swiftkv_context_destroy": (C.c_int, [_vp]),
+    "swiftkv_synchronize": (C.c_int, [_vp]),
+    "swiftkv_set_split_tokens": (C.c_int, [_vp, _i32]),
+    "swiftkv_rope_lut_load": (C.c_int, [_vp, _vp, _sz, C.POINTER(_vp)]),
+    "swiftkv_rope_lut_generate": (C.c_int, [_vp, _i32, C.c_double, C.POINTER(_vp)]),
+    "swiftkv_rope_lut_destroy": (C.c_int, [_vp]),
+    "swiftkv_rope_lut_positions": (_i32, [_vp]),
+    "swiftkv_rope_lut_export": (C.c_int, [_vp, _i32, _i32, _vp]),
+    "swiftkv_kv_cache_create": (C.c_int, [_vp, _i32, _i32, _i32, C.POINTER(_vp)]),
+    "swiftkv_kv_cache_destroy": (C.c_int, [_vp]),
+    "swiftkv_kv_cache_zero": (C.c_int, [_vp, _vp]),
+    "swiftkv_kv_cache_bytes": (_sz, [_vp]),
+    "swiftkv_kv_cache_read": (C.c_int, [_vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp]),
+    "swiftkv_kv_cache_export_records": (C.c_int, [_vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp]),
+    "swiftkv_kv_cache_import_records": (C.c_int, [_vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp]),
+    "swiftkv_attention_f32": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _vp]),
+    "swiftkv_attention_q17": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _vp]),
+    "swiftkv_append_tokens": (C.c_int, [_vp, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _i32]),
+    "swiftkv_fill_synthetic_f32": (C.c_int, [_vp, _vp, _sz, C.c_uint64, C.c_uint64, _i32, _i32]),
+    "swiftkv_kv_cache_fill_synthetic": (C.c_int, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, C.c_uint64,
+                                                  _i32, _i32]),
+    "swiftkv_device_alloc": (C.c_int, [_vp, _sz, C.POINTER(_vp)]),
+    "swiftkv_device_free": (C.c_int, [_vp, _vp]),
+    "swiftkv_memcpy_h2d": (C.c_int, [_vp, _vp, _vp, _sz]),
+    "swiftkv_memcpy_d2h": (C.c_int, [_vp, _vp, _vp, _sz]),
+    "swiftkv_memset_d": (C.c_int, [_vp, _vp, C.c_int, _sz]),
+    "swiftkv_convert_f32_q17": (C.c_int, [_vp, _vp, _vp, _sz]),
+    "swiftkv_timer_record": (C.c_int, [_vp, _i32]),
+    "swiftkv_timer_elapsed": (C.c_int, [_vp, _i32, _i32, C.POINTER(C.c_float)]),
+    "swiftkv_profile_enable": (C.c_int, [_vp, _i32]),
+    "swiftkv_profile_collect": (C.c_int, [_vp, C.POINTER(C.c_int64), C.POINTER(C.c_double)]),
+}
+
+_lib: Optional[C.CDLL] = None
+
+
+def header_symbols() -> list:
+    """Function names declared in include/swiftkv.h."""
+    text = open(HEADER_PATH).read()
+    return sorted(set(re.findall(r"\b(swiftkv_[a-z0-9_]+)\s*\(", text)))
+
+
+def lib() -> C.CDLL:
+    """Load libswiftkv.so; raises if it has not been built (no fallback)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"{LIB_PATH} is missing: build it with `python 4pe_u250_amd/build.py` "
+                          "(or __graft_entry__.build())")
+    L = C.CDLL(LIB_PATH)
+    for name, (res, args) in _SIGNATURES.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+def _check(rc: int) -> None:
+    if rc != OK:
+        msg = lib().swiftkv_last_error()
+        raise SwiftKVError(rc, msg.decode() if msg else "")
+
+
+def _host_ptr(a: np.ndarray):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+class DeviceBuffer:
+    """A device allocation with numpy-style upload/download (no framework needed)."""
+
+    def __init__(self, ctx: "Context", nbytes: int):
+        self.ctx = ctx
+        self.nbytes = int(nbytes)
+        p = C.c_void_p()
+        _check(lib().swiftkv_device_alloc(ctx.handle, self.nbytes, C.byref(p)))
+        self.ptr = p.value
+
+    @classmethod
+    def from_array(cls, ctx: "Context", a: np.ndarray) -> "DeviceBuffer":
+        a = np.ascontiguousarray(a)
+        buf = cls(ctx, a.nbytes)
+        buf.upload(a)
+        return buf
+
+    def upload(self, a: np.ndarray, offset: int = 0) -> None:
+        a = np.ascontiguousarray(a)
+        if offset + a.nbytes > self.nbytes:
+            raise ValueError("upload exceeds the buffer")
+        _check(lib().swiftkv_memcpy_h2d(self.ctx.handle, C.c_void_p(self.ptr + offset), _host_ptr(a), a.nbytes))
+
+    def download(self, dtype, shape, offset: int = 0) -> np.ndarray:
+        out = np.empty(shape, dtype)
+        if offset + out.nbytes > self.nbytes:
+            raise ValueError("download exceeds the buffer")
+        _check(lib().swiftkv_memcpy_d2h(self.ctx.handle, _host_ptr(out), C.c_void_p(self.ptr + offset), out.nbytes))
+        return out
+
+    def zero(self) -> None:
+        _check(lib().swiftkv_memset_d(self.ctx.handle, C.c_void_p(self.ptr), 0, self.nbytes))
+
+    def free(self) -> None:
+        if self.ptr:
+            _check(lib().swiftkv_device_free(self.ctx.handle, C.c_void_p(self.ptr)))
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            if self.ptr and self.ctx.handle:
+                lib().swiftkv_device_free(self.ctx.handle, C.c_void_p(self.ptr))
+        except Exception:
+            pass
+
+
+class Context:
+    """Device, HIP stream and workspace (one per GPU, not thread-safe)."""
+
+    def __init__(self, device: int = 0):
+        h = C.c_void_p()
+        _check(lib().swiftkv_context_create(device, C.byref(h)))
+        self.handle = h.value
+        self.device = device
+
+    def close(self) -> None:
+        if self.handle:
+            _check(lib().swiftkv_context_destroy(self.handle))
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def synchronize(self) -> None:
+        _check(lib().swiftkv_synchronize(self.handle))
+
+    def set_split_tokens(self, n: int) -> None:
+        _check(lib().swiftkv_set_split_tokens(self.handle, int(n)))
+
+    def alloc(self, nbytes: int) -> DeviceBuffer:
+        return DeviceBuffer(self, nbytes)
+
+    def to_device(self, a: np.ndarray) -> DeviceBuffer:
+        return DeviceBuffer.from_array(self, a)
+
+    def timer_record(self, slot: int) -> None:
+        _check(lib().swiftkv_timer_record(self.handle, slot))
+
+    def timer_elapsed_ms(self, a: int, b: int) -> float:
+        ms = C.c_float()
+        _check(lib().swiftkv_timer_elapsed(self.handle, a, b, C.byref(ms)))
+        return float(ms.value)
+
+    def profile(self, on: bool) -> None:
+        _check(lib().swiftkv_profile_enable(self.handle, 1 if on else 0))
+
+    def profile_collect(self):
+        counts = (C.c_int64 * 3)()
+        ms = (C.c_double * 3)()
+        _check(lib().swiftkv_profile_collect(self.handle, counts, ms))
+        return list(counts), list(ms)
+
+    def fill_synthetic(self, dst: DeviceBuffer, n: int, seed: int, stream: int, dist: int = DIST_NORMAL,
+                       outliers: bool = False) -> None:
+        """Elements [0, n) of the synthetic stream (seed, stream) as FP32 into dst."""
+        _check(lib().swiftkv_fill_synthetic_f32(self.handle, C.c_void_p(dst.ptr), n, seed, stream, dist,
+                                                1 if outliers else 0))
+
+    def convert_f32_q17(self, src: DeviceBuffer, dst: DeviceBuffer, n: int) -> None:
+        _check(lib().swiftkv_convert_f32_q17(self.handle, C.c_void_p(src.ptr), C.c_void_p(dst.ptr), n))
+
+
+class RopeLut:
+    """Device RoPE table (rope_lut.bin format: 512 bytes per position)."""
+
+    def __init__(self, ctx: Context, handle):
+        self.ctx = ctx
+        self.handle = handle
+
+    @classmethod
+    def load(cls, ctx: Context, image: bytes) -> "RopeLut":
+        buf = np.frombuffer(image, np.uint8)
+        h = C.c_void_p()
+        _check(lib().swiftkv_rope_lut_load(ctx.handle, _host_ptr(buf), buf.nbytes, C.byref(h)))
+        return cls(ctx, h.value)
+
+    @classmethod
+    def generate(cls, ctx: Context, positions: int = REFERENCE_MAX_SEQ, theta: float = 10000.0) -> "RopeLut":
+        h = C.c_void_p()
+        _check(lib().swiftkv_rope_lut_generate(ctx.handle, positions, theta, C.byref(h)))
+        return cls(ctx, h.value)
+
+    @property
+    def positions(self) -> int:
+        return int(lib().swiftkv_rope_lut_positions(self.handle))
+
+    def export(self, pos0: int = 0, n: Optional[int] = None) -> bytes:
+        n = self.positions - pos0 if n is None else n
+        out = np.zeros(n * ROPE_LUT_BYTES_PER_POSITION, np.uint8)
+        _check(lib().swiftkv_rope_lut_export(self.handle, pos0, n, _host_ptr(out)))
+        return out.tobytes()
+
+    def close(self) -> None:
+        if self.handle:
+            _check(lib().swiftkv_rope_lut_destroy(self.handle))
+            self.handle = None
+
+
+class KVCache:
+    """GPU-resident INT8/G32 KV cache for `max_batch` sequences x `layers` x 32 heads."""
+
+    def __init__(self, ctx: Context, layers: int, max_batch: int, max_seq_len: int):
+        h = C.c_void_p()
+        _check(lib().swiftkv_kv_cache_create(ctx.handle, layers, max_batch, max_seq_len, C.byref(h)))
+        self.ctx = ctx
+        self.handle = h.value
+        self.layers, self.max_batch, self.max_seq_len = layers, max_batch, max_seq_len
+
+    @property
+    def nbytes(self) -> int:
+        return int(lib().swiftkv_kv_cache_bytes(self.handle))
+
+    def zero(self) -> None:
+        _check(lib().swiftkv_kv_cache_zero(self.ctx.handle, self.handle))
+
+    def read(self, seq: int, layer: int, head: int, tok0: int, n: int):
+        """-> (k_codes int8 [n,128], v_codes int8 [n,128], k_scales f32 [n,4], v_scales f32 [n,4])."""
+        kc = np.empty((n, HEAD_DIM), np.int8)
+        vc = np.empty((n, HEAD_DIM), np.int8)
+        ks = np.empty((n, GROUPS_PER_HEAD), np.float32)
+        vs = np.empty((n, GROUPS_PER_HEAD), np.float32)
+        _check(lib().swiftkv_kv_cache_read(self.ctx.handle, self.handle, seq, layer, head, tok0, n,
+                                           _host_ptr(kc), _host_ptr(vc), _host_ptr(ks), _host_ptr(vs)))
+        return kc, vc, ks, vs
+
+    def export_records(self, seq: int, layer: int, head: int, tok0: int, n: int) -> np.ndarray:
+        out = np.empty((n, RECORD_BYTES), np.uint8)
+        _check(lib().swiftkv_kv_cache_export_records(self.ctx.handle, self.handle, seq, layer, head, tok0, n,
+                                                     _host_ptr(out)))
+        return out
+
+    def import_records(self, seq: int, layer: int, head: int, tok0: int, records: np.ndarray) -> None:
+        rec = np.ascontiguousarray(records, np.uint8).reshape(-1, RECORD_BYTES)
+        _check(lib().swiftkv_kv_cache_import_records(self.ctx.handle, self.handle, seq, layer, head, tok0,
+                                                     rec.shape[0], _host_ptr(rec)))
+
+    def fill_synthetic(self, rope_lut: "RopeLut", ntok: int, seed: int, layer0: int = 0, nlayers: Optional[int] = None,
+                       seq0: int = 0, nseq: Optional[int] = None, dist: int = DIST_NORMAL,
+                       k_outliers: bool = False) -> None:
+        """Fill tokens [0, ntok) from synthetic streams through the append rule."""
+        nlayers = self.layers - layer0 if nlayers is None else nlayers
+        nseq = self.max_batch - seq0 if nseq is None else nseq
+        _check(lib().swiftkv_kv_cache_fill_synthetic(self.ctx.handle, self.handle, rope_lut.handle, layer0, nlayers,
+                                                     seq0, nseq, ntok, seed, dist, 1 if k_outliers else 0))
+
+    def close(self) -> None:
+        if self.handle:
+            _check(lib().swiftkv_kv_cache_destroy(self.handle))
+            self.handle = None
+
+
+def _ptr(x) -> Optional[int]:
+    if x is None:
+        return None
+    if isinstance(x, DeviceBuffer):
+        return x.ptr
+    return int(x)
+
+
+def swiftkv_attention(ctx: Context, q, k, v, kv_cache: KVCache, rope_lut: RopeLut,
+                      activation_q, activation_scale, layer_index: int, position,
+                      out, q17: bool = False) -> None:
+    """One decode-attention step (the drop-in for int4_swiftkv_attention_peN).
+
+    q, k, v: device [batch][4096] (FP32, or Q15.17 int32 when q17=True);
+    position: int (batch 1) or a sequence of cached-token counts, one per
+    sequence; out: device [batch][4096] FP32; activation_q/activation_scale:
+    device [batch][128][56] bytes and [batch][128] E8M0 codes, or None.
+    Asynchronous on the context stream.
+    """
+    pos = np.ascontiguousarray(np.atleast_1d(np.asarray(position, dtype=np.int32)))
+    fn = lib().swiftkv_attention_q17 if q17 else lib().swiftkv_attention_f32
+    _check(fn(ctx.handle, _ptr(q), _ptr(k), _ptr(v), kv_cache.handle, rope_lut.handle,
+              _ptr(activation_q), _ptr(activation_scale), int(layer_index), _host_ptr(pos), int(pos.size),
+              _ptr(out)))
+
+
+def swiftkv_append_tokens(ctx: Context, k, v, kv_cache: KVCache, rope_lut: RopeLut, layer_index: int,
+                          seq: int, pos0: int, n: int, q17: bool = False) -> None:
+    """Bulk append (prefill) of n tokens [pos0, pos0+n) of one sequence."""
+    _check(lib().swiftkv_append_tokens(ctx.handle, _ptr(k), _ptr(v), 1 if q17 else 0, kv_cache.handle,
+                                       rope_lut.handle, int(layer_index), int(seq), int(pos0), int(n)))
+
+
+def unpack_a14(words: np.ndarray) -> np.ndarray:
+    """[..., 56] bytes of packed 14-bit lanes -> int16 [..., 32] (lane 0 = bits [13:0])."""
+    w = np.ascontiguousarray(words, np.uint8)
+    bits = np.unpackbits(w, axis=-1, bitorder="little")[..., :32 * 14]
+    bits = bits.reshape(w.shape[:-1] + (32, 14)).astype(np.int32)
+    vals = (bits << np.arange(14, dtype=np.int32)).sum(-1)
+    vals = np.where(vals >= 8192, vals - 16384, vals)
+    return vals.astype(np.int16)
+
+
+def scale_bits(shifts: np.ndarray) -> np.ndarray:
+    """FP32 bit pattern of the G32 scale 2^(s-17)."""
+    return ((np.asarray(shifts, np.uint32) + np.uint32(110)) << np.uint32(23)).astype(np.uint32)
+
+
+def version() -> str:
+    return lib().swiftkv_version().decode()

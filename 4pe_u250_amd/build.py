@@ -1,0 +1,73 @@
+"""Build recipe for libswiftkv.so (gfx950) and the CPU oracle.
+
+    python 4pe_u250_amd/build.py          # library + oracle (+ oracle/_ref when
+                                          # the reference sources are present)
+
+The library is compiled in-tree with hipcc for gfx950 only.  All HIP code is
+built with packed-FP32 instruction selection disabled.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+REPO = os.path.dirname(PKG_DIR)
+CSRC = os.path.join(PKG_DIR, "csrc")
+LIB = os.path.join(PKG_DIR, "libswiftkv.so")
+ORACLE_DIR = os.path.join(REPO, "oracle")
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    "-Wall",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+SOURCES = ["swiftkv_kernels.hip", "swiftkv_synth.hip", "swiftkv_capi.cpp"]
+
+
+def _run(cmd, cwd=None):
+    proc = subprocess.run(cmd, cwd=cwd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    # hipcc's host pass does not know the packed-fp32 feature and says so; drop that line.
+    lines = [ln for ln in proc.stdout.splitlines() if "packed-fp32-ops' is not a recognized feature" not in ln]
+    if proc.returncode != 0:
+        sys.stderr.write("\n".join(lines) + "\n")
+        raise RuntimeError(f"command failed ({proc.returncode}): {' '.join(cmd)}")
+    return "\n".join(lines)
+
+
+def build_library(verbose: bool = False) -> str:
+    srcs = [os.path.join(CSRC, s) for s in SOURCES]
+    tmp = LIB + ".tmp"
+    cmd = [HIPCC, *HIP_FLAGS, "-I", os.path.join(REPO, "include"), *srcs, "-o", tmp]
+    out = _run(cmd)
+    if verbose and out.strip():
+        print(out)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+def build_oracle(verbose: bool = False) -> None:
+    make = shutil.which("make")
+    if make is None:
+        raise RuntimeError("make not found")
+    out = _run([make, "-s", "-B", "-C", ORACLE_DIR])
+    if verbose and out.strip():
+        print(out)
+
+
+def main() -> int:
+    build_oracle(verbose=True)
+    print(build_library(verbose=True))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

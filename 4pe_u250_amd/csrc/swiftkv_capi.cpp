@@ -1,0 +1,786 @@
+// swiftkv_capi.cpp -- host side of the SwiftKV C ABI (include/swiftkv.h).
+//
+// Owns the HIP stream, the device-resident RoPE table and KV arena, the
+// split-context workspace and the argument validation that the reference's
+// XRT host performs before each launch (host/decode_host.cpp:1340-1349).
+// Kernels live in swiftkv_kernels.hip; this file only validates, sizes and
+// enqueues.  No exception crosses the C boundary: every entry point converts
+// failures to a negative status and a thread-local message.
+#include "../../include/swiftkv.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "swiftkv_common.hpp"
+
+namespace {
+
+using namespace swiftkv;
+
+constexpr int kTimerSlots = 64;
+constexpr int kProfilePairs = 8192;
+constexpr size_t kRopeEntryBytes = sizeof(int2);
+constexpr int kMaxSplitTokens = SWIFTKV_MAX_SEQ;
+
+static_assert(SWIFTKV_HEADS == kHeads && SWIFTKV_HEAD_DIM == kHeadDim, "geometry");
+static_assert(SWIFTKV_ROPE_LUT_BYTES_PER_POSITION == 512, "RoPE LUT image: 8 x 64-byte words per position");
+static_assert(SWIFTKV_RECORD_BYTES == 5 * 64, "record is [meta, K0, K1, V0, V1]");
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int ok() {
+    g_last_error.clear();
+    return SWIFTKV_OK;
+}
+
+#define SKV_HIP(expr)                                                                          \
+    do {                                                                                       \
+        hipError_t e_ = (expr);                                                                \
+        if (e_ != hipSuccess)                                                                  \
+            return fail(SWIFTKV_EHIP, "%s: %s (%s:%d)", #expr, hipGetErrorString(e_), __FILE__, \
+                        __LINE__);                                                             \
+    } while (0)
+
+struct ProfilePair {
+    hipEvent_t begin;
+    hipEvent_t end;
+    int kind;
+};
+
+}  // namespace
+
+struct swiftkv_context {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    int32_t split_tokens = 0;   // 0: heuristic
+    // split-context workspace
+    float* qhat = nullptr;
+    size_t qhat_elems = 0;
+    float* partials = nullptr;
+    size_t partial_elems = 0;
+    // timing
+    hipEvent_t timers[kTimerSlots] = {};
+    bool profiling = false;
+    std::vector<ProfilePair> profile_pool;
+    size_t profile_used = 0;
+};
+
+struct swiftkv_rope_lut {
+    swiftkv_context* ctx = nullptr;
+    int32_t positions = 0;
+    int2* table = nullptr;              // device [positions][64] (cos, sin)
+    std::vector<int2> host;             // host copy for export
+};
+
+struct swiftkv_kv_cache {
+    swiftkv_context* ctx = nullptr;
+    int32_t layers = 0;
+    int32_t max_batch = 0;
+    int32_t seq_cap = 0;
+    int64_t page_bytes = 0;
+    size_t bytes = 0;
+    int8_t* base = nullptr;
+};
+
+namespace {
+
+int set_device(const swiftkv_context* ctx) {
+    SKV_HIP(hipSetDevice(ctx->device));
+    return SWIFTKV_OK;
+}
+
+// Device buffer growth.  The old buffer may still be read by queued kernels,
+// so the stream is drained before it is released.
+template <typename T>
+int ensure(swiftkv_context* ctx, T*& ptr, size_t& have, size_t need) {
+    if (need <= have) return SWIFTKV_OK;
+    if (ptr) {
+        SKV_HIP(hipStreamSynchronize(ctx->stream));
+        SKV_HIP(hipFree(ptr));
+        ptr = nullptr;
+        have = 0;
+    }
+    void* p = nullptr;
+    if (hipMalloc(&p, need * sizeof(T)) != hipSuccess)
+        return fail(SWIFTKV_ENOMEM, "hipMalloc of %zu bytes failed", need * sizeof(T));
+    ptr = static_cast<T*>(p);
+    have = need;
+    return SWIFTKV_OK;
+}
+
+// Closed form of scripts/generate_rope_lut.py:67-91: RNE(2^17 cos|sin(pos *
+// theta^(-j/64))), saturated to signed 19 bits.
+int32_t q17_19bit(double x) {
+    double r = std::nearbyint(x * 131072.0);
+    r = std::min(262143.0, std::max(-262144.0, r));
+    return static_cast<int32_t>(r);
+}
+
+uint32_t get_bits(const uint8_t* base, int bit, int width) {
+    uint32_t v = 0;
+    for (int b = 0; b < width; ++b) {
+        const int src = bit + b;
+        v |= static_cast<uint32_t>((base[src >> 3] >> (src & 7)) & 1u) << b;
+    }
+    return v;
+}
+
+void put_bits(uint8_t* base, int bit, int width, uint32_t value) {
+    for (int b = 0; b < width; ++b) {
+        const int dst = bit + b;
+        if ((value >> b) & 1u) base[dst >> 3] |= static_cast<uint8_t>(1u << (dst & 7));
+    }
+}
+
+int32_t sext19(uint32_t raw) {
+    return (raw & 0x40000u) ? static_cast<int32_t>(raw | 0xfff80000u) : static_cast<int32_t>(raw);
+}
+
+int upload_lut(swiftkv_context* ctx, std::vector<int2>&& host, int32_t positions, swiftkv_rope_lut** out) {
+    swiftkv_rope_lut* lut = new (std::nothrow) swiftkv_rope_lut();
+    if (!lut) return fail(SWIFTKV_ENOMEM, "out of host memory");
+    lut->ctx = ctx;
+    lut->positions = positions;
+    lut->host = std::move(host);
+    const size_t bytes = lut->host.size() * kRopeEntryBytes;
+    void* p = nullptr;
+    if (hipMalloc(&p, bytes) != hipSuccess) {
+        delete lut;
+        return fail(SWIFTKV_ENOMEM, "hipMalloc of RoPE table (%zu bytes) failed", bytes);
+    }
+    lut->table = static_cast<int2*>(p);
+    hipError_t e = hipMemcpy(lut->table, lut->host.data(), bytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(lut->table);
+        delete lut;
+        return fail(SWIFTKV_EHIP, "RoPE table upload: %s", hipGetErrorString(e));
+    }
+    *out = lut;
+    return ok();
+}
+
+// Tokens per split: enough work items to fill 256 CUs several times over,
+// without splitting a (sequence, head) finer than one 256-token quantum.
+int32_t choose_split(const swiftkv_context* ctx, const int32_t* positions, int32_t batch) {
+    if (ctx->split_tokens > 0) return ctx->split_tokens;
+    int64_t quanta = 0;
+    for (int32_t b = 0; b < batch; ++b) quanta += (positions[b] + kSplitQuantum) / kSplitQuantum;
+    quanta *= kHeads;
+    int64_t mult = quanta / 8192;
+    mult = std::max<int64_t>(1, std::min<int64_t>(mult, 8));
+    return static_cast<int32_t>(mult * kSplitQuantum);
+}
+
+int validate_step(swiftkv_context* ctx, const void* q, const void* k, const void* v,
+                  const swiftkv_kv_cache* kv, const swiftkv_rope_lut* lut, const uint8_t* act_q,
+                  const uint8_t* act_scale, int32_t layer, const int32_t* positions, int32_t batch,
+                  const float* out) {
+    if (!ctx) return fail(SWIFTKV_EINVAL, "null context");
+    if (!q || !k || !v || !out) return fail(SWIFTKV_EINVAL, "null q/k/v/out pointer");
+    if (!kv || kv->ctx != ctx) return fail(SWIFTKV_EINVAL, "kv_cache is null or belongs to another context");
+    if (!lut || lut->ctx != ctx) return fail(SWIFTKV_EINVAL, "rope_lut is null or belongs to another context");
+    if ((act_q == nullptr) != (act_scale == nullptr))
+        return fail(SWIFTKV_EINVAL, "activation_q and activation_scale must both be set or both be null");
+    if (!positions) return fail(SWIFTKV_EINVAL, "null positions");
+    if (batch < 1 || batch > kv->max_batch)
+        return fail(SWIFTKV_ERANGE, "batch %d outside [1, %d]", batch, kv->max_batch);
+    if (layer < 0 || layer >= kv->layers)
+        return fail(SWIFTKV_ERANGE, "layer_index %d outside [0, %d)", layer, kv->layers);
+    const int32_t limit = std::min(kv->seq_cap, lut->positions);
+    for (int32_t b = 0; b < batch; ++b)
+        if (positions[b] < 0 || positions[b] >= limit)
+            return fail(SWIFTKV_ERANGE, "positions[%d] = %d outside [0, %d) (cache %d, RoPE table %d)", b,
+                        positions[b], limit, kv->seq_cap, lut->positions);
+    return SWIFTKV_OK;
+}
+
+ProfilePair* profile_begin(swiftkv_context* ctx, int kind) {
+    if (!ctx->profiling || ctx->profile_used >= ctx->profile_pool.size()) return nullptr;
+    ProfilePair* p = &ctx->profile_pool[ctx->profile_used++];
+    p->kind = kind;
+    if (hipEventRecord(p->begin, ctx->stream) != hipSuccess) return nullptr;
+    return p;
+}
+
+void profile_end(swiftkv_context* ctx, ProfilePair* p) {
+    if (p) (void)hipEventRecord(p->end, ctx->stream);
+}
+
+int run_step(swiftkv_context* ctx, const void* q, const void* k, const void* v, bool q17,
+             swiftkv_kv_cache* kv, const swiftkv_rope_lut* lut, uint8_t* act_q, uint8_t* act_scale,
+             int32_t layer, const int32_t* positions, int32_t batch, float* out) {
+    int rc = validate_step(ctx, q, k, v, kv, lut, act_q, act_scale, layer, positions, batch, out);
+    if (rc) return rc;
+    if ((rc = set_device(ctx))) return rc;
+    const size_t elem_bytes = 4;
+    for (int32_t b0 = 0; b0 < batch; b0 += kMaxBatchPerLaunch) {
+        const int32_t nb = std::min<int32_t>(kMaxBatchPerLaunch, batch - b0);
+        StepArgs a;
+        std::memset(&a, 0, sizeof(a));
+        const size_t row0 = static_cast<size_t>(b0) * kModelDim;
+        a.q = static_cast<const char*>(q) + row0 * elem_bytes;
+        a.k = static_cast<const char*>(k) + row0 * elem_bytes;
+        a.v = static_cast<const char*>(v) + row0 * elem_bytes;
+        a.kv = CacheView{kv->base, kv->page_bytes, kv->seq_cap, kv->layers};
+        a.lut = lut->table;
+        a.lut_positions = lut->positions;
+        a.layer = layer;
+        a.batch = nb;
+        a.slot0 = b0;
+        int32_t max_pos = 0;
+        for (int32_t b = 0; b < nb; ++b) {
+            a.positions[b] = positions[b0 + b];
+            max_pos = std::max(max_pos, a.positions[b]);
+        }
+        a.split_tokens = choose_split(ctx, a.positions, nb);
+        const int32_t grid_splits = (max_pos + 1 + a.split_tokens - 1) / a.split_tokens;
+        a.max_splits = grid_splits;
+        if ((rc = ensure(ctx, ctx->qhat, ctx->qhat_elems, static_cast<size_t>(nb) * kModelDim))) return rc;
+        if ((rc = ensure(ctx, ctx->partials, ctx->partial_elems,
+                         static_cast<size_t>(nb) * kHeads * grid_splits * kPartialStride)))
+            return rc;
+        a.qhat = ctx->qhat;
+        a.partials = ctx->partials;
+        a.out = out + row0;
+        a.act_q = act_q ? act_q + static_cast<size_t>(b0) * kHeads * kGroupsPerHead * SWIFTKV_A14_WORD_BYTES
+                        : nullptr;
+        a.act_scale = act_scale ? act_scale + static_cast<size_t>(b0) * kHeads * kGroupsPerHead : nullptr;
+
+        ProfilePair* p = profile_begin(ctx, SWIFTKV_KERNEL_APPEND);
+        SKV_HIP(launch_append_step(a, q17, ctx->stream));
+        profile_end(ctx, p);
+        p = profile_begin(ctx, SWIFTKV_KERNEL_ATTEND);
+        SKV_HIP(launch_attend(a, grid_splits, ctx->stream));
+        profile_end(ctx, p);
+        p = profile_begin(ctx, SWIFTKV_KERNEL_COMBINE);
+        SKV_HIP(launch_combine(a, ctx->stream));
+        profile_end(ctx, p);
+    }
+    return ok();
+}
+
+int check_cache_range(const swiftkv_context* ctx, const swiftkv_kv_cache* kv, int32_t seq, int32_t layer,
+                      int32_t head, int32_t tok0, int32_t n) {
+    if (!ctx) return fail(SWIFTKV_EINVAL, "null context");
+    if (!kv || kv->ctx != ctx) return fail(SWIFTKV_EINVAL, "kv_cache is null or belongs to another context");
+    if (seq < 0 || seq >= kv->max_batch) return fail(SWIFTKV_ERANGE, "sequence %d outside [0, %d)", seq, kv->max_batch);
+    if (layer < 0 || layer >= kv->layers) return fail(SWIFTKV_ERANGE, "layer %d outside [0, %d)", layer, kv->layers);
+    if (head < 0 || head >= kHeads) return fail(SWIFTKV_ERANGE, "head %d outside [0, %d)", head, kHeads);
+    if (n < 0 || tok0 < 0 || static_cast<int64_t>(tok0) + n > kv->seq_cap)
+        return fail(SWIFTKV_ERANGE, "tokens [%d, %d) outside the cache capacity %d", tok0, tok0 + n, kv->seq_cap);
+    return SWIFTKV_OK;
+}
+
+// Shift of a stored G32 scale 2^(s-17): the biased exponent minus 110.
+bool scale_to_shift(float scale, uint8_t* s) {
+    uint32_t bits;
+    std::memcpy(&bits, &scale, 4);
+    const uint32_t e = bits >> 23;   // sign bit must be zero
+    if ((bits & 0x7fffffu) != 0 || e < 110u || e > 110u + 31u) return false;
+    *s = static_cast<uint8_t>(e - 110u);
+    return true;
+}
+
+float shift_to_scale(uint32_t s) {
+    const uint32_t bits = (s + 110u) << 23;
+    float f;
+    std::memcpy(&f, &bits, 4);
+    return f;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* swiftkv_last_error(void) { return g_last_error.c_str(); }
+
+const char* swiftkv_version(void) { return "swiftkv-mi355x 0.1 (gfx950)"; }
+
+int swiftkv_context_create(int device, swiftkv_context** out) {
+    if (!out) return fail(SWIFTKV_EINVAL, "null output pointer");
+    *out = nullptr;
+    int count = 0;
+    SKV_HIP(hipGetDeviceCount(&count));
+    if (device < 0 || device >= count) return fail(SWIFTKV_ERANGE, "device %d outside [0, %d)", device, count);
+    SKV_HIP(hipSetDevice(device));
+    swiftkv_context* ctx = new (std::nothrow) swiftkv_context();
+    if (!ctx) return fail(SWIFTKV_ENOMEM, "out of host memory");
+    ctx->device = device;
+    hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+    for (int i = 0; e == hipSuccess && i < kTimerSlots; ++i) e = hipEventCreate(&ctx->timers[i]);
+    if (e != hipSuccess) {
+        swiftkv_context_destroy(ctx);
+        return fail(SWIFTKV_EHIP, "stream/event creation: %s", hipGetErrorString(e));
+    }
+    *out = ctx;
+    return ok();
+}
+
+int swiftkv_context_destroy(swiftkv_context* ctx) {
+    if (!ctx) return ok();
+    (void)hipSetDevice(ctx->device);
+    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->qhat) (void)hipFree(ctx->qhat);
+    if (ctx->partials) (void)hipFree(ctx->partials);
+    for (auto& t : ctx->timers)
+        if (t) (void)hipEventDestroy(t);
+    for (auto& p : ctx->profile_pool) {
+        (void)hipEventDestroy(p.begin);
+        (void)hipEventDestroy(p.end);
+    }
+    if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return ok();
+}
+
+int swiftkv_synchronize(swiftkv_context* ctx) {
+    if (!ctx) return fail(SWIFTKV_EINVAL, "null context");
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    SKV_HIP(hipStreamSynchronize(ctx->stream));
+    return ok();
+}
+
+int swiftkv_set_split_tokens(swiftkv_context* ctx, int32_t split_tokens) {
+    if (!ctx) return fail(SWIFTKV_EINVAL, "null context");
+    if (split_tokens != 0 &&
+        (split_tokens < kSplitQuantum || split_tokens > kMaxSplitTokens || split_tokens % kSplitQuantum != 0))
+        return fail(SWIFTKV_EINVAL, "split_tokens %d must be 0 or a multiple of %d in [%d, %d]", split_tokens,
+                    kSplitQuantum, kSplitQuantum, kMaxSplitTokens);
+    ctx->split_tokens = split_tokens;
+    return ok();
+}
+
+// ---------------------------------------------------------------- RoPE table
+
+int swiftkv_rope_lut_load(swiftkv_context* ctx, const void* image, size_t image_bytes, swiftkv_rope_lut** out) {
+    if (!ctx || !image || !out) return fail(SWIFTKV_EINVAL, "null argument");
+    *out = nullptr;
+    if (image_bytes == 0 || image_bytes % SWIFTKV_ROPE_LUT_BYTES_PER_POSITION != 0)
+        return fail(SWIFTKV_EINVAL, "RoPE image of %zu bytes is not a whole number of %d-byte positions",
+                    image_bytes, SWIFTKV_ROPE_LUT_BYTES_PER_POSITION);
+    const size_t npos = image_bytes / SWIFTKV_ROPE_LUT_BYTES_PER_POSITION;
+    if (npos > static_cast<size_t>(SWIFTKV_MAX_SEQ))
+        return fail(SWIFTKV_ERANGE, "RoPE image holds %zu positions, more than %d", npos, SWIFTKV_MAX_SEQ);
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    const uint8_t* bytes = static_cast<const uint8_t*>(image);
+    std::vector<int2> host(npos * kRopePairs);
+    for (size_t p = 0; p < npos; ++p)
+        for (int j = 0; j < kRopePairs; ++j) {
+            const uint8_t* slot = bytes + (p * 4 + static_cast<size_t>(j / 16)) * 128;
+            const int lane = j % 16;
+            host[p * kRopePairs + j] =
+                make_int2(sext19(get_bits(slot, 38 * lane, 19)), sext19(get_bits(slot, 38 * lane + 19, 19)));
+        }
+    return upload_lut(ctx, std::move(host), static_cast<int32_t>(npos), out);
+}
+
+int swiftkv_rope_lut_generate(swiftkv_context* ctx, int32_t positions, double theta, swiftkv_rope_lut** out) {
+    if (!ctx || !out) return fail(SWIFTKV_EINVAL, "null argument");
+    *out = nullptr;
+    if (positions < 1 || positions > SWIFTKV_MAX_SEQ)
+        return fail(SWIFTKV_ERANGE, "positions %d outside [1, %d]", positions, SWIFTKV_MAX_SEQ);
+    if (!(theta > 1.0) || !std::isfinite(theta)) return fail(SWIFTKV_EINVAL, "theta must be finite and > 1");
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    std::vector<int2> host(static_cast<size_t>(positions) * kRopePairs);
+    for (int32_t p = 0; p < positions; ++p)
+        for (int j = 0; j < kRopePairs; ++j) {
+            const double freq = 1.0 / std::pow(theta, static_cast<double>(j) / kRopePairs);
+            const double ang = static_cast<double>(p) * freq;
+            host[static_cast<size_t>(p) * kRopePairs + j] = make_int2(q17_19bit(std::cos(ang)), q17_19bit(std::sin(ang)));
+        }
+    return upload_lut(ctx, std::move(host), positions, out);
+}
+
+int swiftkv_rope_lut_destroy(swiftkv_rope_lut* lut) {
+    if (!lut) return ok();
+    (void)hipSetDevice(lut->ctx->device);
+    (void)hipStreamSynchronize(lut->ctx->stream);
+    if (lut->table) (void)hipFree(lut->table);
+    delete lut;
+    return ok();
+}
+
+int32_t swiftkv_rope_lut_positions(const swiftkv_rope_lut* lut) { return lut ? lut->positions : 0; }
+
+int swiftkv_rope_lut_export(const swiftkv_rope_lut* lut, int32_t pos0, int32_t n, void* image) {
+    if (!lut || !image) return fail(SWIFTKV_EINVAL, "null argument");
+    if (pos0 < 0 || n < 0 || static_cast<int64_t>(pos0) + n > lut->positions)
+        return fail(SWIFTKV_ERANGE, "positions [%d, %d) outside the table (%d)", pos0, pos0 + n, lut->positions);
+    uint8_t* bytes = static_cast<uint8_t*>(image);
+    std::memset(bytes, 0, static_cast<size_t>(n) * SWIFTKV_ROPE_LUT_BYTES_PER_POSITION);
+    for (int32_t p = 0; p < n; ++p)
+        for (int j = 0; j < kRopePairs; ++j) {
+            const int2 cs = lut->host[static_cast<size_t>(pos0 + p) * kRopePairs + j];
+            uint8_t* slot = bytes + (static_cast<size_t>(p) * 4 + static_cast<size_t>(j / 16)) * 128;
+            const int lane = j % 16;
+            put_bits(slot, 38 * lane, 19, static_cast<uint32_t>(cs.x) & 0x7ffffu);
+            put_bits(slot, 38 * lane + 19, 19, static_cast<uint32_t>(cs.y) & 0x7ffffu);
+        }
+    return ok();
+}
+
+// ---------------------------------------------------------------- KV cache
+
+int swiftkv_kv_cache_create(swiftkv_context* ctx, int32_t layers, int32_t max_batch, int32_t max_seq_len,
+                            swiftkv_kv_cache** out) {
+    if (!ctx || !out) return fail(SWIFTKV_EINVAL, "null argument");
+    *out = nullptr;
+    if (layers < 1 || layers > 64) return fail(SWIFTKV_EINVAL, "layers %d outside [1, 64]", layers);
+    if (max_batch < 1 || max_batch > 4096) return fail(SWIFTKV_EINVAL, "max_batch %d outside [1, 4096]", max_batch);
+    if (max_seq_len < 1 || max_seq_len > SWIFTKV_MAX_SEQ)
+        return fail(SWIFTKV_EINVAL, "max_seq_len %d outside [1, %d]", max_seq_len, SWIFTKV_MAX_SEQ);
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    swiftkv_kv_cache* kv = new (std::nothrow) swiftkv_kv_cache();
+    if (!kv) return fail(SWIFTKV_ENOMEM, "out of host memory");
+    kv->ctx = ctx;
+    kv->layers = layers;
+    kv->max_batch = max_batch;
+    kv->seq_cap = (max_seq_len + kSeqAlign - 1) / kSeqAlign * kSeqAlign;
+    kv->page_bytes = static_cast<int64_t>(kv->seq_cap) * kTokenBytes;
+    kv->bytes = static_cast<size_t>(kv->page_bytes) * kHeads * layers * max_batch;
+    void* p = nullptr;
+    if (hipMalloc(&p, kv->bytes) != hipSuccess) {
+        delete kv;
+        return fail(SWIFTKV_ENOMEM, "hipMalloc of KV cache (%zu bytes) failed", static_cast<size_t>(kv->bytes));
+    }
+    kv->base = static_cast<int8_t*>(p);
+    hipError_t e = hipMemsetAsync(kv->base, 0, kv->bytes, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        (void)hipFree(kv->base);
+        delete kv;
+        return fail(SWIFTKV_EHIP, "KV cache zero-fill: %s", hipGetErrorString(e));
+    }
+    *out = kv;
+    return ok();
+}
+
+int swiftkv_kv_cache_destroy(swiftkv_kv_cache* kv) {
+    if (!kv) return ok();
+    (void)hipSetDevice(kv->ctx->device);
+    (void)hipStreamSynchronize(kv->ctx->stream);
+    if (kv->base) (void)hipFree(kv->base);
+    delete kv;
+    return ok();
+}
+
+int swiftkv_kv_cache_zero(swiftkv_context* ctx, swiftkv_kv_cache* kv) {
+    if (!ctx || !kv || kv->ctx != ctx) return fail(SWIFTKV_EINVAL, "null or foreign argument");
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    SKV_HIP(hipMemsetAsync(kv->base, 0, kv->bytes, ctx->stream));
+    return ok();
+}
+
+size_t swiftkv_kv_cache_bytes(const swiftkv_kv_cache* kv) { return kv ? kv->bytes : 0; }
+
+int swiftkv_kv_cache_read(swiftkv_context* ctx, const swiftkv_kv_cache* kv, int32_t seq, int32_t layer,
+                          int32_t head, int32_t tok0, int32_t n, int8_t* k_codes, int8_t* v_codes,
+                          float* k_scales, float* v_scales) {
+    int rc = check_cache_range(ctx, kv, seq, layer, head, tok0, n);
+    if (rc) return rc;
+    if ((rc = set_device(ctx))) return rc;
+    if (n == 0) return ok();
+    const int8_t* page = page_ptr(CacheView{kv->base, kv->page_bytes, kv->seq_cap, kv->layers}, seq, layer, head);
+    const size_t cap = static_cast<size_t>(kv->seq_cap);
+    SKV_HIP(hipStreamSynchronize(ctx->stream));
+    if (k_codes)
+        SKV_HIP(hipMemcpy(k_codes, page + static_cast<size_t>(tok0) * kCodeBytes,
+                          static_cast<size_t>(n) * kCodeBytes, hipMemcpyDeviceToHost));
+    if (v_codes)
+        SKV_HIP(hipMemcpy(v_codes, page + (cap + tok0) * kCodeBytes, static_cast<size_t>(n) * kCodeBytes,
+                          hipMemcpyDeviceToHost));
+    if (k_scales || v_scales) {
+        std::vector<float> sc(static_cast<size_t>(n) * 8);
+        SKV_HIP(hipMemcpy(sc.data(), page + cap * 2 * kCodeBytes + static_cast<size_t>(tok0) * kScaleBytes,
+                          sc.size() * sizeof(float), hipMemcpyDeviceToHost));
+        for (int32_t t = 0; t < n; ++t)
+            for (int g = 0; g < kGroupsPerHead; ++g) {
+                if (k_scales) k_scales[static_cast<size_t>(t) * 4 + g] = sc[static_cast<size_t>(t) * 8 + 2 * g];
+                if (v_scales) v_scales[static_cast<size_t>(t) * 4 + g] = sc[static_cast<size_t>(t) * 8 + 2 * g + 1];
+            }
+    }
+    return ok();
+}
+
+int swiftkv_kv_cache_export_records(swiftkv_context* ctx, const swiftkv_kv_cache* kv, int32_t seq, int32_t layer,
+                                    int32_t head, int32_t tok0, int32_t n, void* records) {
+    if (!records && n > 0) return fail(SWIFTKV_EINVAL, "null records");
+    std::vector<int8_t> kc(static_cast<size_t>(n) * kCodeBytes), vc(kc.size());
+    std::vector<float> ks(static_cast<size_t>(n) * 4), vs(ks.size());
+    int rc = swiftkv_kv_cache_read(ctx, kv, seq, layer, head, tok0, n, kc.data(), vc.data(), ks.data(), vs.data());
+    if (rc) return rc;
+    uint8_t* out = static_cast<uint8_t*>(records);
+    for (int32_t t = 0; t < n; ++t) {
+        uint8_t* rec = out + static_cast<size_t>(t) * SWIFTKV_RECORD_BYTES;
+        std::memset(rec, 0, SWIFTKV_RECORD_BYTES);
+        for (int g = 0; g < kGroupsPerHead; ++g) {
+            uint8_t sk = 0, sv = 0;
+            if (!scale_to_shift(ks[static_cast<size_t>(t) * 4 + g], &sk) ||
+                !scale_to_shift(vs[static_cast<size_t>(t) * 4 + g], &sv))
+                return fail(SWIFTKV_ESTATE, "token %d group %d holds a scale that is not 2^(s-17), s in [0, 31]",
+                            tok0 + t, g);
+            put_bits(rec, 5 * g, 5, sk);
+            put_bits(rec, 20 + 5 * g, 5, sv);
+        }
+        std::memcpy(rec + 64, kc.data() + static_cast<size_t>(t) * kCodeBytes, kCodeBytes);
+        std::memcpy(rec + 192, vc.data() + static_cast<size_t>(t) * kCodeBytes, kCodeBytes);
+    }
+    return ok();
+}
+
+int swiftkv_kv_cache_import_records(swiftkv_context* ctx, swiftkv_kv_cache* kv, int32_t seq, int32_t layer,
+                                    int32_t head, int32_t tok0, int32_t n, const void* records) {
+    int rc = check_cache_range(ctx, kv, seq, layer, head, tok0, n);
+    if (rc) return rc;
+    if (!records && n > 0) return fail(SWIFTKV_EINVAL, "null records");
+    if ((rc = set_device(ctx))) return rc;
+    if (n == 0) return ok();
+    const uint8_t* in = static_cast<const uint8_t*>(records);
+    std::vector<int8_t> kc(static_cast<size_t>(n) * kCodeBytes), vc(kc.size());
+    std::vector<float> sc(static_cast<size_t>(n) * 8);
+    for (int32_t t = 0; t < n; ++t) {
+        const uint8_t* rec = in + static_cast<size_t>(t) * SWIFTKV_RECORD_BYTES;
+        for (int g = 0; g < kGroupsPerHead; ++g) {
+            sc[static_cast<size_t>(t) * 8 + 2 * g] = shift_to_scale(get_bits(rec, 5 * g, 5));
+            sc[static_cast<size_t>(t) * 8 + 2 * g + 1] = shift_to_scale(get_bits(rec, 20 + 5 * g, 5));
+        }
+        std::memcpy(kc.data() + static_cast<size_t>(t) * kCodeBytes, rec + 64, kCodeBytes);
+        std::memcpy(vc.data() + static_cast<size_t>(t) * kCodeBytes, rec + 192, kCodeBytes);
+    }
+    int8_t* page = page_ptr(CacheView{kv->base, kv->page_bytes, kv->seq_cap, kv->layers}, seq, layer, head);
+    const size_t cap = static_cast<size_t>(kv->seq_cap);
+    SKV_HIP(hipStreamSynchronize(ctx->stream));
+    SKV_HIP(hipMemcpy(page + static_cast<size_t>(tok0) * kCodeBytes, kc.data(), kc.size(), hipMemcpyHostToDevice));
+    SKV_HIP(hipMemcpy(page + (cap + tok0) * kCodeBytes, vc.data(), vc.size(), hipMemcpyHostToDevice));
+    SKV_HIP(hipMemcpy(page + cap * 2 * kCodeBytes + static_cast<size_t>(tok0) * kScaleBytes, sc.data(),
+                      sc.size() * sizeof(float), hipMemcpyHostToDevice));
+    return ok();
+}
+
+// ---------------------------------------------------------------- the step
+
+int swiftkv_attention_f32(swiftkv_context* ctx, const float* q, const float* k, const float* v,
+                          swiftkv_kv_cache* kv_cache, const swiftkv_rope_lut* rope_lut, uint8_t* activation_q,
+                          uint8_t* activation_scale, int32_t layer_index, const int32_t* positions,
+                          int32_t batch, float* out) {
+    return run_step(ctx, q, k, v, false, kv_cache, rope_lut, activation_q, activation_scale, layer_index,
+                    positions, batch, out);
+}
+
+int swiftkv_attention_q17(swiftkv_context* ctx, const int32_t* q, const int32_t* k, const int32_t* v,
+                          swiftkv_kv_cache* kv_cache, const swiftkv_rope_lut* rope_lut, uint8_t* activation_q,
+                          uint8_t* activation_scale, int32_t layer_index, const int32_t* positions,
+                          int32_t batch, float* out) {
+    return run_step(ctx, q, k, v, true, kv_cache, rope_lut, activation_q, activation_scale, layer_index,
+                    positions, batch, out);
+}
+
+int swiftkv_append_tokens(swiftkv_context* ctx, const void* k, const void* v, int32_t q17,
+                          swiftkv_kv_cache* kv_cache, const swiftkv_rope_lut* rope_lut, int32_t layer_index,
+                          int32_t seq, int32_t pos0, int32_t n) {
+    if (!ctx) return fail(SWIFTKV_EINVAL, "null context");
+    if (!k || !v) return fail(SWIFTKV_EINVAL, "null k/v pointer");
+    if (!rope_lut || rope_lut->ctx != ctx) return fail(SWIFTKV_EINVAL, "rope_lut is null or belongs to another context");
+    int rc = check_cache_range(ctx, kv_cache, seq, layer_index, 0, pos0, n);
+    if (rc) return rc;
+    if (static_cast<int64_t>(pos0) + n > rope_lut->positions)
+        return fail(SWIFTKV_ERANGE, "positions [%d, %d) exceed the RoPE table (%d)", pos0, pos0 + n,
+                    rope_lut->positions);
+    if (n == 0) return ok();
+    if ((rc = set_device(ctx))) return rc;
+    BulkArgs a;
+    a.k = k;
+    a.v = v;
+    a.kv = CacheView{kv_cache->base, kv_cache->page_bytes, kv_cache->seq_cap, kv_cache->layers};
+    a.lut = rope_lut->table;
+    a.lut_positions = rope_lut->positions;
+    a.layer = layer_index;
+    a.slot = seq;
+    a.pos0 = pos0;
+    a.n = n;
+    ProfilePair* p = profile_begin(ctx, SWIFTKV_KERNEL_APPEND);
+    SKV_HIP(launch_append_bulk(a, q17 != 0, ctx->stream));
+    profile_end(ctx, p);
+    return ok();
+}
+
+// ---------------------------------------------------------------- synthetic data
+
+int swiftkv_fill_synthetic_f32(swiftkv_context* ctx, float* out, size_t n, uint64_t seed, uint64_t stream,
+                               int32_t distribution, int32_t outliers) {
+    if (!ctx || (n && !out)) return fail(SWIFTKV_EINVAL, "null argument");
+    if (distribution != SWIFTKV_DIST_NORMAL && distribution != SWIFTKV_DIST_STUDENT_T3)
+        return fail(SWIFTKV_EINVAL, "unknown distribution %d", distribution);
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    SKV_HIP(launch_fill_f32(out, n, seed, stream, distribution, outliers != 0, ctx->stream));
+    return ok();
+}
+
+int swiftkv_kv_cache_fill_synthetic(swiftkv_context* ctx, swiftkv_kv_cache* kv, const swiftkv_rope_lut* rope_lut,
+                                    int32_t layer0, int32_t nlayers, int32_t seq0, int32_t nseq, int32_t ntok,
+                                    uint64_t seed, int32_t distribution, int32_t k_outliers) {
+    if (!ctx) return fail(SWIFTKV_EINVAL, "null context");
+    if (!kv || kv->ctx != ctx) return fail(SWIFTKV_EINVAL, "kv_cache is null or belongs to another context");
+    if (!rope_lut || rope_lut->ctx != ctx) return fail(SWIFTKV_EINVAL, "rope_lut is null or belongs to another context");
+    if (distribution != SWIFTKV_DIST_NORMAL && distribution != SWIFTKV_DIST_STUDENT_T3)
+        return fail(SWIFTKV_EINVAL, "unknown distribution %d", distribution);
+    if (layer0 < 0 || nlayers < 1 || static_cast<int64_t>(layer0) + nlayers > kv->layers)
+        return fail(SWIFTKV_ERANGE, "layers [%d, %d) outside [0, %d)", layer0, layer0 + nlayers, kv->layers);
+    if (seq0 < 0 || nseq < 1 || static_cast<int64_t>(seq0) + nseq > kv->max_batch)
+        return fail(SWIFTKV_ERANGE, "sequences [%d, %d) outside [0, %d)", seq0, seq0 + nseq, kv->max_batch);
+    if (ntok < 0 || ntok > kv->seq_cap || ntok > rope_lut->positions)
+        return fail(SWIFTKV_ERANGE, "ntok %d exceeds the cache (%d) or the RoPE table (%d)", ntok, kv->seq_cap,
+                    rope_lut->positions);
+    if (ntok == 0) return ok();
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    const CacheView view{kv->base, kv->page_bytes, kv->seq_cap, kv->layers};
+    // grid.z = sequences x layers per launch, kept below the 65535 limit
+    const int32_t per_launch = std::max<int32_t>(1, 65535 / nlayers);
+    for (int32_t s0 = 0; s0 < nseq; s0 += per_launch) {
+        const int32_t ns = std::min(per_launch, nseq - s0);
+        SKV_HIP(launch_fill_cache(view, rope_lut->table, seed, layer0, nlayers, seq0 + s0, ns, ntok, distribution,
+                                  k_outliers != 0, ctx->stream));
+    }
+    return ok();
+}
+
+// ---------------------------------------------------------------- memory
+
+int swiftkv_device_alloc(swiftkv_context* ctx, size_t bytes, void** out) {
+    if (!ctx || !out) return fail(SWIFTKV_EINVAL, "null argument");
+    *out = nullptr;
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    if (hipMalloc(out, bytes ? bytes : 1) != hipSuccess) return fail(SWIFTKV_ENOMEM, "hipMalloc of %zu bytes failed", bytes);
+    return ok();
+}
+
+int swiftkv_device_free(swiftkv_context* ctx, void* ptr) {
+    if (!ctx) return fail(SWIFTKV_EINVAL, "null context");
+    if (!ptr) return ok();
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    SKV_HIP(hipStreamSynchronize(ctx->stream));
+    SKV_HIP(hipFree(ptr));
+    return ok();
+}
+
+int swiftkv_memcpy_h2d(swiftkv_context* ctx, void* dst, const void* src, size_t bytes) {
+    if (!ctx || (bytes && (!dst || !src))) return fail(SWIFTKV_EINVAL, "null argument");
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    SKV_HIP(hipStreamSynchronize(ctx->stream));
+    if (bytes) SKV_HIP(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+    return ok();
+}
+
+int swiftkv_memcpy_d2h(swiftkv_context* ctx, void* dst, const void* src, size_t bytes) {
+    if (!ctx || (bytes && (!dst || !src))) return fail(SWIFTKV_EINVAL, "null argument");
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    SKV_HIP(hipStreamSynchronize(ctx->stream));
+    if (bytes) SKV_HIP(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+    return ok();
+}
+
+int swiftkv_memset_d(swiftkv_context* ctx, void* dst, int value, size_t bytes) {
+    if (!ctx || (bytes && !dst)) return fail(SWIFTKV_EINVAL, "null argument");
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    if (bytes) SKV_HIP(hipMemsetAsync(dst, value, bytes, ctx->stream));
+    return ok();
+}
+
+int swiftkv_convert_f32_q17(swiftkv_context* ctx, const float* in, int32_t* out, size_t n) {
+    if (!ctx || (n && (!in || !out))) return fail(SWIFTKV_EINVAL, "null argument");
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    SKV_HIP(launch_convert(in, out, n, ctx->stream));
+    return ok();
+}
+
+// ---------------------------------------------------------------- timing
+
+int swiftkv_timer_record(swiftkv_context* ctx, int32_t slot) {
+    if (!ctx) return fail(SWIFTKV_EINVAL, "null context");
+    if (slot < 0 || slot >= kTimerSlots) return fail(SWIFTKV_ERANGE, "timer slot %d outside [0, %d)", slot, kTimerSlots);
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    SKV_HIP(hipEventRecord(ctx->timers[slot], ctx->stream));
+    return ok();
+}
+
+int swiftkv_timer_elapsed(swiftkv_context* ctx, int32_t slot_begin, int32_t slot_end, float* ms) {
+    if (!ctx || !ms) return fail(SWIFTKV_EINVAL, "null argument");
+    if (slot_begin < 0 || slot_begin >= kTimerSlots || slot_end < 0 || slot_end >= kTimerSlots)
+        return fail(SWIFTKV_ERANGE, "timer slot outside [0, %d)", kTimerSlots);
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    SKV_HIP(hipEventSynchronize(ctx->timers[slot_end]));
+    SKV_HIP(hipEventElapsedTime(ms, ctx->timers[slot_begin], ctx->timers[slot_end]));
+    return ok();
+}
+
+int swiftkv_profile_enable(swiftkv_context* ctx, int32_t on) {
+    if (!ctx) return fail(SWIFTKV_EINVAL, "null context");
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    if (on && ctx->profile_pool.empty()) {
+        ctx->profile_pool.resize(kProfilePairs);
+        for (auto& p : ctx->profile_pool) {
+            SKV_HIP(hipEventCreate(&p.begin));
+            SKV_HIP(hipEventCreate(&p.end));
+        }
+    }
+    ctx->profiling = on != 0;
+    ctx->profile_used = 0;
+    return ok();
+}
+
+int swiftkv_profile_collect(swiftkv_context* ctx, int64_t counts[SWIFTKV_KERNEL_KINDS],
+                            double ms[SWIFTKV_KERNEL_KINDS]) {
+    if (!ctx || !counts || !ms) return fail(SWIFTKV_EINVAL, "null argument");
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    for (int i = 0; i < SWIFTKV_KERNEL_KINDS; ++i) {
+        counts[i] = 0;
+        ms[i] = 0.0;
+    }
+    SKV_HIP(hipStreamSynchronize(ctx->stream));
+    for (size_t i = 0; i < ctx->profile_used; ++i) {
+        const ProfilePair& p = ctx->profile_pool[i];
+        float t = 0.0f;
+        SKV_HIP(hipEventElapsedTime(&t, p.begin, p.end));
+        counts[p.kind] += 1;
+        ms[p.kind] += t;
+    }
+    ctx->profile_used = 0;
+    return ok();
+}
+
+}  // extern "C"

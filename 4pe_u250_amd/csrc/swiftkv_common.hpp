@@ -1,0 +1,96 @@
+// swiftkv_common.hpp -- geometry, cache layout and kernel argument blocks
+// shared by the host C-ABI (swiftkv_capi.cpp) and the HIP kernels
+// (swiftkv_kernels.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace swiftkv {
+
+// Geometry fixed by the reference (kernel_HLS/swiftkv_attention.hpp:5-13).
+constexpr int kHeads = 32;
+constexpr int kHeadDim = 128;
+constexpr int kModelDim = kHeads * kHeadDim;
+constexpr int kGroup = 32;                       // G32 quantization group
+constexpr int kGroupsPerHead = kHeadDim / kGroup;
+constexpr int kRopePairs = kHeadDim / 2;         // adjacent pairs (2j, 2j+1)
+
+// Page of one (sequence, layer, head): K codes [S][128] int8, V codes
+// [S][128] int8, scales [S][8] float interleaved (K_g, V_g) per group g.
+constexpr int kCodeBytes = kHeadDim;             // 128 B per token per plane
+constexpr int kScaleBytes = 8 * 4;               // 32 B per token
+constexpr int kTokenBytes = 2 * kCodeBytes + kScaleBytes;  // 288 B
+constexpr int kSeqAlign = 64;                    // capacity granularity (tokens)
+
+// Split-context work: a workgroup of kAttendWaves wavefronts scans a range of
+// split_tokens tokens; each wave takes 64-token blocks round-robin.
+constexpr int kAttendWaves = 4;
+constexpr int kBlockTokens = 64;
+constexpr int kSplitQuantum = kAttendWaves * kBlockTokens;   // 256
+constexpr int kPartialStride = 4 + kHeadDim;     // (m, l, pad, pad, acc[128]) floats
+
+// Sequences per launch: positions travel by value in the kernel arguments.
+constexpr int kMaxBatchPerLaunch = 256;
+
+static_assert(kTokenBytes == 288, "algorithmic bytes per token-head");
+static_assert(kGroupsPerHead == 4, "four G32 groups per head");
+
+struct CacheView {
+    int8_t* base;         // arena: pages ordered [slot][layer][head]
+    int64_t page_bytes;   // seq_cap * 288
+    int32_t seq_cap;      // tokens per page (multiple of 64)
+    int32_t layers;
+};
+
+__host__ __device__ inline int8_t* page_ptr(const CacheView& v, int slot, int layer, int head) {
+    return v.base + ((static_cast<int64_t>(slot) * v.layers + layer) * kHeads + head) * v.page_bytes;
+}
+
+// One decode step over a chunk of <= kMaxBatchPerLaunch sequences.
+struct StepArgs {
+    const void* q;            // [batch][4096] FP32 or Q15.17
+    const void* k;
+    const void* v;
+    float* qhat;              // [batch][4096] rotated query, q_raw * 2^-17
+    CacheView kv;
+    const int2* lut;          // [lut_positions][64] (cos, sin) Q1.17
+    int32_t lut_positions;
+    int32_t layer;
+    int32_t batch;            // sequences in this launch
+    int32_t slot0;            // cache slot of sequence 0 of this launch
+    int32_t split_tokens;     // multiple of kSplitQuantum
+    int32_t max_splits;       // partial slots per (sequence, head)
+    float* partials;          // [batch][32][max_splits][kPartialStride]
+    float* out;               // [batch][4096]
+    uint8_t* act_q;           // [batch][128][56] or null
+    uint8_t* act_scale;       // [batch][128] or null
+    int32_t positions[kMaxBatchPerLaunch];
+};
+
+// Bulk append of n tokens of one sequence (prefill).
+struct BulkArgs {
+    const void* k;            // [n][4096]
+    const void* v;
+    CacheView kv;
+    const int2* lut;
+    int32_t lut_positions;
+    int32_t layer;
+    int32_t slot;
+    int32_t pos0;
+    int32_t n;
+};
+
+// Launchers (swiftkv_kernels.hip).
+hipError_t launch_append_step(const StepArgs& a, bool q17, hipStream_t s);
+hipError_t launch_attend(const StepArgs& a, int grid_splits, hipStream_t s);
+hipError_t launch_combine(const StepArgs& a, hipStream_t s);
+hipError_t launch_append_bulk(const BulkArgs& a, bool q17, hipStream_t s);
+hipError_t launch_convert(const float* in, int32_t* out, size_t n, hipStream_t s);
+// Synthetic inputs (swiftkv_synth.hip).
+hipError_t launch_fill_f32(float* out, size_t n, uint64_t seed, uint64_t stream, int dist, int outliers,
+                           hipStream_t s);
+hipError_t launch_fill_cache(const CacheView& kv, const int2* lut, uint64_t seed, int layer0, int nlayers,
+                             int slot0, int nslots, int ntok, int dist, int k_outliers, hipStream_t s);
+
+}  // namespace swiftkv

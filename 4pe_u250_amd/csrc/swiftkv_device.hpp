@@ -1,0 +1,146 @@
+// swiftkv_device.hpp -- device-side arithmetic shared by the kernels:
+// FP32 -> Q15.17, integer RoPE, G32 quantization, the append of one row, and
+// the DPP cross-lane helpers.  Included by swiftkv_kernels.hip and
+// swiftkv_synth.hip only.
+#pragma once
+
+#include "swiftkv_common.hpp"
+
+namespace swiftkv {
+namespace dev {
+
+// ---------------------------------------------------------------- numerics
+
+// FP32 -> Q15.17 with round-half-even and saturation, on the bit pattern
+// (int4_linear_controller.cpp:38-83): |x| < 2^-18 -> 0, |x| >= 2^14 (and
+// inf/nan) -> saturate by sign.
+__device__ __forceinline__ int32_t f32_to_q17(float x) {
+    const uint32_t b = __float_as_uint(x);
+    const uint32_t e = (b >> 23) & 0xffu;
+    const bool neg = (b >> 31) != 0u;
+    if (e < 109u) return 0;
+    if (e >= 141u) return neg ? INT32_MIN : INT32_MAX;
+    const uint32_t sig = (1u << 23) | (b & 0x7fffffu);
+    uint32_t mag;
+    if (e >= 133u) {
+        mag = sig << (e - 133u);                 // < 2^31 for e <= 140
+    } else {
+        const uint32_t sh = 133u - e;            // 1..24
+        const uint32_t half = 1u << (sh - 1u);
+        const uint32_t rem = sig & ((half << 1) - 1u);
+        mag = sig >> sh;
+        mag += (rem > half || (rem == half && (mag & 1u))) ? 1u : 0u;
+    }
+    return neg ? -static_cast<int32_t>(mag) : static_cast<int32_t>(mag);
+}
+
+__device__ __forceinline__ int32_t sat32(int64_t x) {
+    return x > INT32_MAX ? INT32_MAX : (x < INT32_MIN ? INT32_MIN : static_cast<int32_t>(x));
+}
+
+// Adjacent-pair rotation with a Q1.17 (cos, sin): floor shift of the 52-bit
+// sum, saturated to int32 (swiftkv_attention.cpp:20-51).
+__device__ __forceinline__ void rope_pair(int32_t a, int32_t b, int2 cs, int32_t& x0, int32_t& x1) {
+    const int64_t c = cs.x, s = cs.y;
+    x0 = sat32((static_cast<int64_t>(a) * c - static_cast<int64_t>(b) * s) >> 17);
+    x1 = sat32((static_cast<int64_t>(a) * s + static_cast<int64_t>(b) * c) >> 17);
+}
+
+__device__ __forceinline__ uint32_t magnitude(int32_t r) {
+    return r < 0 ? 0u - static_cast<uint32_t>(r) : static_cast<uint32_t>(r);
+}
+
+// G32 shift: msb(max|r|) - 6, floored at 0 (swiftkv_attention.cpp:374-399).
+__device__ __forceinline__ uint32_t g32_shift(uint32_t m) {
+    if (m == 0u) return 0u;
+    const uint32_t msb = 31u - static_cast<uint32_t>(__clz(m));
+    return msb > 6u ? msb - 6u : 0u;
+}
+
+// Code = sign * min(127, (|r| + 2^(s-1)) >> s) (swiftkv_attention.cpp:401-418).
+__device__ __forceinline__ uint32_t g32_code_byte(int32_t r, uint32_t s) {
+    const uint32_t rnd = s ? (1u << (s - 1u)) : 0u;
+    uint32_t q = (magnitude(r) + rnd) >> s;      // |r| <= 2^31, rnd <= 2^24: no wrap
+    q = q > 127u ? 127u : q;
+    const int32_t c = r < 0 ? -static_cast<int32_t>(q) : static_cast<int32_t>(q);
+    return static_cast<uint32_t>(c) & 0xffu;
+}
+
+// FP32 bit pattern of 2^(s-17) (s <= 25: always a normal float).
+__device__ __forceinline__ float shift_scale(uint32_t s) { return __uint_as_float((s + 110u) << 23); }
+
+// ---------------------------------------------------------------- cross-lane
+// DPP controls (GFX9 encoding).
+constexpr int kDppQuadXor1 = 0xB1;     // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;     // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;  // lane i <-> 7-i within 8 lanes
+constexpr int kDppRowRor8 = 0x128;     // rotate by 8 within 16 lanes
+
+template <int Ctrl>
+__device__ __forceinline__ float dpp_f(float x) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), Ctrl, 0xF, 0xF, true));
+}
+
+// Sum over the 8 lanes of an aligned octet; every lane gets the same bits
+// (each step adds a value and its partner in commutative order).
+__device__ __forceinline__ float octet_sum(float x) {
+    x += dpp_f<kDppQuadXor1>(x);
+    x += dpp_f<kDppQuadXor2>(x);
+    x += dpp_f<kDppHalfMirror>(x);
+    return x;
+}
+
+// Max / sum across the 8 octets of a wave (lanes l, l^8, l^16, ...).
+__device__ __forceinline__ float across_octets_max(float x) {
+    x = fmaxf(x, dpp_f<kDppRowRor8>(x));
+    x = fmaxf(x, __shfl_xor(x, 16));
+    x = fmaxf(x, __shfl_xor(x, 32));
+    return x;
+}
+__device__ __forceinline__ float across_octets_sum(float x) {
+    x += dpp_f<kDppRowRor8>(x);
+    x += __shfl_xor(x, 16);
+    x += __shfl_xor(x, 32);
+    return x;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// ---------------------------------------------------------------- append
+
+template <bool Q17>
+__device__ __forceinline__ int2 load_pair(const void* base, size_t elem) {
+    if constexpr (Q17) {
+        return *reinterpret_cast<const int2*>(static_cast<const int32_t*>(base) + elem);
+    } else {
+        const float2 f = *reinterpret_cast<const float2*>(static_cast<const float*>(base) + elem);
+        return make_int2(f32_to_q17(f.x), f32_to_q17(f.y));
+    }
+}
+
+// Quantize this wave's (k rotated, v) row and write it at token `pos` of
+// `page`.  Lane l holds channels 2l, 2l+1; G32 group g = lanes 16g..16g+15.
+__device__ __forceinline__ void append_row(int8_t* page, int seq_cap, int pos, int lane,
+                                           int32_t k0, int32_t k1, int32_t v0, int32_t v1) {
+    uint32_t mk = max(magnitude(k0), magnitude(k1));
+    uint32_t mv = max(magnitude(v0), magnitude(v1));
+#pragma unroll
+    for (int d = 1; d < 16; d <<= 1) {
+        mk = max(mk, static_cast<uint32_t>(__shfl_xor(static_cast<int>(mk), d)));
+        mv = max(mv, static_cast<uint32_t>(__shfl_xor(static_cast<int>(mv), d)));
+    }
+    const uint32_t sk = g32_shift(mk), sv = g32_shift(mv);
+    const uint16_t kc = static_cast<uint16_t>(g32_code_byte(k0, sk) | (g32_code_byte(k1, sk) << 8));
+    const uint16_t vc = static_cast<uint16_t>(g32_code_byte(v0, sv) | (g32_code_byte(v1, sv) << 8));
+    const int64_t row = static_cast<int64_t>(pos) * kCodeBytes;
+    reinterpret_cast<uint16_t*>(page + row)[lane] = kc;
+    reinterpret_cast<uint16_t*>(page + static_cast<int64_t>(seq_cap) * kCodeBytes + row)[lane] = vc;
+    if ((lane & 15) == 0) {
+        float2* sc = reinterpret_cast<float2*>(page + static_cast<int64_t>(seq_cap) * (2 * kCodeBytes) +
+                                               static_cast<int64_t>(pos) * kScaleBytes);
+        sc[lane >> 4] = make_float2(shift_scale(sk), shift_scale(sv));
+    }
+}
+
+}  // namespace dev
+}  // namespace swiftkv

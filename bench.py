@@ -1,0 +1,229 @@
+#!/usr/bin/env python3
+"""Decode-attention benchmark on one MI355X.
+
+Workload (one "step"): the SwiftKV decode-attention stage of a full decode step
+of Llama-2-7B geometry -- 32 layers x 32 heads x head_dim 128, MHA -- for a
+batch of 64 independent sequences at position 4095 (context 4096).  Per layer
+one call of swiftkv_attention_f32: FP32 q/k/v -> Q15.17, RoPE, INT8/G32
+quantize + append of token 4095, attention over the 4096-token INT8 cache.
+Inputs (q/k/v for all 32 layers) and the 77 GB cache are resident in HBM
+before timing; the cache is filled on the device through the append rule from
+seeded N(0,1) rows.
+
+    python bench.py [--steps K] [--warmup W] [--batch 64] [--context 4096]
+
+Prints ONE JSON line.  value = algorithmic bytes of the step / step time
+(GB/s), where per (sequence, layer) at position p the step moves
+9216*p + 9216 + 65536 bytes (288 B per cached token-head + the appended row +
+FP32 q/k/v/out).  Also reported: us/layer, tokens/s, % of 8 TB/s, the batch-1
+figures, the split-attention kernel's roofline from per-launch hipEvents, and
+the reference emulator's attention stage timed on this host (cpu_baseline).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, REPO)
+
+HBM_PEAK_GBPS = 8000.0
+METRIC = "decode-attn µs/layer + achieved HBM GB/s (% of peak), ctx 4096, batch 1/64"
+TOKEN_HEAD_BYTES = 288
+
+
+def step_bytes(position: int) -> int:
+    """Algorithmic bytes of one (sequence, layer) step at `position`."""
+    return 32 * (position * TOKEN_HEAD_BYTES + TOKEN_HEAD_BYTES + 4 * 128 * 4)
+
+
+def attend_bytes(position: int) -> int:
+    """Algorithmic bytes of the split-attention kernel per (sequence, layer):
+    (position+1) cached token-heads + the FP32 rotated query per head."""
+    return 32 * ((position + 1) * TOKEN_HEAD_BYTES + 128 * 4)
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def run_gpu(skv, ctx, batch, context, layers, steps, warmup, seed, outliers=False):
+    pos = context - 1
+    lut = skv.RopeLut.generate(ctx, max(context, 4096))
+    kv = skv.KVCache(ctx, layers=layers, max_batch=batch, max_seq_len=context)
+    t0 = time.time()
+    kv.fill_synthetic(lut, ntok=pos, seed=seed, k_outliers=outliers)
+    ctx.synchronize()
+    log(f"[bench] batch {batch}: filled {kv.nbytes / 1e9:.1f} GB cache ({layers} layers x {batch} seq x "
+        f"{pos} tokens) in {time.time() - t0:.1f} s")
+    n_in = layers * batch * 4096
+    qkv = [ctx.alloc(n_in * 4) for _ in range(3)]
+    for i, buf in enumerate(qkv):
+        ctx.fill_synthetic(buf, n_in, seed + 1, 1000 + i, outliers=(outliers and i == 1))
+    out = ctx.alloc(batch * 4096 * 4)
+    aq = ctx.alloc(batch * 128 * 56)
+    asc = ctx.alloc(batch * 128)
+    positions = np.full(batch, pos, np.int32)
+    layer_stride = batch * 4096 * 4
+
+    def one_step():
+        for layer in range(layers):
+            off = layer * layer_stride
+            skv.swiftkv_attention(ctx, qkv[0].ptr + off, qkv[1].ptr + off, qkv[2].ptr + off, kv, lut, aq, asc,
+                                  layer, positions, out)
+
+    for _ in range(warmup):
+        one_step()
+    ctx.synchronize()
+    ctx.profile(True)
+    ctx.timer_record(0)
+    for _ in range(steps):
+        one_step()
+    ctx.timer_record(1)
+    ms = ctx.timer_elapsed_ms(0, 1)
+    counts, kms = ctx.profile_collect()
+    ctx.profile(False)
+    o = out.download(np.float32, (batch, 4096))
+    assert np.isfinite(o).all(), "non-finite attention output"
+    for b in qkv + [out, aq, asc]:
+        b.free()
+    kv.close()
+    lut.close()
+    total_bytes = steps * layers * batch * step_bytes(pos)
+    ms_step = ms / steps
+    res = {
+        "ms_per_step": ms_step,
+        "us_per_layer": 1000.0 * ms_step / layers,
+        "gbps": total_bytes / (ms / 1e3) / 1e9,
+        "tokens_per_s": batch * steps / (ms / 1e3),
+        "kernel_launches": dict(zip(["append", "attend", "combine"], counts)),
+        "kernel_avg_us": {k: (1000.0 * t / c if c else None)
+                          for k, t, c in zip(["append", "attend", "combine"], kms, counts)},
+    }
+    res["pct_of_peak"] = 100.0 * res["gbps"] / HBM_PEAK_GBPS
+    att_avg_s = kms[1] / counts[1] / 1e3
+    res["attend_achieved_gbps"] = batch * attend_bytes(pos) / att_avg_s / 1e9
+    return res
+
+
+def cpu_baseline(target_seconds: float, position: int, omp: bool):
+    """The reference emulator's attention stage (oracle/_ref, compiled from the
+    reference source) on this host: one sequence x 32 heads per call at
+    `position`, cache pre-filled through the oracle's append rule."""
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    sys.path.insert(0, os.path.join(REPO, "tests"))
+    import oracle as O
+    from helpers import f32_normal
+    if not O.Reference.available(omp):
+        return None
+    R = O.Reference(omp=omp)
+    cos, sin = O.rope_values(position + 1)
+    R.set_rope(cos, sin)
+    sc = O.SequenceCache(32, position + 1)
+    sc.fill_q17(O.f2q17(f32_normal(7, (position, 4096))), O.f2q17(f32_normal(8, (position, 4096))), 0, cos, sin)
+    rc = R.cache(position + 1)
+    rc.load_from(sc, position)
+    q, k, v = (O.f2q17(f32_normal(9 + i, (4096,))) for i in range(3))
+    qr, kr = R.apply_rope(q, position), R.apply_rope(k, position)
+    rc.attention(qr, kr, v, position)          # warm-up call
+    times = []
+    t_start = time.perf_counter()
+    while time.perf_counter() - t_start < target_seconds or len(times) < 3:
+        t0 = time.perf_counter()
+        rc.attention(qr, kr, v, position)
+        times.append(time.perf_counter() - t0)
+    per_call = float(np.median(times))
+    return {
+        "value": step_bytes(position) / per_call / 1e9,
+        "unit": "GB/s",
+        "us_per_layer_batch1": per_call * 1e6,
+        "us_per_layer_batch64": per_call * 64 * 1e6,
+        "cores": R.L.ref_omp_threads(),
+        "kind": "reference",
+        "sample": (f"{len(times)} calls of the reference emulator's swiftkv_attention_4pe (32 heads, one "
+                   f"sequence, one layer, position {position}), median; batch-64 figure = 64 x per-call"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--batch", type=int, default=64)
+    ap.add_argument("--context", type=int, default=4096)
+    ap.add_argument("--layers", type=int, default=32)
+    ap.add_argument("--split", type=int, default=0, help="tokens per split (0 = heuristic)")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-batch1", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (the path shards by "
+                                   "head/sequence across GPUs by design only)"}))
+        sys.exit(2)
+
+    import importlib
+    skv = importlib.import_module("4pe_u250_amd")
+    ctx = skv.Context(0)
+    ctx.set_split_tokens(args.split)
+    log(f"[bench] {skv.version()}")
+    main_res = run_gpu(skv, ctx, args.batch, args.context, args.layers, args.steps, args.warmup, seed=2026)
+    log(f"[bench] batch {args.batch}: {main_res['us_per_layer']:.1f} us/layer, {main_res['gbps']:.0f} GB/s")
+    b1 = None
+    if not args.no_batch1:
+        b1 = run_gpu(skv, ctx, 1, args.context, args.layers, max(args.steps, 20), args.warmup, seed=2027)
+        log(f"[bench] batch 1: {b1['us_per_layer']:.2f} us/layer, {b1['gbps']:.0f} GB/s")
+    ctx.close()
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(args.cpu_seconds, args.context - 1, omp=False)
+        if cpu:
+            log(f"[bench] cpu reference: {cpu['us_per_layer_batch1']:.0f} us per sequence-layer")
+            omp = cpu_baseline(max(2.0, args.cpu_seconds / 4), args.context - 1, omp=True)
+            if omp:
+                cpu["openmp"] = {"value": omp["value"], "cores": omp["cores"],
+                                 "us_per_layer_batch1": omp["us_per_layer_batch1"]}
+
+    att = main_res["kernel_avg_us"]["attend"]
+    line = {
+        "metric": METRIC,
+        "value": round(main_res["gbps"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(main_res["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic (seeded N(0,1) q/k/v and cache rows, cache built on device by the append rule)",
+        "config": {"workload": "decode-attention step: 32 layers x batch 64 x position 4095 (ctx 4096), "
+                               "32 heads x 128, MHA, INT8/G32 KV cache",
+                   "batch": args.batch, "context": args.context, "layers": args.layers, "heads": 32,
+                   "head_dim": 128, "kv_dtype": "int8+fp32 G32 scales"},
+        "us_per_layer": round(main_res["us_per_layer"], 2),
+        "tokens_per_s": round(main_res["tokens_per_s"], 1),
+        "pct_of_peak": round(main_res["pct_of_peak"], 2),
+        "kernel_avg_us": {k: (round(v, 2) if v else v) for k, v in main_res["kernel_avg_us"].items()},
+        "roofline": {"bound": "hbm", "achieved": round(main_res["attend_achieved_gbps"], 1),
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(main_res["attend_achieved_gbps"] / HBM_PEAK_GBPS, 4),
+                     "traffic": None, "kernel": "attend_kernel",
+                     "avg_launch_us": round(att, 2) if att else None},
+        "cpu_baseline": cpu,
+    }
+    if b1:
+        line["batch1"] = {"us_per_layer": round(b1["us_per_layer"], 3), "gbps": round(b1["gbps"], 1),
+                          "pct_of_peak": round(b1["pct_of_peak"], 2), "tokens_per_s": round(b1["tokens_per_s"], 1),
+                          "kernel_avg_us": {k: (round(v, 2) if v else v) for k, v in b1["kernel_avg_us"].items()}}
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

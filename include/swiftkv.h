@@ -1,0 +1,233 @@
+/*
+ * swiftkv.h -- C ABI of the MI355X SwiftKV decode-attention stage.
+ *
+ * Drop-in for the reference's local-PE attention entry
+ *   void int4_swiftkv_attention_pe{0..3}(q, k, v, kv_cache, rope_lut_ddr,
+ *        activation_q, activation_scale, layer_index, position)
+ * (kernel_HLS/swiftkv_attention.hpp:167-209, swiftkv_attention.cpp:2821-2883).
+ * One call performs, for every (sequence, head) of a batch:
+ *   1. FP32 -> Q15.17 conversion of q/k/v, exactly as the upstream linear
+ *      finalize does (int4_linear_controller.cpp:38-83) -- skipped by the
+ *      _q17 entry, which takes Q15.17 words as the reference does;
+ *   2. adjacent-pair integer RoPE of q and k from the position-indexed Q1.17
+ *      table (swiftkv_attention.cpp:20-95);
+ *   3. INT8/G32 quantization of the new K/V row and its append to the cache
+ *      at `position` (swiftkv_attention.cpp:348-582, 752-786) -- bit-exact;
+ *   4. attention of the rotated query over cached tokens [0, position]
+ *      (swiftkv_attention.cpp:934-1880), evaluated with the reference's FP32
+ *      softmax formula (llama2_decoder_sw_emulator.cpp:1164-1194) over the
+ *      dequantized INT8 cache;
+ *   5. optionally the A14/G32 + E8M0 output quantization for the O projection
+ *      (swiftkv_attention.cpp:1715-1771, 2656-2682).
+ *
+ * All 32 heads of a layer run on one GPU (the reference shards 8 heads per
+ * FPGA PE).  Conventions:
+ *   - every function returns 0 (SWIFTKV_OK) or a negative SWIFTKV_E* code;
+ *     no C++ exception crosses the boundary; swiftkv_last_error() describes
+ *     the most recent failure of the calling thread;
+ *   - tensors passed to the step functions are DEVICE pointers (allocate with
+ *     swiftkv_device_alloc or any HIP allocator); position/length arrays are
+ *     HOST pointers;
+ *   - work is issued asynchronously on the context's HIP stream; call
+ *     swiftkv_synchronize() before reading results on the host;
+ *   - calls on one context are not thread-safe; distinct contexts are.
+ */
+#ifndef SWIFTKV_H
+#define SWIFTKV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Geometry fixed by the reference (swiftkv_attention.hpp:5-13, config.json). */
+#define SWIFTKV_HEADS 32
+#define SWIFTKV_HEAD_DIM 128
+#define SWIFTKV_MODEL_DIM (SWIFTKV_HEADS * SWIFTKV_HEAD_DIM)
+#define SWIFTKV_GROUP 32
+#define SWIFTKV_GROUPS_PER_HEAD (SWIFTKV_HEAD_DIM / SWIFTKV_GROUP)
+/* Reference limits: position is ap_uint<12>, SWIFTKV_MAX_SEQ_LEN = 4096
+ * (hpp:26-30).  This build accepts longer caches (up to 32768 tokens) with the
+ * RoPE table extended by the same closed form. */
+#define SWIFTKV_REFERENCE_MAX_SEQ 4096
+#define SWIFTKV_MAX_SEQ 32768
+/* Byte sizes of the reference formats. */
+#define SWIFTKV_ROPE_LUT_BYTES_PER_POSITION 512 /* 4 LUT words x 2 x 64 B */
+#define SWIFTKV_RECORD_BYTES 320                /* [meta, K0, K1, V0, V1] x 64 B */
+#define SWIFTKV_A14_WORD_BYTES 56               /* ap_uint<448>: 32 x int14 */
+
+/* Status codes. */
+#define SWIFTKV_OK 0
+#define SWIFTKV_EINVAL (-1)  /* null pointer, bad size or geometry */
+#define SWIFTKV_ERANGE (-2)  /* position / layer / sequence out of range */
+#define SWIFTKV_EHIP (-3)    /* HIP runtime error (no device, launch failure) */
+#define SWIFTKV_ENOMEM (-4)  /* device or host allocation failed */
+#define SWIFTKV_ESTATE (-5)  /* object not ready (e.g. RoPE table not loaded) */
+
+typedef struct swiftkv_context swiftkv_context;
+typedef struct swiftkv_kv_cache swiftkv_kv_cache;
+typedef struct swiftkv_rope_lut swiftkv_rope_lut;
+
+/* Thread-local description of the last failure ("" after success). */
+const char* swiftkv_last_error(void);
+/* Library version string. */
+const char* swiftkv_version(void);
+
+/* --------------------------------------------------------------------------
+ * Context: device, HIP stream, split-context workspace.
+ * Replaces the per-PE compute-unit handle the XRT host launches
+ * (host/decode_host.cpp:1256-1294, 1378-1404).
+ * ------------------------------------------------------------------------ */
+int swiftkv_context_create(int device, swiftkv_context** out);
+int swiftkv_context_destroy(swiftkv_context* ctx);
+int swiftkv_synchronize(swiftkv_context* ctx);
+/* Tokens per split-context work item; 0 selects the built-in heuristic.
+ * Must be 0 or a multiple of 256 in [256, 32768]. */
+int swiftkv_set_split_tokens(swiftkv_context* ctx, int32_t split_tokens);
+
+/* --------------------------------------------------------------------------
+ * RoPE table (kernel_HLS/swiftkv_attention.hpp:55-81; rope_lut.bin format of
+ * scripts/generate_rope_lut.py:20-41, 104-150): per position, 64 (cos, sin)
+ * pairs as signed 19-bit Q1.17, packed 16 pairs per 608-bit LUT word, each
+ * LUT word padded into two 64-byte DDR words (512 bytes per position).
+ * ------------------------------------------------------------------------ */
+/* Load `positions` positions from the reference file image (host bytes,
+ * positions * 512 bytes, e.g. the 2 MiB rope_lut.bin). */
+int swiftkv_rope_lut_load(swiftkv_context* ctx, const void* image, size_t image_bytes,
+                          swiftkv_rope_lut** out);
+/* Closed form RNE(2^17 cos|sin(pos * theta^(-j/64))) for pos < positions
+ * (reproduces rope_lut.bin bit for bit at theta = 10000, 4096 positions). */
+int swiftkv_rope_lut_generate(swiftkv_context* ctx, int32_t positions, double theta,
+                              swiftkv_rope_lut** out);
+int swiftkv_rope_lut_destroy(swiftkv_rope_lut* lut);
+int32_t swiftkv_rope_lut_positions(const swiftkv_rope_lut* lut);
+/* Write positions [pos0, pos0+n) back in the reference file format (host). */
+int swiftkv_rope_lut_export(const swiftkv_rope_lut* lut, int32_t pos0, int32_t n, void* image);
+
+/* --------------------------------------------------------------------------
+ * KV cache: GPU-resident INT8 codes with per-(token, head) G32 FP32 scales
+ * 2^(shift-17).  Replaces the reference's per-PE DDR region
+ * [layer][local_head][token][meta,K0,K1,V0,V1] (hpp:98-110; sized and zeroed
+ * by host/decode_host.cpp:98-119, 1256-1259, 1291-1294).
+ * Layout (one page per sequence x layer x head, capacity S tokens):
+ *   K codes  [S][128] int8   | V codes [S][128] int8 |
+ *   scales   [S][8] float  = (K_g0, V_g0, K_g1, V_g1, K_g2, V_g2, K_g3, V_g3)
+ * The cache is zero-filled on creation.
+ * ------------------------------------------------------------------------ */
+int swiftkv_kv_cache_create(swiftkv_context* ctx, int32_t layers, int32_t max_batch,
+                            int32_t max_seq_len, swiftkv_kv_cache** out);
+int swiftkv_kv_cache_destroy(swiftkv_kv_cache* kv);
+int swiftkv_kv_cache_zero(swiftkv_context* ctx, swiftkv_kv_cache* kv);
+/* Bytes held on the device (codes + scales). */
+size_t swiftkv_kv_cache_bytes(const swiftkv_kv_cache* kv);
+/* Copy tokens [tok0, tok0+n) of (seq, layer, head) to host buffers:
+ * k_codes/v_codes [n][128] int8, k_scales/v_scales [n][4] float (any may be
+ * NULL).  Synchronizes the context stream. */
+int swiftkv_kv_cache_read(swiftkv_context* ctx, const swiftkv_kv_cache* kv, int32_t seq,
+                          int32_t layer, int32_t head, int32_t tok0, int32_t n,
+                          int8_t* k_codes, int8_t* v_codes, float* k_scales, float* v_scales);
+/* Reference record format [meta, K0, K1, V0, V1] (320 bytes per token-head,
+ * hpp:94-110, swiftkv_attention.cpp:534-581): export to / import from host
+ * memory, records [n][320] for tokens [tok0, tok0+n) of (seq, layer, head). */
+int swiftkv_kv_cache_export_records(swiftkv_context* ctx, const swiftkv_kv_cache* kv,
+                                    int32_t seq, int32_t layer, int32_t head, int32_t tok0,
+                                    int32_t n, void* records);
+int swiftkv_kv_cache_import_records(swiftkv_context* ctx, swiftkv_kv_cache* kv, int32_t seq,
+                                    int32_t layer, int32_t head, int32_t tok0, int32_t n,
+                                    const void* records);
+
+/* --------------------------------------------------------------------------
+ * The decode-attention step (the drop-in for int4_swiftkv_attention_peN).
+ *   q, k, v        device [batch][4096]: FP32 (…_f32) or Q15.17 int32 (…_q17)
+ *   kv_cache       persistent cache; sequence b of the batch uses cache slot b
+ *   rope_lut       table covering every position used
+ *   activation_q   optional device [batch][128][56] bytes: A14 words, group
+ *                  index = head*4 + g, lane 0 in bits [13:0] (may be NULL)
+ *   activation_scale optional device [batch][128] E8M0 codes (may be NULL;
+ *                  must be NULL iff activation_q is NULL)
+ *   layer_index    0 <= layer < kv_cache layers
+ *   positions      host [batch]: cached-token count of each sequence; the
+ *                  step writes token `positions[b]` and attends [0, positions[b]]
+ *   out            device [batch][4096] FP32 attention output (required)
+ * ------------------------------------------------------------------------ */
+int swiftkv_attention_f32(swiftkv_context* ctx, const float* q, const float* k, const float* v,
+                          swiftkv_kv_cache* kv_cache, const swiftkv_rope_lut* rope_lut,
+                          uint8_t* activation_q, uint8_t* activation_scale, int32_t layer_index,
+                          const int32_t* positions, int32_t batch, float* out);
+int swiftkv_attention_q17(swiftkv_context* ctx, const int32_t* q, const int32_t* k,
+                          const int32_t* v, swiftkv_kv_cache* kv_cache,
+                          const swiftkv_rope_lut* rope_lut, uint8_t* activation_q,
+                          uint8_t* activation_scale, int32_t layer_index,
+                          const int32_t* positions, int32_t batch, float* out);
+
+/* Bulk append (prompt prefill): apply the append rule -- conversion, RoPE of
+ * k at its own position, G32 quantization -- to n tokens [pos0, pos0+n) of
+ * one sequence without attending.  k, v: device [n][4096], FP32 when
+ * q17 == 0, Q15.17 int32 otherwise.  The reference has no prefill entry; it
+ * feeds prompt tokens through the decode step one at a time
+ * (host/decode_host.cpp:1340-1556). */
+int swiftkv_append_tokens(swiftkv_context* ctx, const void* k, const void* v, int32_t q17,
+                          swiftkv_kv_cache* kv_cache, const swiftkv_rope_lut* rope_lut,
+                          int32_t layer_index, int32_t seq, int32_t pos0, int32_t n);
+
+/* --------------------------------------------------------------------------
+ * Synthetic inputs for benchmarks and capacity tests (no reference
+ * counterpart; the reference's testbenches read weight files or fixed
+ * generators).  A synthetic stream (seed, stream) is an FP32 tensor whose
+ * element i comes from a counter-based generator (splitmix64 + Box-Muller):
+ * N(0,1), or unit-variance Student-t(3); with `outliers` set, elements whose
+ * channel i % 4096 is one of ~1% seed-selected channels are scaled by 20.
+ * ------------------------------------------------------------------------ */
+#define SWIFTKV_DIST_NORMAL 0
+#define SWIFTKV_DIST_STUDENT_T3 1
+/* Elements [0, n) of stream (seed, stream) into device memory. */
+int swiftkv_fill_synthetic_f32(swiftkv_context* ctx, float* out, size_t n, uint64_t seed, uint64_t stream,
+                               int32_t distribution, int32_t outliers);
+/* Tokens [0, ntok) of sequences [seq0, seq0+nseq) x layers [layer0,
+ * layer0+nlayers) through the append rule, K row t of (slot s, layer l) =
+ * elements [4096t, 4096t+4096) of stream 2*(64s + l) (with k_outliers),
+ * V row of stream 2*(64s + l) + 1. */
+int swiftkv_kv_cache_fill_synthetic(swiftkv_context* ctx, swiftkv_kv_cache* kv,
+                                    const swiftkv_rope_lut* rope_lut, int32_t layer0, int32_t nlayers,
+                                    int32_t seq0, int32_t nseq, int32_t ntok, uint64_t seed,
+                                    int32_t distribution, int32_t k_outliers);
+
+/* --------------------------------------------------------------------------
+ * Device-memory helpers for FFI callers without a GPU framework (ctypes).
+ * ------------------------------------------------------------------------ */
+int swiftkv_device_alloc(swiftkv_context* ctx, size_t bytes, void** out);
+int swiftkv_device_free(swiftkv_context* ctx, void* ptr);
+int swiftkv_memcpy_h2d(swiftkv_context* ctx, void* dst, const void* src, size_t bytes);
+int swiftkv_memcpy_d2h(swiftkv_context* ctx, void* dst, const void* src, size_t bytes);
+int swiftkv_memset_d(swiftkv_context* ctx, void* dst, int value, size_t bytes);
+
+/* Elementwise FP32 -> Q15.17 on the device (the conversion of step 1),
+ * n elements, device pointers.  Exposed for exhaustive conversion tests. */
+int swiftkv_convert_f32_q17(swiftkv_context* ctx, const float* in, int32_t* out, size_t n);
+
+/* --------------------------------------------------------------------------
+ * Timing (hipEvents on the context stream).  Stands in for the host's
+ * per-stage timers (host/decode_host.cpp:1539-1553).
+ * ------------------------------------------------------------------------ */
+/* Record timestamp slot `slot` (0..63) on the context stream. */
+int swiftkv_timer_record(swiftkv_context* ctx, int32_t slot);
+/* Milliseconds between two recorded slots (waits for the later one). */
+int swiftkv_timer_elapsed(swiftkv_context* ctx, int32_t slot_begin, int32_t slot_end, float* ms);
+/* Per-kernel timing: when enabled, every launch of each kernel is bracketed
+ * by events; swiftkv_profile_collect() synchronizes and returns, per kernel
+ * kind (0 append, 1 split attention, 2 combine), the launch count and the
+ * summed duration in ms, then clears the record. */
+#define SWIFTKV_KERNEL_APPEND 0
+#define SWIFTKV_KERNEL_ATTEND 1
+#define SWIFTKV_KERNEL_COMBINE 2
+#define SWIFTKV_KERNEL_KINDS 3
+int swiftkv_profile_enable(swiftkv_context* ctx, int32_t on);
+int swiftkv_profile_collect(swiftkv_context* ctx, int64_t counts[SWIFTKV_KERNEL_KINDS],
+                            double ms[SWIFTKV_KERNEL_KINDS]);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SWIFTKV_H */

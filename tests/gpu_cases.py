@@ -1,0 +1,88 @@
+"""Scenario builder shared by the GPU tests: the same seeded inputs go through
+the HIP path (C ABI) and the oracle."""
+import numpy as np
+
+import oracle as O
+from helpers import f32_normal, splitmix64
+
+H = 32
+
+
+def student_t3(seed: int, shape) -> np.ndarray:
+    """Student-t(nu=3) scaled to unit variance: N / sqrt(chi2_3 / 3) / sqrt(3)."""
+    n = f32_normal(seed, shape).astype(np.float64)
+    c = sum(f32_normal(seed + 7919 * (i + 1), shape).astype(np.float64) ** 2 for i in range(3))
+    return (n / np.sqrt(c / 3.0) / np.sqrt(3.0)).astype(np.float32)
+
+
+def outlier_channels(seed: int, count: int = 41) -> np.ndarray:
+    z = splitmix64(seed, 4 * count)
+    return np.unique((z % np.uint64(4096)).astype(np.int64))[:count]
+
+
+def history(seed: int, n: int, dist: str = "normal", outliers=None):
+    if dist == "t3":
+        k, v = student_t3(seed, (n, 4096)), student_t3(seed + 1, (n, 4096))
+    else:
+        k, v = f32_normal(seed, (n, 4096)), f32_normal(seed + 1, (n, 4096))
+    if outliers is not None:
+        k[:, outliers] *= np.float32(20.0)
+    return k, v
+
+
+def prefill(skv, ctx, kv, lut, layer, seq, k_hist, v_hist, chunk=1024):
+    """Bulk-append a FP32 history [n][4096] at positions [0, n)."""
+    n = k_hist.shape[0]
+    for t0 in range(0, n, chunk):
+        t1 = min(n, t0 + chunk)
+        dk = ctx.to_device(k_hist[t0:t1])
+        dv = ctx.to_device(v_hist[t0:t1])
+        skv.swiftkv_append_tokens(ctx, dk, dv, kv, lut, layer, seq, t0, t1 - t0)
+        ctx.synchronize()
+        dk.free()
+        dv.free()
+
+
+def run_step(skv, ctx, kv, lut, layer, positions, q, k, v, q17=False, a14=True):
+    """One step through the C ABI; returns (out [B,4096], act_q [B,128,56], act_scale [B,128])."""
+    B = len(positions)
+    dq, dk, dv = ctx.to_device(q), ctx.to_device(k), ctx.to_device(v)
+    out = ctx.alloc(B * 4096 * 4)
+    aq = ctx.alloc(B * 128 * 56) if a14 else None
+    asc = ctx.alloc(B * 128) if a14 else None
+    skv.swiftkv_attention(ctx, dq, dk, dv, kv, lut, aq, asc, layer, positions, out, q17=q17)
+    ctx.synchronize()
+    res = (out.download(np.float32, (B, 4096)),
+           aq.download(np.uint8, (B, 128, 56)) if a14 else None,
+           asc.download(np.uint8, (B, 128)) if a14 else None)
+    for b in (dq, dk, dv, out, aq, asc):
+        if b is not None:
+            b.free()
+    return res
+
+
+def oracle_sequence(cos, sin, k_hist, v_hist, cap):
+    sc = O.SequenceCache(H, cap)
+    if k_hist.shape[0]:
+        sc.fill_q17(O.f2q17(k_hist), O.f2q17(v_hist), 0, cos, sin)
+    return sc
+
+
+def assert_rows_equal(kv, sc, seq, layer, tok0, n, heads=range(H)):
+    for h in heads:
+        kc, vc, ks, vs = kv.read(seq, layer, h, tok0, n)
+        assert (kc == sc.kc[h, tok0:tok0 + n]).all(), f"seq {seq} head {h}: K codes differ"
+        assert (vc == sc.vc[h, tok0:tok0 + n]).all(), f"seq {seq} head {h}: V codes differ"
+        assert (ks.view(np.uint32) == O.shift_scale_bits(sc.ks[h, tok0:tok0 + n])).all(), f"seq {seq} head {h}: K scales"
+        assert (vs.view(np.uint32) == O.shift_scale_bits(sc.vs[h, tok0:tok0 + n])).all(), f"seq {seq} head {h}: V scales"
+
+
+RTOL, ATOL = 1e-4, 2e-5   # north-star tolerance vs the FP32 formula
+
+
+def assert_close(got, ref, what=""):
+    err = np.abs(got.astype(np.float64) - ref)
+    bad = err > ATOL + RTOL * np.abs(ref)
+    assert not bad.any(), (f"{what}: {int(bad.sum())} values outside atol {ATOL} + rtol {RTOL}; "
+                           f"max abs err {err.max():.3g}")
+    return float(err.max())

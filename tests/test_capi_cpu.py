@@ -1,0 +1,84 @@
+"""CPU-only checks of the C ABI: the library loads, exports every symbol that
+include/swiftkv.h declares, and rejects bad arguments with the documented
+status codes before touching a device.  No compute calls (no GPU here)."""
+import ctypes as C
+import subprocess
+
+import numpy as np
+import pytest
+
+
+def test_library_exports_every_header_symbol(skv):
+    L = skv.lib()
+    names = skv.header_symbols()
+    assert len(names) >= 30
+    for n in names:
+        assert hasattr(L, n), n
+    assert set(names) == set(skv._SIGNATURES), "ctypes signature table out of sync with the header"
+
+
+def test_dynamic_symbol_table(skv):
+    out = subprocess.run(["nm", "-D", "--defined-only", skv.LIB_PATH], capture_output=True, text=True).stdout
+    exported = {ln.split()[-1] for ln in out.splitlines() if " T " in ln}
+    for n in skv.header_symbols():
+        assert n in exported, n
+
+
+def test_built_for_gfx950_only(skv, tmp_path):
+    """The offload bundle in .hip_fatbin holds gfx950 code objects only."""
+    import re
+    blob = tmp_path / "fatbin.bin"
+    subprocess.run(["objcopy", "-O", "binary", "--only-section=.hip_fatbin", skv.LIB_PATH, str(blob)], check=True)
+    targets = set(re.findall(rb"hipv4-amdgcn-amd-amdhsa--(gfx[0-9a-z]+)", blob.read_bytes()))
+    assert targets == {b"gfx950"}
+
+
+def test_version_and_last_error(skv):
+    assert "gfx950" in skv.version()
+    assert isinstance(skv.lib().swiftkv_last_error(), bytes)
+
+
+def test_null_and_range_checks_without_device(skv):
+    L = skv.lib()
+    assert L.swiftkv_context_create(0, None) == skv.EINVAL
+    assert L.swiftkv_synchronize(None) == skv.EINVAL
+    assert L.swiftkv_set_split_tokens(None, 256) == skv.EINVAL
+    pos = np.array([0], np.int32)
+    assert L.swiftkv_attention_f32(None, None, None, None, None, None, None, None, 0,
+                                   pos.ctypes.data_as(C.c_void_p), 1, None) == skv.EINVAL
+    assert b"null" in L.swiftkv_last_error()
+    assert L.swiftkv_rope_lut_export(None, 0, 1, None) == skv.EINVAL
+    assert L.swiftkv_kv_cache_bytes(None) == 0
+    assert L.swiftkv_rope_lut_positions(None) == 0
+    h = C.c_void_p()
+    assert L.swiftkv_rope_lut_generate(None, 4096, 10000.0, C.byref(h)) == skv.EINVAL
+    assert L.swiftkv_kv_cache_create(None, 1, 1, 1, C.byref(h)) == skv.EINVAL
+    assert L.swiftkv_timer_record(None, 0) == skv.EINVAL
+    counts = (C.c_int64 * 3)()
+    ms = (C.c_double * 3)()
+    assert L.swiftkv_profile_collect(None, counts, ms) == skv.EINVAL
+    # destroy functions accept null like free()
+    assert L.swiftkv_context_destroy(None) == skv.OK
+    assert L.swiftkv_kv_cache_destroy(None) == skv.OK
+    assert L.swiftkv_rope_lut_destroy(None) == skv.OK
+
+
+def test_no_device_is_a_hip_error(skv):
+    import torch  # noqa: F401  (only to know whether a device is visible)
+    if torch.cuda.is_available():
+        pytest.skip("a device is visible")
+    with pytest.raises(skv.SwiftKVError) as ei:
+        skv.Context(0)
+    assert ei.value.code == skv.EHIP
+
+
+def test_unpack_a14_roundtrip(skv, oracle):
+    rng = np.random.default_rng(4)
+    q = rng.integers(-8191, 8192, (10, 32)).astype(np.int16)
+    assert (skv.unpack_a14(oracle.pack_a14(q)) == q).all()
+
+
+def test_scale_bits(skv, oracle):
+    s = np.arange(26, dtype=np.uint8)
+    assert (skv.scale_bits(s) == oracle.shift_scale_bits(s)).all()
+    assert (skv.scale_bits(s).view(np.float32) == np.ldexp(np.float32(1), s.astype(int) - 17)).all()

@@ -1,0 +1,271 @@
+"""GPU parity: the HIP path (through the C ABI) against the oracle on the same
+seeded inputs.  Appended codes and scales bit-exact; FP32 outputs within
+max-abs 2e-5 + rel 1e-4 of the FP32 formula (double-precision oracle)."""
+import hashlib
+import sys
+
+import numpy as np
+import pytest
+
+import oracle as O
+from gpu_cases import (H, assert_close, assert_rows_equal, history, oracle_sequence, outlier_channels,
+                       prefill, run_step)
+from helpers import f32_normal, kat_vector
+
+pytestmark = pytest.mark.gpu
+
+
+def _note(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def lut4096(skv, ctx):
+    lut = skv.RopeLut.generate(ctx, 4096)
+    yield lut
+    lut.close()
+
+
+def _scenario(skv, ctx, lut, rope_tables, positions, seed, layers=1, layer=0, cap=None, dist="normal",
+              outliers=None, split=0, q17=False):
+    """Prefill each sequence's history, run one step, compare everything."""
+    cos, sin = rope_tables
+    B = len(positions)
+    cap = cap or (max(positions) + 1)
+    kv = skv.KVCache(ctx, layers=layers, max_batch=B, max_seq_len=cap)
+    ctx.set_split_tokens(split)
+    scs = []
+    for b, p in enumerate(positions):
+        kh, vh = history(seed + 10 * b, p, dist, outliers)
+        prefill(skv, ctx, kv, lut, layer, b, kh, vh)
+        scs.append(oracle_sequence(cos, sin, kh, vh, p + 1))
+    q = f32_normal(seed + 1000, (B, 4096))
+    k = f32_normal(seed + 1001, (B, 4096))
+    v = f32_normal(seed + 1002, (B, 4096))
+    if outliers is not None:
+        k[:, outliers] *= np.float32(20.0)
+    if q17:
+        q, k, v = O.f2q17(q), O.f2q17(k), O.f2q17(v)
+        out, aq, asc = run_step(skv, ctx, kv, lut, layer, positions, q, k, v, q17=True)
+        qq, kq, vq = q, k, v
+    else:
+        out, aq, asc = run_step(skv, ctx, kv, lut, layer, positions, q, k, v)
+        qq, kq, vq = O.f2q17(q), O.f2q17(k), O.f2q17(v)
+    errs = []
+    for b, p in enumerate(positions):
+        res = scs[b].step_q17(qq[b], kq[b], vq[b], p, cos[p], sin[p], fp=True)
+        assert_rows_equal(kv, scs[b], b, layer, 0, p + 1)
+        errs.append(assert_close(out[b].reshape(H, 128), res["fp"], f"seq {b} position {p}"))
+        # A14/E8M0 epilogue: bit-exact against the rule applied to the GPU's own FP32 output
+        q14, e8 = O.a14(out[b].reshape(128, 32))
+        assert (asc[b] == e8).all(), f"seq {b}: E8M0 codes"
+        assert (aq[b] == O.pack_a14(q14)).all(), f"seq {b}: A14 words"
+        # and within one code of the rule applied to the oracle's output
+        q14r, e8r = O.a14(res["fp"].reshape(128, 32).astype(np.float32))
+        same_e = e8r == e8
+        assert same_e.mean() > 0.95
+        assert np.all(np.abs(q14.astype(np.int32) - q14r.astype(np.int32))[same_e] <= 1)
+    ctx.set_split_tokens(0)
+    kv.close()
+    return max(errs)
+
+
+def test_config1_batch1_position127(skv, ctx, lut4096, rope_tables):
+    _note("case: batch 1, position 127")
+    _scenario(skv, ctx, lut4096, rope_tables, [127], seed=11)
+
+
+def test_batch_positions_edges(skv, ctx, lut4096, rope_tables):
+    _note("case: batch 6 positions [0,1,63,64,255,300], layer 1 of 3")
+    _scenario(skv, ctx, lut4096, rope_tables, [0, 1, 63, 64, 255, 300], seed=21, layers=3, layer=1, cap=320)
+
+
+def test_q17_entry(skv, ctx, lut4096, rope_tables):
+    _note("case: Q15.17 entry, batch 2")
+    _scenario(skv, ctx, lut4096, rope_tables, [5, 200], seed=31, q17=True)
+
+
+@pytest.mark.parametrize("split", [256, 512, 1024, 0])
+def test_split_sizes_ragged(skv, ctx, lut4096, rope_tables, split):
+    _note(f"case: ragged batch 4, split_tokens {split}")
+    _scenario(skv, ctx, lut4096, rope_tables, [256, 700, 1300, 2047], seed=41, split=split)
+
+
+def test_outlier_channels_context4096(skv, ctx, lut4096, rope_tables):
+    _note("case: batch 1 position 4095, 1% K channels x20")
+    _scenario(skv, ctx, lut4096, rope_tables, [4095], seed=51, outliers=outlier_channels(51))
+
+
+def test_student_t_beyond_reference_limit(skv, ctx, rope_tables):
+    _note("case: batch 2 positions 4200/4350, Student-t(3), extended RoPE table")
+    lut = skv.RopeLut.generate(ctx, 4416)
+    cos, sin = O.rope_values(4416)
+    _scenario(skv, ctx, lut, (cos, sin), [4200, 4350], seed=61, dist="t3")
+    lut.close()
+
+
+def test_kat_inputs_through_q17_entry(skv, ctx, lut4096, rope_tables):
+    """The reference KAT sequence (positions 0 then 1 on one cache, PE0 heads
+    0..7 from tb_attention_pe0_kv_rtl.cpp:79-101) through the GPU path."""
+    _note("case: reference KAT inputs, positions 0 and 1")
+    cos, sin = rope_tables
+    kv = skv.KVCache(ctx, layers=1, max_batch=1, max_seq_len=64)
+    sc = O.SequenceCache(H, 2)
+    seeds = [(3, 11, 29), (43, 61, 79)]
+    for pos in (0, 1):
+        # PE0 heads 0..7 carry the KAT words; other heads reuse the generator with shifted seeds
+        vecs = [np.concatenate([kat_vector(s + 100 * pe) for pe in range(4)]) for s in seeds[pos]]
+        q, k, v = (x.reshape(1, 4096) for x in vecs)
+        out, _, _ = run_step(skv, ctx, kv, lut4096, 0, [pos], q, k, v, q17=True)
+        res = sc.step_q17(q, k, v, pos, cos[pos], sin[pos], fp=True)
+        assert_rows_equal(kv, sc, 0, 0, 0, pos + 1)
+        assert_close(out[0].reshape(H, 128), res["fp"], f"KAT position {pos}")
+    kv.close()
+
+
+def test_sequential_decode_and_repeat(skv, ctx, lut4096, rope_tables):
+    """Three consecutive steps on one cache (append of step p visible to p+1),
+    then a repeated step at the same position (idempotent overwrite)."""
+    _note("case: sequential decode 3 steps + repeat")
+    cos, sin = rope_tables
+    kv = skv.KVCache(ctx, layers=2, max_batch=2, max_seq_len=600)
+    kh, vh = history(71, 500)
+    scs = []
+    for b in range(2):
+        prefill(skv, ctx, kv, lut4096, 1, b, kh, vh)
+        scs.append(oracle_sequence(cos, sin, kh, vh, 600))
+    for step in range(3):
+        pos = [500 + step, 500 + step]
+        q, k, v = (f32_normal(80 + 3 * step + i, (2, 4096)) for i in range(3))
+        out, _, _ = run_step(skv, ctx, kv, lut4096, 1, pos, q, k, v, a14=False)
+        for b in range(2):
+            res = scs[b].step_q17(O.f2q17(q[b]), O.f2q17(k[b]), O.f2q17(v[b]), pos[b], cos[pos[b]], sin[pos[b]])
+            assert_close(out[b].reshape(H, 128), res["fp"], f"step {step} seq {b}")
+    out2, _, _ = run_step(skv, ctx, kv, lut4096, 1, [502, 502], q, k, v, a14=False)
+    assert np.array_equal(out, out2)
+    for b in range(2):
+        assert_rows_equal(kv, scs[b], b, 1, 0, 503)
+    # layer 0 untouched
+    kc, vc, ks, vs = kv.read(0, 0, 5, 0, 600)
+    assert not kc.any() and not vc.any() and not ks.any() and not vs.any()
+    kv.close()
+
+
+def test_records_export_import(skv, ctx, lut4096, rope_tables):
+    _note("case: reference record export/import")
+    cos, sin = rope_tables
+    kv = skv.KVCache(ctx, layers=1, max_batch=2, max_seq_len=128)
+    kh, vh = history(91, 100)
+    prefill(skv, ctx, kv, lut4096, 0, 0, kh, vh)
+    sc = oracle_sequence(cos, sin, kh, vh, 100)
+    for h in (0, 17, 31):
+        rec = kv.export_records(0, 0, h, 0, 100)
+        for t in (0, 42, 99):
+            assert (rec[t] == O.pack_record(sc.kc[h, t], sc.ks[h, t], sc.vc[h, t], sc.vs[h, t])).all()
+        kv.import_records(1, 0, h, 0, rec)
+        a, b = kv.read(0, 0, h, 0, 100), kv.read(1, 0, h, 0, 100)
+        assert all(np.array_equal(x, y) for x, y in zip(a, b))
+    kv.close()
+
+
+@pytest.mark.parametrize("dist,outliers", [(0, False), (0, True), (1, False)])
+def test_synthetic_fill_is_the_append_rule(skv, ctx, lut4096, rope_tables, dist, outliers):
+    """The device cache filler equals the oracle's append rule applied to the
+    FP32 rows of the same synthetic streams; other slots/layers untouched."""
+    _note(f"case: synthetic cache fill dist={dist} outliers={outliers}")
+    cos, sin = rope_tables
+    ntok = 150
+    kv = skv.KVCache(ctx, layers=2, max_batch=3, max_seq_len=200)
+    kv.fill_synthetic(lut4096, ntok=ntok, seed=5, layer0=1, nlayers=1, seq0=1, nseq=2, dist=dist,
+                      k_outliers=outliers)
+    buf = ctx.alloc(ntok * 4096 * 4)
+    for slot in (1, 2):
+        sid = 2 * (slot * 64 + 1)
+        ctx.fill_synthetic(buf, ntok * 4096, 5, sid, dist, outliers)
+        kf = buf.download(np.float32, (ntok, 4096))
+        ctx.fill_synthetic(buf, ntok * 4096, 5, sid + 1, dist, False)
+        vf = buf.download(np.float32, (ntok, 4096))
+        sc = oracle_sequence(cos, sin, kf, vf, ntok)
+        assert_rows_equal(kv, sc, slot, 1, 0, ntok)
+        x = vf.astype(np.float64)
+        assert abs(x.mean()) < 0.01 and abs(x.std() - 1.0) < 0.05
+        if outliers:
+            big = np.abs(kf).mean(axis=0) > 5.0
+            assert 20 <= big.sum() <= 70
+    for slot, layer in ((0, 1), (1, 0)):
+        kc, vc, ks, vs = kv.read(slot, layer, 3, 0, 200)
+        assert not kc.any() and not ks.any()
+    buf.free()
+    kv.close()
+
+
+def test_rope_table_generate_load_export(skv, ctx, golden):
+    _note("case: RoPE table generate/load/export")
+    lut = skv.RopeLut.generate(ctx, 4096)
+    image = lut.export()
+    assert hashlib.sha256(image).hexdigest() == golden["rope"]["sha256"]
+    lut2 = skv.RopeLut.load(ctx, image)
+    assert lut2.positions == 4096 and lut2.export() == image
+    lut.close()
+    lut2.close()
+
+
+def test_convert_stratified_bit_patterns(skv, ctx):
+    """Device FP32 -> Q15.17 on every exponent x sign x 2^15 fractions (incl.
+    every halfway pattern class) against the oracle, which is itself pinned
+    exhaustively on the CPU."""
+    _note("case: FP32 -> Q15.17 stratified sweep")
+    e = np.arange(256, dtype=np.uint32)
+    frac = np.unique(np.concatenate([
+        (np.arange(1 << 15, dtype=np.uint64) * np.uint64(2654435761) % np.uint64(1 << 23)).astype(np.uint32),
+        (np.uint32(1) << np.arange(23, dtype=np.uint32)),
+        (np.uint32(1) << np.arange(23, dtype=np.uint32)) - np.uint32(1),
+        (np.uint32(3) << np.arange(22, dtype=np.uint32)),
+        np.array([0, (1 << 23) - 1], np.uint32)]))
+    bits = ((e[:, None, None] << np.uint32(23)) | frac[None, None, :] |
+            (np.array([0, 1], np.uint32)[None, :, None] << np.uint32(31))).reshape(-1)
+    n = bits.size
+    din = ctx.to_device(bits)
+    dout = ctx.alloc(n * 4)
+    ctx.convert_f32_q17(din, dout, n)
+    got = dout.download(np.int32, (n,))
+    assert (got == O.f2q17(bits.view(np.float32))).all()
+
+
+def test_error_codes(skv, ctx, lut4096):
+    _note("case: argument validation")
+    kv = skv.KVCache(ctx, layers=2, max_batch=2, max_seq_len=128)
+    buf = ctx.alloc(2 * 4096 * 4)
+    small = skv.RopeLut.generate(ctx, 64)
+
+    def step(**kw):
+        args = dict(q=buf, k=buf, v=buf, kv_cache=kv, rope_lut=lut4096, activation_q=None,
+                    activation_scale=None, layer_index=0, position=[3], out=buf)
+        args.update(kw)
+        skv.swiftkv_attention(ctx, **args)
+
+    cases = [
+        (dict(position=[128]), skv.ERANGE),          # beyond cache capacity
+        (dict(position=[-1]), skv.ERANGE),
+        (dict(position=[100], rope_lut=small), skv.ERANGE),   # beyond the RoPE table
+        (dict(layer_index=2), skv.ERANGE),
+        (dict(position=[1, 2, 3]), skv.ERANGE),      # batch > max_batch
+        (dict(activation_q=buf), skv.EINVAL),         # activation_scale missing
+        (dict(out=None), skv.EINVAL),
+    ]
+    for kw, code in cases:
+        with pytest.raises(skv.SwiftKVError) as ei:
+            step(**kw)
+        assert ei.value.code == code, kw
+    with pytest.raises(skv.SwiftKVError) as ei:
+        skv.swiftkv_append_tokens(ctx, buf, buf, kv, lut4096, 0, 0, 120, 16)
+    assert ei.value.code == skv.ERANGE
+    with pytest.raises(skv.SwiftKVError) as ei:
+        ctx.set_split_tokens(300)
+    assert ei.value.code == skv.EINVAL
+    step()   # a valid call still works after the failures
+    ctx.synchronize()
+    small.close()
+    kv.close()
+    buf.free()
