@@ -43,7 +43,7 @@ TOKEN_BYTES = 288          # algorithmic bytes per cached token-head: 2 x 128 co
 
 OK, EINVAL, ERANGE, EHIP, ENOMEM, ESTATE = 0, -1, -2, -3, -4, -5
 DIST_NORMAL, DIST_STUDENT_T3 = 0, 1
-KERNEL_APPEND, KERNEL_ATTEND, KERNEL_COMBINE = 0, 1, 2
+KERNEL_APPEND, KERNEL_STEP, KERNEL_COMBINE = 0, 1, 2
 _STATUS_NAMES = {EINVAL: "EINVAL", ERANGE: "ERANGE", EHIP: "EHIP", ENOMEM: "ENOMEM", ESTATE: "ESTATE"}
 
 

@@ -72,8 +72,6 @@ struct swiftkv_context {
     hipStream_t stream = nullptr;
     int32_t split_tokens = 0;   // 0: heuristic
     // split-context workspace
-    float* qhat = nullptr;
-    size_t qhat_elems = 0;
     float* partials = nullptr;
     size_t partial_elems = 0;
     // timing
@@ -177,16 +175,21 @@ int upload_lut(swiftkv_context* ctx, std::vector<int2>&& host, int32_t positions
     return ok();
 }
 
-// Tokens per split: enough work items to fill 256 CUs several times over,
-// without splitting a (sequence, head) finer than one 256-token quantum.
+// Tokens per split.  Aim for about 2048 workgroups (a few residency rounds on
+// 256 CUs): split a head only when batch x 32 heads is below that, and never
+// below one 256-token quantum.  A head held by one split needs no combine
+// launch, which is worth more than the finer tail of smaller splits (batch
+// 64 at context 4096: one split per head runs 378 us/layer, 1024-token
+// splits 385 us/layer including their combine).
 int32_t choose_split(const swiftkv_context* ctx, const int32_t* positions, int32_t batch) {
     if (ctx->split_tokens > 0) return ctx->split_tokens;
-    int64_t quanta = 0;
-    for (int32_t b = 0; b < batch; ++b) quanta += (positions[b] + kSplitQuantum) / kSplitQuantum;
-    quanta *= kHeads;
-    int64_t mult = quanta / 8192;
-    mult = std::max<int64_t>(1, std::min<int64_t>(mult, 8));
-    return static_cast<int32_t>(mult * kSplitQuantum);
+    int32_t max_len = 1;
+    for (int32_t b = 0; b < batch; ++b) max_len = std::max(max_len, positions[b] + 1);
+    const int64_t heads = static_cast<int64_t>(batch) * kHeads;
+    const int64_t splits_per_head = std::max<int64_t>(1, (2048 + heads - 1) / heads);
+    const int64_t tokens = (max_len + splits_per_head - 1) / splits_per_head;
+    const int64_t quanta = std::max<int64_t>(1, (tokens + kSplitQuantum - 1) / kSplitQuantum);
+    return static_cast<int32_t>(std::min<int64_t>(quanta * kSplitQuantum, kMaxSeq));
 }
 
 int validate_step(swiftkv_context* ctx, const void* q, const void* k, const void* v,
@@ -253,26 +256,23 @@ int run_step(swiftkv_context* ctx, const void* q, const void* k, const void* v, 
         a.split_tokens = choose_split(ctx, a.positions, nb);
         const int32_t grid_splits = (max_pos + 1 + a.split_tokens - 1) / a.split_tokens;
         a.max_splits = grid_splits;
-        if ((rc = ensure(ctx, ctx->qhat, ctx->qhat_elems, static_cast<size_t>(nb) * kModelDim))) return rc;
         if ((rc = ensure(ctx, ctx->partials, ctx->partial_elems,
                          static_cast<size_t>(nb) * kHeads * grid_splits * kPartialStride)))
             return rc;
-        a.qhat = ctx->qhat;
         a.partials = ctx->partials;
         a.out = out + row0;
         a.act_q = act_q ? act_q + static_cast<size_t>(b0) * kHeads * kGroupsPerHead * SWIFTKV_A14_WORD_BYTES
                         : nullptr;
         a.act_scale = act_scale ? act_scale + static_cast<size_t>(b0) * kHeads * kGroupsPerHead : nullptr;
 
-        ProfilePair* p = profile_begin(ctx, SWIFTKV_KERNEL_APPEND);
-        SKV_HIP(launch_append_step(a, q17, ctx->stream));
+        ProfilePair* p = profile_begin(ctx, SWIFTKV_KERNEL_STEP);
+        SKV_HIP(launch_step(a, grid_splits, q17, ctx->stream));
         profile_end(ctx, p);
-        p = profile_begin(ctx, SWIFTKV_KERNEL_ATTEND);
-        SKV_HIP(launch_attend(a, grid_splits, ctx->stream));
-        profile_end(ctx, p);
-        p = profile_begin(ctx, SWIFTKV_KERNEL_COMBINE);
-        SKV_HIP(launch_combine(a, ctx->stream));
-        profile_end(ctx, p);
+        if (grid_splits > 1) {   // some head spans several splits
+            p = profile_begin(ctx, SWIFTKV_KERNEL_COMBINE);
+            SKV_HIP(launch_combine(a, ctx->stream));
+            profile_end(ctx, p);
+        }
     }
     return ok();
 }
@@ -338,7 +338,6 @@ int swiftkv_context_destroy(swiftkv_context* ctx) {
     if (!ctx) return ok();
     (void)hipSetDevice(ctx->device);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
-    if (ctx->qhat) (void)hipFree(ctx->qhat);
     if (ctx->partials) (void)hipFree(ctx->partials);
     for (auto& t : ctx->timers)
         if (t) (void)hipEventDestroy(t);

@@ -29,6 +29,8 @@ constexpr int kAttendWaves = 4;
 constexpr int kBlockTokens = 64;
 constexpr int kSplitQuantum = kAttendWaves * kBlockTokens;   // 256
 constexpr int kPartialStride = 4 + kHeadDim;     // (m, l, pad, pad, acc[128]) floats
+constexpr int kMaxSeq = 32768;                   // longest cache this build accepts
+constexpr int kMaxSplits = kMaxSeq / kSplitQuantum;   // 128 partials per (sequence, head)
 
 // Sequences per launch: positions travel by value in the kernel arguments.
 constexpr int kMaxBatchPerLaunch = 256;
@@ -52,7 +54,6 @@ struct StepArgs {
     const void* q;            // [batch][4096] FP32 or Q15.17
     const void* k;
     const void* v;
-    float* qhat;              // [batch][4096] rotated query, q_raw * 2^-17
     CacheView kv;
     const int2* lut;          // [lut_positions][64] (cos, sin) Q1.17
     int32_t lut_positions;
@@ -82,8 +83,7 @@ struct BulkArgs {
 };
 
 // Launchers (swiftkv_kernels.hip).
-hipError_t launch_append_step(const StepArgs& a, bool q17, hipStream_t s);
-hipError_t launch_attend(const StepArgs& a, int grid_splits, hipStream_t s);
+hipError_t launch_step(const StepArgs& a, int grid_splits, bool q17, hipStream_t s);
 hipError_t launch_combine(const StepArgs& a, hipStream_t s);
 hipError_t launch_append_bulk(const BulkArgs& a, bool q17, hipStream_t s);
 hipError_t launch_convert(const float* in, int32_t* out, size_t n, hipStream_t s);

@@ -1,21 +1,26 @@
 // swiftkv_kernels.hip -- CDNA4 (gfx950) kernels of the SwiftKV decode-attention
-// stage.  Three kernels per decode step:
+// stage.
 //
-//   append   one wavefront per (sequence, head).  Lane l owns RoPE pair l
-//            (channels 2l, 2l+1): FP32 -> Q15.17, integer rotation, G32
-//            max by a 16-lane butterfly (one G32 group = 16 lanes), INT8
-//            codes, and the appended row (128-B coalesced code rows and the
-//            scale pair).  Also writes the rotated query as FP32.
-//   attend   split-context scan (flash-decoding).  A 256-thread workgroup
-//            scans split_tokens tokens of one (sequence, head); each wave
-//            takes 64-token blocks.  Lane = (chunk c = lane&7, row r =
-//            lane>>3): one dwordx4 per lane reads a 16-channel chunk, so one
-//            wave instruction reads 8 full 128-B code rows.  INT8 codes are
-//            dequantized in VGPRs, partial dots are reduced over the 8 chunk
-//            lanes with DPP, and the running (max, sum, acc) lives in VGPRs.
-//            Waves merge through LDS; one partial (m, l, acc[128]) per split.
-//   combine  log-sum-exp merge of the splits per (sequence, head), the FP32
-//            output, and optionally the A14/E8M0 epilogue.
+// step kernel (one launch per decode step and layer), grid (splits, 32 heads,
+// batch) of 256-thread workgroups; workgroup (j, h, b) owns tokens
+// [j*C, min((j+1)*C, position+1)) of sequence b, head h:
+//   1. every lane rotates the 16 query channels it needs (integer RoPE from
+//      the Q1.17 table, FP32 -> Q15.17 first for FP32 inputs);
+//   2. the workgroup whose range holds `position` also converts, rotates and
+//      G32-quantizes the new K/V row, appends it to the cache, and forwards it
+//      into its own merge as one more partial -- the new token is written once
+//      and never read back (the reference does the same, hpp:37-41);
+//   3. four waves scan the cached tokens in 64-token blocks.  Lane = (chunk
+//      c = lane&7, row r = lane>>3): one nontemporal dwordx4 per lane reads a
+//      16-channel chunk, so one wave instruction covers 8 full 128-B code
+//      rows.  Codes are dequantized in VGPRs, partial dots reduced over the 8
+//      chunk lanes with DPP, the running (max, sum, acc) stays in VGPRs;
+//   4. waves (plus the forwarded row) merge through LDS;
+//   5. a head held by one split is finished in place (FP32 output and the
+//      optional A14/E8M0 words); otherwise the split stores its partial
+//      (m, l, acc[128]).
+// combine kernel (only when some head spans several splits): log-sum-exp
+// merge of the partials of each (sequence, head), then the same epilogue.
 //
 // No MFMA: q_len = 1 multi-head attention is a memory-bound GEMV.
 #include "swiftkv_device.hpp"
@@ -25,25 +30,334 @@ namespace {
 
 using namespace dev;
 
-// Grid (8, batch): 4 waves per workgroup, wave = head.
-template <bool Q17>
-__global__ __launch_bounds__(256) void append_step_kernel(StepArgs a) {
-    const int b = blockIdx.y;
-    const int h = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    const int pos = a.positions[b];
-    const size_t elem = static_cast<size_t>(b) * kModelDim + h * kHeadDim + 2 * lane;
-    const int2 cs = a.lut[static_cast<size_t>(pos) * kRopePairs + lane];
-    const int2 qi = load_pair<Q17>(a.q, elem);
-    const int2 ki = load_pair<Q17>(a.k, elem);
-    const int2 vi = load_pair<Q17>(a.v, elem);
-    int32_t q0, q1, k0, k1;
-    rope_pair(qi.x, qi.y, cs, q0, q1);
-    rope_pair(ki.x, ki.y, cs, k0, k1);
-    reinterpret_cast<float2*>(a.qhat)[elem >> 1] =
-        make_float2(static_cast<float>(q0) * 0x1p-17f, static_cast<float>(q1) * 0x1p-17f);
-    append_row(page_ptr(a.kv, a.slot0 + b, a.layer, h), a.kv.seq_cap, pos, lane, k0, k1, vi.x, vi.y);
+static_assert(kMaxSplits <= kHeadDim, "one combine thread per split statistic");
+
+// Scores are kept in the log2 domain: the query is pre-scaled by
+// 1/sqrt(128) * log2(e) so the softmax uses v_exp_f32 (2^x) directly.
+constexpr float kScoreScale = (1.0f / 11.313708498984761f) * 1.4426950408889634f;
+
+// Native vector types: the nontemporal load builtin takes ext_vector pointers.
+typedef int32_t v4i __attribute__((ext_vector_type(4)));
+typedef float v2f __attribute__((ext_vector_type(2)));
+typedef int32_t v2i __attribute__((ext_vector_type(2)));
+
+// The cache is streamed exactly once per step, so every cache load is
+// nontemporal: it keeps the stream from displacing reusable lines in L2/MALL
+// (streaming reads reach ~88% of HBM peak this way versus ~78% with
+// default-policy loads).
+
+// 16 int8 codes of one dwordx4 times 16 query values.
+__device__ __forceinline__ float dot16(const float* q, v4i w) {
+    const int32_t d[4] = {w[0], w[1], w[2], w[3]};
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+        for (int byte = 0; byte < 4; ++byte) {
+            const float code = static_cast<float>(static_cast<int8_t>(d[j] >> (8 * byte)));
+            acc = __builtin_fmaf(q[4 * j + byte], code, acc);
+        }
+    }
+    return acc;
 }
+
+__device__ __forceinline__ void axpy16(float* acc, float w, v4i v) {
+    const int32_t d[4] = {v[0], v[1], v[2], v[3]};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+        for (int byte = 0; byte < 4; ++byte) {
+            const float code = static_cast<float>(static_cast<int8_t>(d[j] >> (8 * byte)));
+            acc[4 * j + byte] = __builtin_fmaf(w, code, acc[4 * j + byte]);
+        }
+    }
+}
+
+// ---------------------------------------------------------------- pieces
+
+// Rotated, pre-scaled query channels [16c, 16c+16) of head h (pairs 8c..8c+7).
+template <bool Q17>
+__device__ __forceinline__ void query_chunk(const StepArgs& a, int b, int h, int c, int pos, float* qf) {
+    const size_t base = static_cast<size_t>(b) * kModelDim + h * kHeadDim + c * 16;
+    const int2* cs = a.lut + static_cast<size_t>(pos) * kRopePairs + c * 8;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int2 qi = load_pair<Q17>(a.q, base + 2 * j);
+        int32_t x0, x1;
+        rope_pair(qi.x, qi.y, cs[j], x0, x1);
+        qf[2 * j] = (static_cast<float>(x0) * 0x1p-17f) * kScoreScale;
+        qf[2 * j + 1] = (static_cast<float>(x1) * 0x1p-17f) * kScoreScale;
+    }
+}
+
+// A page is read through one buffer resource held in SGPRs: the per-lane
+// offset is fixed for the whole scan and the token offset is a wave-uniform
+// SGPR, so the 24 loads of a block need no per-load 64-bit address VGPRs.
+// Reads past the page return zero instead of faulting.
+struct PageReader {
+    __amdgpu_buffer_rsrc_t rsrc;
+    int32_t k_lane;       // lane's byte offset in the K plane (row r, chunk c)
+    int32_t v_lane;       // the same in the V plane
+    int32_t s_lane;       // lane's (K, V) scale pair of group c/2 in the scale plane
+};
+
+constexpr int32_t kBufferWord3 = 0x00020000;   // raw buffer, gfx9 data format
+constexpr int kNontemporal = 2;                // cache policy: nt
+
+__device__ __forceinline__ PageReader make_reader(const int8_t* page, int64_t cap, int c, int r) {
+    PageReader pr;
+    pr.rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(page), static_cast<short>(0),
+                                                static_cast<int32_t>(cap * kTokenBytes), kBufferWord3);
+    pr.k_lane = r * kCodeBytes + c * 16;
+    pr.v_lane = static_cast<int32_t>(cap * kCodeBytes) + r * kCodeBytes + c * 16;
+    pr.s_lane = static_cast<int32_t>(cap * 2 * kCodeBytes) + r * kScaleBytes + (c >> 1) * 8;
+    return pr;
+}
+
+// One 64-token block [t0, t0+64) of the scan; MASKED blocks drop tokens >= t_stop.
+template <bool MASKED>
+__device__ __forceinline__ void scan_block(const PageReader& pr, const float* qf, int t0, int t_stop, int r,
+                                           float& m_run, float& l_run, float* acc) {
+    v4i kw[8], vw[8];
+    v2f sw[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int32_t tok = t0 + 8 * i;
+        kw[i] = __builtin_amdgcn_raw_buffer_load_b128(pr.rsrc, pr.k_lane, tok * kCodeBytes, kNontemporal);
+        sw[i] = __builtin_bit_cast(v2f, __builtin_amdgcn_raw_buffer_load_b64(pr.rsrc, pr.s_lane, tok * kScaleBytes,
+                                                                              kNontemporal));
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int32_t tok = t0 + 8 * i;
+        vw[i] = __builtin_amdgcn_raw_buffer_load_b128(pr.rsrc, pr.v_lane, tok * kCodeBytes, kNontemporal);
+    }
+    // Keep all 24 loads of the block in flight before any math: without this
+    // fence the scheduler sinks V loads next to their uses (to save VGPRs) and
+    // serializes them at full memory latency.
+    __builtin_amdgcn_sched_barrier(0);
+    float s[8];
+    float blk = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        s[i] = octet_sum(dot16(qf, kw[i]) * sw[i][0]);
+        if (MASKED && t0 + 8 * i + r >= t_stop) s[i] = -INFINITY;
+        blk = fmaxf(blk, s[i]);
+    }
+    blk = across_octets_max(blk);
+    const float m_new = fmaxf(m_run, blk);
+    const float alpha = fast_exp2(m_run - m_new);
+    m_run = m_new;
+    l_run *= alpha;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[j] *= alpha;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        float p = fast_exp2(s[i] - m_new);            // masked: 2^-inf = 0
+        float w = p * sw[i][1];
+        if (MASKED && t0 + 8 * i + r >= t_stop) w = 0.0f;   // never multiply a stale scale
+        l_run += p;
+        axpy16(acc, w, vw[i]);
+    }
+}
+
+// One wave's online-softmax scan over the 64-token blocks starting at t0,
+// t0+stride, ... below t_stop, lane layout (c, r).  On return every lane
+// holds the wave's (m, l) and, for its chunk c, acc[16] summed over the rows.
+__device__ __forceinline__ void scan_range(const PageReader& pr, const float* qf, int t0, int t_stop, int stride,
+                                           int r, float& m_run, float& l_run, float* acc) {
+    m_run = -INFINITY;
+    l_run = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
+    for (; t0 + kBlockTokens <= t_stop; t0 += stride) scan_block<false>(pr, qf, t0, t_stop, r, m_run, l_run, acc);
+    if (t0 < t_stop) scan_block<true>(pr, qf, t0, t_stop, r, m_run, l_run, acc);
+    l_run = across_octets_sum(l_run);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[j] = across_octets_sum(acc[j]);
+}
+
+// Per-(sequence, head) output: FP32 row and, when requested, A14/G32 + E8M0
+// (swiftkv_attention.cpp:1715-1771, 2656-2682): per 32 outputs, e = frexp
+// exponent of max|o|, q = trunc(clamp(o*2^(13-e) +- 0.5, +-8191)), code =
+// e + 127 (0 for an all-zero group).  Called by every thread of the block;
+// threads d < 128 supply output channel d.
+__device__ __forceinline__ void finalize_head(const StepArgs& a, int b, int h, float o) {
+    const int d = threadIdx.x;
+    const bool active = d < kHeadDim;
+    if (active) a.out[static_cast<size_t>(b) * kModelDim + h * kHeadDim + d] = o;
+    if (a.act_q == nullptr) return;
+    float mx_abs = active ? fabsf(o) : 0.0f;
+#pragma unroll
+    for (int s = 1; s < 32; s <<= 1) mx_abs = fmaxf(mx_abs, __shfl_xor(mx_abs, s));
+    int16_t q14 = 0;
+    uint8_t code = 0;
+    if (mx_abs != 0.0f) {
+        int e = 0;
+        (void)frexpf(mx_abs, &e);
+        const float inv = ldexpf(1.0f, 13 - e);
+        const float sc = __fmul_rn(o, inv);
+        float rr = sc >= 0.0f ? __fadd_rn(sc, 0.5f) : __fsub_rn(sc, 0.5f);
+        rr = fminf(fmaxf(rr, -8191.0f), 8191.0f);
+        q14 = static_cast<int16_t>(static_cast<int>(rr));
+        code = static_cast<uint8_t>(e + 127);
+    }
+    __shared__ int16_t s_q14[kHeadDim];
+    if (active) s_q14[d] = q14;
+    __syncthreads();
+    const size_t grp0 = static_cast<size_t>(b) * (kHeads * kGroupsPerHead) + h * kGroupsPerHead;
+    if (active && (d & 31) == 0) a.act_scale[grp0 + (d >> 5)] = code;
+    // 4 groups x 14 dwords of packed 14-bit lanes (lane i at bits [14i, 14i+13]).
+    if (d < kGroupsPerHead * 14) {
+        const int g = d / 14, w = d % 14;
+        uint32_t word = 0;
+        const int bit0 = 32 * w;
+        for (int i = bit0 / 14; i <= (bit0 + 31) / 14 && i < 32; ++i) {
+            const uint32_t val = static_cast<uint32_t>(static_cast<uint16_t>(s_q14[g * 32 + i])) & 0x3fffu;
+            const int sh = 14 * i - bit0;
+            word |= sh >= 0 ? (val << sh) : (val >> -sh);
+        }
+        reinterpret_cast<uint32_t*>(a.act_q + (grp0 + g) * 56)[w] = word;
+    }
+}
+
+// Log-sum-exp merge of n split partials; threads d < 128 get output channel d.
+// Split statistics are fetched in parallel (thread j loads split j), so the
+// merge costs two dependent memory round trips whatever n is.
+__device__ __forceinline__ float merge_partials(const float* part, int n) {
+    const int d = threadIdx.x;
+    __shared__ float s_m[kMaxSplits], s_l[kMaxSplits], s_w[kMaxSplits];
+    __shared__ float s_mx, s_den;
+    if (d < n) {
+        s_m[d] = part[d * kPartialStride];
+        s_l[d] = part[d * kPartialStride + 1];
+    }
+    __syncthreads();
+    if (d == 0) {
+        float mx = s_m[0];
+        for (int j = 1; j < n; ++j) mx = fmaxf(mx, s_m[j]);
+        s_mx = mx;
+    }
+    __syncthreads();
+    if (d < n) s_w[d] = fast_exp2(s_m[d] - s_mx);
+    __syncthreads();
+    if (d == 0) {
+        float den = 0.0f;
+        for (int j = 0; j < n; ++j) den += s_w[j] * s_l[j];
+        s_den = den;
+    }
+    float num = 0.0f;
+    if (d < kHeadDim) {
+#pragma unroll 8
+        for (int j = 0; j < n; ++j) num += s_w[j] * part[j * kPartialStride + 4 + d];
+    }
+    __syncthreads();
+    return num / s_den;
+}
+
+// ---------------------------------------------------------------- step
+
+// Grid (splits, 32 heads, batch), 256 threads.
+template <bool Q17>
+__global__ __launch_bounds__(kAttendWaves * 64) void step_kernel(StepArgs a) {
+    const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int pos = a.positions[b];
+    const int len = pos + 1;
+    const int C = a.split_tokens;
+    const int t_begin = split * C;
+    if (t_begin >= len) return;
+    const int t_end = min(t_begin + C, len);
+    const int nsplit = (len + C - 1) / C;
+    const bool owner = pos < t_end;               // this split holds the new token
+
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int c = lane & 7, r = lane >> 3;
+    int8_t* page = page_ptr(a.kv, a.slot0 + b, a.layer, h);
+    const int64_t cap = a.kv.seq_cap;
+
+    __shared__ float s_acc[kAttendWaves + 1][kHeadDim];
+    __shared__ float s_m[kAttendWaves + 1], s_l[kAttendWaves + 1];
+
+    // The new row: convert, rotate k, quantize, append; forward (k^ . q', v^).
+    if (owner && wave == 0) {
+        const size_t elem = static_cast<size_t>(b) * kModelDim + h * kHeadDim + 2 * lane;
+        const int2 cs = a.lut[static_cast<size_t>(pos) * kRopePairs + lane];
+        const int2 qi = load_pair<Q17>(a.q, elem);
+        const int2 ki = load_pair<Q17>(a.k, elem);
+        const int2 vi = load_pair<Q17>(a.v, elem);
+        int32_t q0, q1, k0, k1;
+        rope_pair(qi.x, qi.y, cs, q0, q1);
+        rope_pair(ki.x, ki.y, cs, k0, k1);
+        float kh0, kh1, vh0, vh1;
+        append_row_dequant(page, a.kv.seq_cap, pos, lane, k0, k1, vi.x, vi.y, kh0, kh1, vh0, vh1);
+        float sp = ((static_cast<float>(q0) * 0x1p-17f) * kScoreScale) * kh0 +
+                   ((static_cast<float>(q1) * 0x1p-17f) * kScoreScale) * kh1;
+#pragma unroll
+        for (int s = 1; s < 64; s <<= 1) sp += __shfl_xor(sp, s);
+        s_acc[kAttendWaves][2 * lane] = vh0;
+        s_acc[kAttendWaves][2 * lane + 1] = vh1;
+        if (lane == 0) {
+            s_m[kAttendWaves] = sp;
+            s_l[kAttendWaves] = 1.0f;
+        }
+    }
+
+    // Scan of the cached tokens of this split (the new token excluded).
+    float qf[16];
+    query_chunk<Q17>(a, b, h, c, pos, qf);
+    float m_run, l_run, acc[16];
+    scan_range(make_reader(page, cap, c, r), qf, t_begin + wave * kBlockTokens, owner ? pos : t_end,
+               kAttendWaves * kBlockTokens, r, m_run, l_run, acc);
+    if (r == 0) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) s_acc[wave][c * 16 + j] = acc[j];
+        if (c == 0) {
+            s_m[wave] = m_run;
+            s_l[wave] = l_run;
+        }
+    }
+    __syncthreads();
+
+    const int nparts = owner ? kAttendWaves + 1 : kAttendWaves;
+    const int d = threadIdx.x;
+    float o = 0.0f, l = 0.0f, mx = -INFINITY;
+    if (d < kHeadDim) {
+        mx = s_m[0];
+        for (int w = 1; w < nparts; ++w) mx = fmaxf(mx, s_m[w]);
+        for (int w = 0; w < nparts; ++w) {
+            const float sc = fast_exp2(s_m[w] - mx);     // parts with no tokens: 2^-inf = 0
+            o += sc * s_acc[w][d];
+            l += sc * s_l[w];
+        }
+    }
+    if (nsplit == 1) {
+        finalize_head(a, b, h, o / l);
+        return;
+    }
+
+    float* part = a.partials + ((static_cast<size_t>(b) * kHeads + h) * a.max_splits + split) * kPartialStride;
+    if (d < kHeadDim) {
+        part[4 + d] = o;
+        if (d == 0) {
+            part[0] = mx;
+            part[1] = l;
+        }
+    }
+}
+
+// ---------------------------------------------------------------- combine
+
+// Grid (32 heads, batch), 128 threads: thread d = output channel d.
+__global__ __launch_bounds__(kHeadDim) void combine_kernel(StepArgs a) {
+    const int h = blockIdx.x, b = blockIdx.y;
+    const int len = a.positions[b] + 1;
+    const int n = (len + a.split_tokens - 1) / a.split_tokens;
+    if (n == 1) return;   // finished by its only split in the step kernel
+    const float* parts = a.partials + (static_cast<size_t>(b) * kHeads + h) * a.max_splits * kPartialStride;
+    finalize_head(a, b, h, merge_partials(parts, n));
+}
+
+// ---------------------------------------------------------------- utilities
 
 // Grid (n, 8): token t = blockIdx.x, wave = head.
 template <bool Q17>
@@ -68,219 +382,14 @@ __global__ __launch_bounds__(256) void convert_kernel(const float* __restrict__ 
         out[i] = f32_to_q17(in[i]);
 }
 
-// ---------------------------------------------------------------- attend
-
-// 16 int8 codes of one dwordx4 times 16 query values.
-__device__ __forceinline__ float dot16(const float* q, int4 w) {
-    const int32_t d[4] = {w.x, w.y, w.z, w.w};
-    float acc = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-#pragma unroll
-        for (int byte = 0; byte < 4; ++byte) {
-            const float code = static_cast<float>(static_cast<int8_t>(d[j] >> (8 * byte)));
-            acc = __builtin_fmaf(q[4 * j + byte], code, acc);
-        }
-    }
-    return acc;
-}
-
-__device__ __forceinline__ void axpy16(float* acc, float w, int4 v) {
-    const int32_t d[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-#pragma unroll
-        for (int byte = 0; byte < 4; ++byte) {
-            const float code = static_cast<float>(static_cast<int8_t>(d[j] >> (8 * byte)));
-            acc[4 * j + byte] = __builtin_fmaf(w, code, acc[4 * j + byte]);
-        }
-    }
-}
-
-// Grid (splits, 32 heads, batch), 256 threads.
-__global__ __launch_bounds__(kAttendWaves * 64) void attend_kernel(StepArgs a) {
-    const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-    const int len = a.positions[b] + 1;
-    const int t_begin = split * a.split_tokens;
-    if (t_begin >= len) return;
-    const int t_end = min(t_begin + a.split_tokens, len);
-
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int c = lane & 7, r = lane >> 3;
-    const int8_t* page = page_ptr(a.kv, a.slot0 + b, a.layer, h);
-    const int64_t cap = a.kv.seq_cap;
-    const int8_t* kp = page + c * 16;
-    const int8_t* vp = page + cap * kCodeBytes + c * 16;
-    const float* sp = reinterpret_cast<const float*>(page + cap * (2 * kCodeBytes)) + (c >> 1) * 2;
-
-    // Query chunk, pre-scaled by 1/sqrt(128) * log2(e): scores live in the
-    // log2 domain so the softmax uses v_exp_f32 directly.
-    const float kScoreScale = (1.0f / 11.313708498984761f) * 1.4426950408889634f;
-    float qf[16];
-    {
-        const float4* qs = reinterpret_cast<const float4*>(a.qhat + static_cast<size_t>(b) * kModelDim +
-                                                           h * kHeadDim + c * 16);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float4 x = qs[j];
-            qf[4 * j + 0] = x.x * kScoreScale;
-            qf[4 * j + 1] = x.y * kScoreScale;
-            qf[4 * j + 2] = x.z * kScoreScale;
-            qf[4 * j + 3] = x.w * kScoreScale;
-        }
-    }
-
-    float m_run = -INFINITY, l_run = 0.0f;
-    float acc[16];
-#pragma unroll
-    for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
-
-    for (int t0 = t_begin + wave * kBlockTokens; t0 < t_end; t0 += kAttendWaves * kBlockTokens) {
-        int4 kw[8], vw[8];
-        float2 sw[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int64_t t = t0 + 8 * i + r;
-            kw[i] = *reinterpret_cast<const int4*>(kp + t * kCodeBytes);
-            sw[i] = *reinterpret_cast<const float2*>(sp + t * 8);
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int64_t t = t0 + 8 * i + r;
-            vw[i] = *reinterpret_cast<const int4*>(vp + t * kCodeBytes);
-        }
-        float s[8];
-        float blk = -INFINITY;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float d = octet_sum(dot16(qf, kw[i]) * sw[i].x);
-            s[i] = (t0 + 8 * i + r < t_end) ? d : -INFINITY;
-            blk = fmaxf(blk, s[i]);
-        }
-        blk = across_octets_max(blk);
-        const float m_new = fmaxf(m_run, blk);
-        const float alpha = fast_exp2(m_run - m_new);
-        m_run = m_new;
-        l_run *= alpha;
-#pragma unroll
-        for (int j = 0; j < 16; ++j) acc[j] *= alpha;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const bool valid = t0 + 8 * i + r < t_end;
-            const float p = valid ? fast_exp2(s[i] - m_new) : 0.0f;
-            l_run += p;
-            axpy16(acc, valid ? p * sw[i].y : 0.0f, vw[i]);
-        }
-    }
-
-    // Reduce over the 8 rows (token phases) of the wave.
-    l_run = across_octets_sum(l_run);
-#pragma unroll
-    for (int j = 0; j < 16; ++j) acc[j] = across_octets_sum(acc[j]);
-
-    __shared__ float s_acc[kAttendWaves][kHeadDim];
-    __shared__ float s_m[kAttendWaves], s_l[kAttendWaves];
-    if (r == 0) {
-#pragma unroll
-        for (int j = 0; j < 16; ++j) s_acc[wave][c * 16 + j] = acc[j];
-        if (c == 0) {
-            s_m[wave] = m_run;
-            s_l[wave] = l_run;
-        }
-    }
-    __syncthreads();
-    if (threadIdx.x < kHeadDim) {
-        const int d = threadIdx.x;
-        float mx = s_m[0];
-#pragma unroll
-        for (int w = 1; w < kAttendWaves; ++w) mx = fmaxf(mx, s_m[w]);
-        float o = 0.0f, l = 0.0f;
-#pragma unroll
-        for (int w = 0; w < kAttendWaves; ++w) {
-            const float sc = fast_exp2(s_m[w] - mx);   // waves with no tokens: 2^-inf = 0
-            o += sc * s_acc[w][d];
-            l += sc * s_l[w];
-        }
-        float* part = a.partials +
-                      ((static_cast<size_t>(b) * kHeads + h) * a.max_splits + split) * kPartialStride;
-        part[4 + d] = o;
-        if (d == 0) {
-            part[0] = mx;
-            part[1] = l;
-        }
-    }
-}
-
-// ---------------------------------------------------------------- combine
-
-// Grid (32 heads, batch), 128 threads: thread d = output channel d.
-__global__ __launch_bounds__(kHeadDim) void combine_kernel(StepArgs a) {
-    const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
-    const int len = a.positions[b] + 1;
-    const int n = (len + a.split_tokens - 1) / a.split_tokens;
-    const float* part = a.partials + (static_cast<size_t>(b) * kHeads + h) * a.max_splits * kPartialStride;
-    float mx = -INFINITY;
-    for (int j = 0; j < n; ++j) mx = fmaxf(mx, part[j * kPartialStride]);
-    float num = 0.0f, den = 0.0f;
-    for (int j = 0; j < n; ++j) {
-        const float w = fast_exp2(part[j * kPartialStride] - mx);
-        den += w * part[j * kPartialStride + 1];
-        num += w * part[j * kPartialStride + 4 + d];
-    }
-    const float o = num / den;
-    a.out[static_cast<size_t>(b) * kModelDim + h * kHeadDim + d] = o;
-
-    if (a.act_q == nullptr) return;
-    // A14/G32 + E8M0 (swiftkv_attention.cpp:1715-1771, 2656-2682): per 32
-    // outputs, e = frexp exponent of max|o|, q = trunc(clamp(o*2^(13-e) +-
-    // 0.5, +-8191)), code = e + 127 (0 for an all-zero group).
-    float mx_abs = fabsf(o);
-#pragma unroll
-    for (int s = 1; s < 32; s <<= 1) mx_abs = fmaxf(mx_abs, __shfl_xor(mx_abs, s));
-    int e = 0;
-    int16_t q14 = 0;
-    uint8_t code = 0;
-    if (mx_abs != 0.0f) {
-        (void)frexpf(mx_abs, &e);
-        const float inv = ldexpf(1.0f, 13 - e);
-        const float sc = __fmul_rn(o, inv);
-        float rr = sc >= 0.0f ? __fadd_rn(sc, 0.5f) : __fsub_rn(sc, 0.5f);
-        rr = fminf(fmaxf(rr, -8191.0f), 8191.0f);
-        q14 = static_cast<int16_t>(static_cast<int>(rr));
-        code = static_cast<uint8_t>(e + 127);
-    }
-    __shared__ int16_t s_q[kHeadDim];
-    s_q[d] = q14;
-    __syncthreads();
-    const size_t grp0 = static_cast<size_t>(b) * (kHeads * kGroupsPerHead) + h * kGroupsPerHead;
-    if ((d & 31) == 0) a.act_scale[grp0 + (d >> 5)] = code;
-    // 4 groups x 14 dwords of packed 14-bit lanes (lane i at bits [14i, 14i+13]).
-    if (d < kGroupsPerHead * 14) {
-        const int g = d / 14, w = d % 14;
-        uint32_t word = 0;
-        const int bit0 = 32 * w;
-        for (int i = bit0 / 14; i <= (bit0 + 31) / 14 && i < 32; ++i) {
-            const uint32_t val = static_cast<uint32_t>(static_cast<uint16_t>(s_q[g * 32 + i])) & 0x3fffu;
-            const int sh = 14 * i - bit0;
-            word |= sh >= 0 ? (val << sh) : (val >> -sh);
-        }
-        reinterpret_cast<uint32_t*>(a.act_q + (grp0 + g) * 56)[w] = word;
-    }
-}
-
 }  // namespace
 
 // ---------------------------------------------------------------- launchers
 
-hipError_t launch_append_step(const StepArgs& a, bool q17, hipStream_t s) {
-    const dim3 grid(kHeads / 4, a.batch);
-    if (q17) append_step_kernel<true><<<grid, 256, 0, s>>>(a);
-    else append_step_kernel<false><<<grid, 256, 0, s>>>(a);
-    return hipGetLastError();
-}
-
-hipError_t launch_attend(const StepArgs& a, int grid_splits, hipStream_t s) {
-    attend_kernel<<<dim3(grid_splits, kHeads, a.batch), kAttendWaves * 64, 0, s>>>(a);
+hipError_t launch_step(const StepArgs& a, int grid_splits, bool q17, hipStream_t s) {
+    const dim3 grid(grid_splits, kHeads, a.batch);
+    if (q17) step_kernel<true><<<grid, kAttendWaves * 64, 0, s>>>(a);
+    else step_kernel<false><<<grid, kAttendWaves * 64, 0, s>>>(a);
     return hipGetLastError();
 }
 

@@ -217,11 +217,11 @@ int swiftkv_timer_record(swiftkv_context* ctx, int32_t slot);
 int swiftkv_timer_elapsed(swiftkv_context* ctx, int32_t slot_begin, int32_t slot_end, float* ms);
 /* Per-kernel timing: when enabled, every launch of each kernel is bracketed
  * by events; swiftkv_profile_collect() synchronizes and returns, per kernel
- * kind (0 append, 1 split attention, 2 combine), the launch count and the
- * summed duration in ms, then clears the record. */
-#define SWIFTKV_KERNEL_APPEND 0
-#define SWIFTKV_KERNEL_ATTEND 1
-#define SWIFTKV_KERNEL_COMBINE 2
+ * kind, the launch count and the summed duration in ms, then clears the
+ * record. */
+#define SWIFTKV_KERNEL_APPEND 0  /* bulk append (prefill) */
+#define SWIFTKV_KERNEL_STEP 1    /* the step kernel: append + split scan (+ output) */
+#define SWIFTKV_KERNEL_COMBINE 2 /* split combine, launched when a head spans splits */
 #define SWIFTKV_KERNEL_KINDS 3
 int swiftkv_profile_enable(swiftkv_context* ctx, int32_t on);
 int swiftkv_profile_collect(swiftkv_context* ctx, int64_t counts[SWIFTKV_KERNEL_KINDS],

@@ -76,9 +76,13 @@ def test_config1_batch1_position127(skv, ctx, lut4096, rope_tables):
     _scenario(skv, ctx, lut4096, rope_tables, [127], seed=11)
 
 
-def test_batch_positions_edges(skv, ctx, lut4096, rope_tables):
-    _note("case: batch 6 positions [0,1,63,64,255,300], layer 1 of 3")
-    _scenario(skv, ctx, lut4096, rope_tables, [0, 1, 63, 64, 255, 300], seed=21, layers=3, layer=1, cap=320)
+@pytest.mark.parametrize("split", [256, 4096])
+def test_batch_positions_edges(skv, ctx, lut4096, rope_tables, split):
+    """Positions around block (64) and split (256) boundaries; with split 256
+    some heads finish in the step kernel and others go through the combine."""
+    _note(f"case: batch 8 positions [0,1,63,64,255,256,257,300], layer 1 of 3, split {split}")
+    _scenario(skv, ctx, lut4096, rope_tables, [0, 1, 63, 64, 255, 256, 257, 300], seed=21, layers=3, layer=1,
+              cap=320, split=split)
 
 
 def test_q17_entry(skv, ctx, lut4096, rope_tables):
@@ -86,7 +90,7 @@ def test_q17_entry(skv, ctx, lut4096, rope_tables):
     _scenario(skv, ctx, lut4096, rope_tables, [5, 200], seed=31, q17=True)
 
 
-@pytest.mark.parametrize("split", [256, 512, 1024, 0])
+@pytest.mark.parametrize("split", [256, 512, 1024, 2048, 0])
 def test_split_sizes_ragged(skv, ctx, lut4096, rope_tables, split):
     _note(f"case: ragged batch 4, split_tokens {split}")
     _scenario(skv, ctx, lut4096, rope_tables, [256, 700, 1300, 2047], seed=41, split=split)
