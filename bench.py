@@ -44,6 +44,19 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
+def profiled_traffic(batch: int, context: int):
+    """HBM bytes per step-kernel launch measured by rocprofv3 FETCH_SIZE and
+    WRITE_SIZE (each scaled by the copy-kernel calibration) for this workload,
+    from the committed summary; None when no summary covers it."""
+    path = os.path.join(REPO, "profiles", f"step_kernel_batch{batch}_ctx{context}.md")
+    if not os.path.exists(path):
+        return None, None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(float(line.split(":", 1)[1])), os.path.relpath(path, REPO)
+    return None, None
+
+
 def run_gpu(skv, ctx, batch, context, layers, steps, warmup, seed, outliers=False):
     pos = context - 1
     lut = skv.RopeLut.generate(ctx, max(context, 4096))
@@ -201,6 +214,7 @@ def main():
                                  "us_per_layer_batch1": omp["us_per_layer_batch1"]}
 
     att = main_res["kernel_avg_us"]["step"]
+    traffic, traffic_src = profiled_traffic(args.batch, args.context)
     line = {
         "metric": METRIC,
         "value": round(main_res["gbps"], 1),
@@ -225,7 +239,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(main_res["step_kernel_gbps"], 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(main_res["step_kernel_gbps"] / HBM_PEAK_GBPS, 4),
-                     "traffic": None, "kernel": "step_kernel",
+                     "traffic": traffic, "traffic_source": traffic_src, "kernel": "step_kernel",
                      "bytes_per_launch": main_res["dominant_bytes_per_launch"],
                      "avg_launch_us": round(att, 2) if att else None},
         "cpu_baseline": cpu,
