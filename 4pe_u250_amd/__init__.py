@@ -89,6 +89,10 @@ _SIGNATURES = {
     "swiftkv_memcpy_d2h": (C.c_int, [_vp, _vp, _vp, _sz]),
     "swiftkv_memset_d": (C.c_int, [_vp, _vp, C.c_int, _sz]),
     "swiftkv_convert_f32_q17": (C.c_int, [_vp, _vp, _vp, _sz]),
+    "swiftkv_capture_begin": (C.c_int, [_vp]),
+    "swiftkv_capture_end": (C.c_int, [_vp, C.POINTER(_vp)]),
+    "swiftkv_graph_launch": (C.c_int, [_vp, _vp]),
+    "swiftkv_graph_destroy": (C.c_int, [_vp]),
     "swiftkv_timer_record": (C.c_int, [_vp, _i32]),
     "swiftkv_timer_elapsed": (C.c_int, [_vp, _i32, _i32, C.POINTER(C.c_float)]),
     "swiftkv_profile_enable": (C.c_int, [_vp, _i32]),
@@ -209,6 +213,14 @@ class Context:
     def to_device(self, a: np.ndarray) -> DeviceBuffer:
         return DeviceBuffer.from_array(self, a)
 
+    def capture_begin(self) -> None:
+        _check(lib().swiftkv_capture_begin(self.handle))
+
+    def capture_end(self) -> "Graph":
+        g = C.c_void_p()
+        _check(lib().swiftkv_capture_end(self.handle, C.byref(g)))
+        return Graph(self, g.value)
+
     def timer_record(self, slot: int) -> None:
         _check(lib().swiftkv_timer_record(self.handle, slot))
 
@@ -234,6 +246,22 @@ class Context:
 
     def convert_f32_q17(self, src: DeviceBuffer, dst: DeviceBuffer, n: int) -> None:
         _check(lib().swiftkv_convert_f32_q17(self.handle, C.c_void_p(src.ptr), C.c_void_p(dst.ptr), n))
+
+
+class Graph:
+    """A recorded sequence of asynchronous calls, replayed with one launch."""
+
+    def __init__(self, ctx: Context, handle):
+        self.ctx = ctx
+        self.handle = handle
+
+    def launch(self) -> None:
+        _check(lib().swiftkv_graph_launch(self.ctx.handle, self.handle))
+
+    def close(self) -> None:
+        if self.handle:
+            _check(lib().swiftkv_graph_destroy(self.handle))
+            self.handle = None
 
 
 class RopeLut:

@@ -79,6 +79,13 @@ struct swiftkv_context {
     bool profiling = false;
     std::vector<ProfilePair> profile_pool;
     size_t profile_used = 0;
+    bool capturing = false;     // the stream is being recorded into a graph
+};
+
+struct swiftkv_graph {
+    swiftkv_context* ctx = nullptr;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
 };
 
 struct swiftkv_rope_lut {
@@ -105,11 +112,20 @@ int set_device(const swiftkv_context* ctx) {
     return SWIFTKV_OK;
 }
 
+// Entry points that synchronize, copy, allocate or memset cannot be recorded.
+int not_capturing(const swiftkv_context* ctx, const char* what) {
+    if (ctx && ctx->capturing) return fail(SWIFTKV_ESTATE, "%s is not allowed during graph capture", what);
+    return SWIFTKV_OK;
+}
+
 // Device buffer growth.  The old buffer may still be read by queued kernels,
 // so the stream is drained before it is released.
 template <typename T>
 int ensure(swiftkv_context* ctx, T*& ptr, size_t& have, size_t need) {
     if (need <= have) return SWIFTKV_OK;
+    if (ctx->capturing)
+        return fail(SWIFTKV_ESTATE, "split workspace too small during graph capture (%zu < %zu bytes): run the "
+                    "call once before capturing", have * sizeof(T), need * sizeof(T));
     if (ptr) {
         SKV_HIP(hipStreamSynchronize(ctx->stream));
         SKV_HIP(hipFree(ptr));
@@ -216,7 +232,7 @@ int validate_step(swiftkv_context* ctx, const void* q, const void* k, const void
 }
 
 ProfilePair* profile_begin(swiftkv_context* ctx, int kind) {
-    if (!ctx->profiling || ctx->profile_used >= ctx->profile_pool.size()) return nullptr;
+    if (!ctx->profiling || ctx->capturing || ctx->profile_used >= ctx->profile_pool.size()) return nullptr;
     ProfilePair* p = &ctx->profile_pool[ctx->profile_used++];
     p->kind = kind;
     if (hipEventRecord(p->begin, ctx->stream) != hipSuccess) return nullptr;
@@ -336,6 +352,11 @@ int swiftkv_context_create(int device, swiftkv_context** out) {
 
 int swiftkv_context_destroy(swiftkv_context* ctx) {
     if (!ctx) return ok();
+    if (ctx->capturing) {   // abandon the recording so the stream can be released
+        hipGraph_t g = nullptr;
+        if (hipStreamEndCapture(ctx->stream, &g) == hipSuccess && g) (void)hipGraphDestroy(g);
+        ctx->capturing = false;
+    }
     (void)hipSetDevice(ctx->device);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     if (ctx->partials) (void)hipFree(ctx->partials);
@@ -352,7 +373,9 @@ int swiftkv_context_destroy(swiftkv_context* ctx) {
 
 int swiftkv_synchronize(swiftkv_context* ctx) {
     if (!ctx) return fail(SWIFTKV_EINVAL, "null context");
-    int rc = set_device(ctx);
+    int rc = not_capturing(ctx, "swiftkv_synchronize");
+    if (rc) return rc;
+    rc = set_device(ctx);
     if (rc) return rc;
     SKV_HIP(hipStreamSynchronize(ctx->stream));
     return ok();
@@ -373,6 +396,7 @@ int swiftkv_set_split_tokens(swiftkv_context* ctx, int32_t split_tokens) {
 int swiftkv_rope_lut_load(swiftkv_context* ctx, const void* image, size_t image_bytes, swiftkv_rope_lut** out) {
     if (!ctx || !image || !out) return fail(SWIFTKV_EINVAL, "null argument");
     *out = nullptr;
+    if (int rc0 = not_capturing(ctx, "swiftkv_rope_lut_load")) return rc0;
     if (image_bytes == 0 || image_bytes % SWIFTKV_ROPE_LUT_BYTES_PER_POSITION != 0)
         return fail(SWIFTKV_EINVAL, "RoPE image of %zu bytes is not a whole number of %d-byte positions",
                     image_bytes, SWIFTKV_ROPE_LUT_BYTES_PER_POSITION);
@@ -396,6 +420,7 @@ int swiftkv_rope_lut_load(swiftkv_context* ctx, const void* image, size_t image_
 int swiftkv_rope_lut_generate(swiftkv_context* ctx, int32_t positions, double theta, swiftkv_rope_lut** out) {
     if (!ctx || !out) return fail(SWIFTKV_EINVAL, "null argument");
     *out = nullptr;
+    if (int rc0 = not_capturing(ctx, "swiftkv_rope_lut_generate")) return rc0;
     if (positions < 1 || positions > SWIFTKV_MAX_SEQ)
         return fail(SWIFTKV_ERANGE, "positions %d outside [1, %d]", positions, SWIFTKV_MAX_SEQ);
     if (!(theta > 1.0) || !std::isfinite(theta)) return fail(SWIFTKV_EINVAL, "theta must be finite and > 1");
@@ -413,6 +438,7 @@ int swiftkv_rope_lut_generate(swiftkv_context* ctx, int32_t positions, double th
 
 int swiftkv_rope_lut_destroy(swiftkv_rope_lut* lut) {
     if (!lut) return ok();
+    if (int rc = not_capturing(lut->ctx, "swiftkv_rope_lut_destroy")) return rc;
     (void)hipSetDevice(lut->ctx->device);
     (void)hipStreamSynchronize(lut->ctx->stream);
     if (lut->table) (void)hipFree(lut->table);
@@ -445,6 +471,7 @@ int swiftkv_kv_cache_create(swiftkv_context* ctx, int32_t layers, int32_t max_ba
                             swiftkv_kv_cache** out) {
     if (!ctx || !out) return fail(SWIFTKV_EINVAL, "null argument");
     *out = nullptr;
+    if (int rc0 = not_capturing(ctx, "swiftkv_kv_cache_create")) return rc0;
     if (layers < 1 || layers > 64) return fail(SWIFTKV_EINVAL, "layers %d outside [1, 64]", layers);
     if (max_batch < 1 || max_batch > 4096) return fail(SWIFTKV_EINVAL, "max_batch %d outside [1, 4096]", max_batch);
     if (max_seq_len < 1 || max_seq_len > SWIFTKV_MAX_SEQ)
@@ -478,6 +505,7 @@ int swiftkv_kv_cache_create(swiftkv_context* ctx, int32_t layers, int32_t max_ba
 
 int swiftkv_kv_cache_destroy(swiftkv_kv_cache* kv) {
     if (!kv) return ok();
+    if (int rc = not_capturing(kv->ctx, "swiftkv_kv_cache_destroy")) return rc;
     (void)hipSetDevice(kv->ctx->device);
     (void)hipStreamSynchronize(kv->ctx->stream);
     if (kv->base) (void)hipFree(kv->base);
@@ -487,7 +515,9 @@ int swiftkv_kv_cache_destroy(swiftkv_kv_cache* kv) {
 
 int swiftkv_kv_cache_zero(swiftkv_context* ctx, swiftkv_kv_cache* kv) {
     if (!ctx || !kv || kv->ctx != ctx) return fail(SWIFTKV_EINVAL, "null or foreign argument");
-    int rc = set_device(ctx);
+    int rc = not_capturing(ctx, "swiftkv_kv_cache_zero");
+    if (rc) return rc;
+    rc = set_device(ctx);
     if (rc) return rc;
     SKV_HIP(hipMemsetAsync(kv->base, 0, kv->bytes, ctx->stream));
     return ok();
@@ -500,6 +530,7 @@ int swiftkv_kv_cache_read(swiftkv_context* ctx, const swiftkv_kv_cache* kv, int3
                           float* k_scales, float* v_scales) {
     int rc = check_cache_range(ctx, kv, seq, layer, head, tok0, n);
     if (rc) return rc;
+    if ((rc = not_capturing(ctx, "swiftkv_kv_cache_read"))) return rc;
     if ((rc = set_device(ctx))) return rc;
     if (n == 0) return ok();
     const int8_t* page = page_ptr(CacheView{kv->base, kv->page_bytes, kv->seq_cap, kv->layers}, seq, layer, head);
@@ -555,6 +586,7 @@ int swiftkv_kv_cache_import_records(swiftkv_context* ctx, swiftkv_kv_cache* kv, 
     int rc = check_cache_range(ctx, kv, seq, layer, head, tok0, n);
     if (rc) return rc;
     if (!records && n > 0) return fail(SWIFTKV_EINVAL, "null records");
+    if ((rc = not_capturing(ctx, "swiftkv_kv_cache_import_records"))) return rc;
     if ((rc = set_device(ctx))) return rc;
     if (n == 0) return ok();
     const uint8_t* in = static_cast<const uint8_t*>(records);
@@ -673,7 +705,9 @@ int swiftkv_kv_cache_fill_synthetic(swiftkv_context* ctx, swiftkv_kv_cache* kv, 
 int swiftkv_device_alloc(swiftkv_context* ctx, size_t bytes, void** out) {
     if (!ctx || !out) return fail(SWIFTKV_EINVAL, "null argument");
     *out = nullptr;
-    int rc = set_device(ctx);
+    int rc = not_capturing(ctx, "swiftkv_device_alloc");
+    if (rc) return rc;
+    rc = set_device(ctx);
     if (rc) return rc;
     if (hipMalloc(out, bytes ? bytes : 1) != hipSuccess) return fail(SWIFTKV_ENOMEM, "hipMalloc of %zu bytes failed", bytes);
     return ok();
@@ -682,7 +716,9 @@ int swiftkv_device_alloc(swiftkv_context* ctx, size_t bytes, void** out) {
 int swiftkv_device_free(swiftkv_context* ctx, void* ptr) {
     if (!ctx) return fail(SWIFTKV_EINVAL, "null context");
     if (!ptr) return ok();
-    int rc = set_device(ctx);
+    int rc = not_capturing(ctx, "swiftkv_device_free");
+    if (rc) return rc;
+    rc = set_device(ctx);
     if (rc) return rc;
     SKV_HIP(hipStreamSynchronize(ctx->stream));
     SKV_HIP(hipFree(ptr));
@@ -691,7 +727,9 @@ int swiftkv_device_free(swiftkv_context* ctx, void* ptr) {
 
 int swiftkv_memcpy_h2d(swiftkv_context* ctx, void* dst, const void* src, size_t bytes) {
     if (!ctx || (bytes && (!dst || !src))) return fail(SWIFTKV_EINVAL, "null argument");
-    int rc = set_device(ctx);
+    int rc = not_capturing(ctx, "swiftkv_memcpy_h2d");
+    if (rc) return rc;
+    rc = set_device(ctx);
     if (rc) return rc;
     SKV_HIP(hipStreamSynchronize(ctx->stream));
     if (bytes) SKV_HIP(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
@@ -700,7 +738,9 @@ int swiftkv_memcpy_h2d(swiftkv_context* ctx, void* dst, const void* src, size_t 
 
 int swiftkv_memcpy_d2h(swiftkv_context* ctx, void* dst, const void* src, size_t bytes) {
     if (!ctx || (bytes && (!dst || !src))) return fail(SWIFTKV_EINVAL, "null argument");
-    int rc = set_device(ctx);
+    int rc = not_capturing(ctx, "swiftkv_memcpy_d2h");
+    if (rc) return rc;
+    rc = set_device(ctx);
     if (rc) return rc;
     SKV_HIP(hipStreamSynchronize(ctx->stream));
     if (bytes) SKV_HIP(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
@@ -709,7 +749,9 @@ int swiftkv_memcpy_d2h(swiftkv_context* ctx, void* dst, const void* src, size_t 
 
 int swiftkv_memset_d(swiftkv_context* ctx, void* dst, int value, size_t bytes) {
     if (!ctx || (bytes && !dst)) return fail(SWIFTKV_EINVAL, "null argument");
-    int rc = set_device(ctx);
+    int rc = not_capturing(ctx, "swiftkv_memset_d");
+    if (rc) return rc;
+    rc = set_device(ctx);
     if (rc) return rc;
     if (bytes) SKV_HIP(hipMemsetAsync(dst, value, bytes, ctx->stream));
     return ok();
@@ -723,12 +765,75 @@ int swiftkv_convert_f32_q17(swiftkv_context* ctx, const float* in, int32_t* out,
     return ok();
 }
 
+// ---------------------------------------------------------------- graphs
+
+int swiftkv_capture_begin(swiftkv_context* ctx) {
+    if (!ctx) return fail(SWIFTKV_EINVAL, "null context");
+    if (ctx->capturing) return fail(SWIFTKV_ESTATE, "a capture is already in progress");
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    SKV_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    ctx->capturing = true;
+    return ok();
+}
+
+int swiftkv_capture_end(swiftkv_context* ctx, swiftkv_graph** out) {
+    if (!ctx || !out) return fail(SWIFTKV_EINVAL, "null argument");
+    *out = nullptr;
+    if (!ctx->capturing) return fail(SWIFTKV_ESTATE, "no capture in progress");
+    ctx->capturing = false;
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    hipGraph_t graph = nullptr;
+    SKV_HIP(hipStreamEndCapture(ctx->stream, &graph));
+    hipGraphExec_t exec = nullptr;
+    hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(graph);
+        return fail(SWIFTKV_EHIP, "hipGraphInstantiate: %s", hipGetErrorString(e));
+    }
+    swiftkv_graph* g = new (std::nothrow) swiftkv_graph();
+    if (!g) {
+        (void)hipGraphExecDestroy(exec);
+        (void)hipGraphDestroy(graph);
+        return fail(SWIFTKV_ENOMEM, "out of host memory");
+    }
+    g->ctx = ctx;
+    g->graph = graph;
+    g->exec = exec;
+    *out = g;
+    return ok();
+}
+
+int swiftkv_graph_launch(swiftkv_context* ctx, const swiftkv_graph* graph) {
+    if (!ctx || !graph) return fail(SWIFTKV_EINVAL, "null argument");
+    if (graph->ctx != ctx) return fail(SWIFTKV_EINVAL, "graph belongs to another context");
+    int rc = not_capturing(ctx, "swiftkv_graph_launch");
+    if (rc) return rc;
+    if ((rc = set_device(ctx))) return rc;
+    SKV_HIP(hipGraphLaunch(graph->exec, ctx->stream));
+    return ok();
+}
+
+int swiftkv_graph_destroy(swiftkv_graph* graph) {
+    if (!graph) return ok();
+    if (int rc = not_capturing(graph->ctx, "swiftkv_graph_destroy")) return rc;
+    (void)hipSetDevice(graph->ctx->device);
+    (void)hipStreamSynchronize(graph->ctx->stream);
+    if (graph->exec) (void)hipGraphExecDestroy(graph->exec);
+    if (graph->graph) (void)hipGraphDestroy(graph->graph);
+    delete graph;
+    return ok();
+}
+
 // ---------------------------------------------------------------- timing
 
 int swiftkv_timer_record(swiftkv_context* ctx, int32_t slot) {
     if (!ctx) return fail(SWIFTKV_EINVAL, "null context");
     if (slot < 0 || slot >= kTimerSlots) return fail(SWIFTKV_ERANGE, "timer slot %d outside [0, %d)", slot, kTimerSlots);
-    int rc = set_device(ctx);
+    int rc = not_capturing(ctx, "swiftkv_timer_record");
+    if (rc) return rc;
+    rc = set_device(ctx);
     if (rc) return rc;
     SKV_HIP(hipEventRecord(ctx->timers[slot], ctx->stream));
     return ok();
@@ -738,7 +843,9 @@ int swiftkv_timer_elapsed(swiftkv_context* ctx, int32_t slot_begin, int32_t slot
     if (!ctx || !ms) return fail(SWIFTKV_EINVAL, "null argument");
     if (slot_begin < 0 || slot_begin >= kTimerSlots || slot_end < 0 || slot_end >= kTimerSlots)
         return fail(SWIFTKV_ERANGE, "timer slot outside [0, %d)", kTimerSlots);
-    int rc = set_device(ctx);
+    int rc = not_capturing(ctx, "swiftkv_timer_elapsed");
+    if (rc) return rc;
+    rc = set_device(ctx);
     if (rc) return rc;
     SKV_HIP(hipEventSynchronize(ctx->timers[slot_end]));
     SKV_HIP(hipEventElapsedTime(ms, ctx->timers[slot_begin], ctx->timers[slot_end]));
@@ -764,7 +871,9 @@ int swiftkv_profile_enable(swiftkv_context* ctx, int32_t on) {
 int swiftkv_profile_collect(swiftkv_context* ctx, int64_t counts[SWIFTKV_KERNEL_KINDS],
                             double ms[SWIFTKV_KERNEL_KINDS]) {
     if (!ctx || !counts || !ms) return fail(SWIFTKV_EINVAL, "null argument");
-    int rc = set_device(ctx);
+    int rc = not_capturing(ctx, "swiftkv_profile_collect");
+    if (rc) return rc;
+    rc = set_device(ctx);
     if (rc) return rc;
     for (int i = 0; i < SWIFTKV_KERNEL_KINDS; ++i) {
         counts[i] = 0;

@@ -114,33 +114,42 @@ __device__ __forceinline__ PageReader make_reader(const int8_t* page, int64_t ca
     return pr;
 }
 
-// One 64-token block [t0, t0+64) of the scan; MASKED blocks drop tokens >= t_stop.
-template <bool MASKED>
-__device__ __forceinline__ void scan_block(const PageReader& pr, const float* qf, int t0, int t_stop, int r,
-                                           float& m_run, float& l_run, float* acc) {
-    v4i kw[8], vw[8];
-    v2f sw[8];
+// The 24 loads of one 64-token block: 8 x 16 B of K codes, 8 x 8 B of scale
+// pairs, 8 x 16 B of V codes per lane.
+struct BlockLoads {
+    v4i k[8], v[8];
+    v2f s[8];
+};
+
+__device__ __forceinline__ void issue_block(const PageReader& pr, int t0, BlockLoads& bl) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         const int32_t tok = t0 + 8 * i;
-        kw[i] = __builtin_amdgcn_raw_buffer_load_b128(pr.rsrc, pr.k_lane, tok * kCodeBytes, kNontemporal);
-        sw[i] = __builtin_bit_cast(v2f, __builtin_amdgcn_raw_buffer_load_b64(pr.rsrc, pr.s_lane, tok * kScaleBytes,
-                                                                              kNontemporal));
+        bl.k[i] = __builtin_amdgcn_raw_buffer_load_b128(pr.rsrc, pr.k_lane, tok * kCodeBytes, kNontemporal);
+        bl.s[i] = __builtin_bit_cast(v2f, __builtin_amdgcn_raw_buffer_load_b64(pr.rsrc, pr.s_lane,
+                                                                                tok * kScaleBytes, kNontemporal));
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         const int32_t tok = t0 + 8 * i;
-        vw[i] = __builtin_amdgcn_raw_buffer_load_b128(pr.rsrc, pr.v_lane, tok * kCodeBytes, kNontemporal);
+        bl.v[i] = __builtin_amdgcn_raw_buffer_load_b128(pr.rsrc, pr.v_lane, tok * kCodeBytes, kNontemporal);
     }
-    // Keep all 24 loads of the block in flight before any math: without this
-    // fence the scheduler sinks V loads next to their uses (to save VGPRs) and
+    // Keep all 24 loads in flight before any math: without this fence the
+    // scheduler sinks V loads next to their uses (to save VGPRs) and
     // serializes them at full memory latency.
     __builtin_amdgcn_sched_barrier(0);
+}
+
+// Online-softmax update with one block [t0, t0+64); MASKED blocks drop
+// tokens >= t_stop.
+template <bool MASKED>
+__device__ __forceinline__ void consume_block(const BlockLoads& bl, const float* qf, int t0, int t_stop, int r,
+                                              float& m_run, float& l_run, float* acc) {
     float s[8];
     float blk = -INFINITY;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        s[i] = octet_sum(dot16(qf, kw[i]) * sw[i][0]);
+        s[i] = octet_sum(dot16(qf, bl.k[i]) * bl.s[i][0]);
         if (MASKED && t0 + 8 * i + r >= t_stop) s[i] = -INFINITY;
         blk = fmaxf(blk, s[i]);
     }
@@ -154,24 +163,36 @@ __device__ __forceinline__ void scan_block(const PageReader& pr, const float* qf
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         float p = fast_exp2(s[i] - m_new);            // masked: 2^-inf = 0
-        float w = p * sw[i][1];
+        float w = p * bl.s[i][1];
         if (MASKED && t0 + 8 * i + r >= t_stop) w = 0.0f;   // never multiply a stale scale
         l_run += p;
-        axpy16(acc, w, vw[i]);
+        axpy16(acc, w, bl.v[i]);
     }
 }
 
-// One wave's online-softmax scan over the 64-token blocks starting at t0,
-// t0+stride, ... below t_stop, lane layout (c, r).  On return every lane
-// holds the wave's (m, l) and, for its chunk c, acc[16] summed over the rows.
-__device__ __forceinline__ void scan_range(const PageReader& pr, const float* qf, int t0, int t_stop, int stride,
-                                           int r, float& m_run, float& l_run, float* acc) {
+// One wave's online-softmax scan over the 64-token blocks t0, t0+stride, ...
+// below t_stop, lane layout (c, r); the caller has already issued the loads
+// of the first block into `bl` (so its prologue overlaps them).  On return
+// every lane holds the wave's (m, l) and, for its chunk c, acc[16] summed
+// over the 8 rows.
+__device__ __forceinline__ void scan_range(const PageReader& pr, BlockLoads& bl, const float* qf, int t0,
+                                           int t_stop, int stride, int r, float& m_run, float& l_run,
+                                           float* acc) {
     m_run = -INFINITY;
     l_run = 0.0f;
 #pragma unroll
     for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
-    for (; t0 + kBlockTokens <= t_stop; t0 += stride) scan_block<false>(pr, qf, t0, t_stop, r, m_run, l_run, acc);
-    if (t0 < t_stop) scan_block<true>(pr, qf, t0, t_stop, r, m_run, l_run, acc);
+    // Full blocks, then at most one partial tail block.  (Both variants in one
+    // loop body would double the live VGPRs.)
+    bool first = true;
+    for (; t0 + kBlockTokens <= t_stop; t0 += stride, first = false) {
+        if (!first) issue_block(pr, t0, bl);
+        consume_block<false>(bl, qf, t0, t_stop, r, m_run, l_run, acc);
+    }
+    if (t0 < t_stop) {
+        if (!first) issue_block(pr, t0, bl);
+        consume_block<true>(bl, qf, t0, t_stop, r, m_run, l_run, acc);
+    }
     l_run = across_octets_sum(l_run);
 #pragma unroll
     for (int j = 0; j < 16; ++j) acc[j] = across_octets_sum(acc[j]);
@@ -270,13 +291,25 @@ __global__ __launch_bounds__(kAttendWaves * 64) void step_kernel(StepArgs a) {
     const int nsplit = (len + C - 1) / C;
     const bool owner = pos < t_end;               // this split holds the new token
 
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    // wave index made provably uniform so token offsets stay in SGPRs (the
+    // buffer loads' soffset operand) instead of forcing waterfall loops
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int lane = threadIdx.x & 63;
     const int c = lane & 7, r = lane >> 3;
     int8_t* page = page_ptr(a.kv, a.slot0 + b, a.layer, h);
     const int64_t cap = a.kv.seq_cap;
 
     __shared__ float s_acc[kAttendWaves + 1][kHeadDim];
     __shared__ float s_m[kAttendWaves + 1], s_l[kAttendWaves + 1];
+
+    // First block's loads go out before anything else, so the query rotation
+    // and the new row overlap their latency.  The new token is excluded from
+    // the scan (it is forwarded below).
+    const PageReader pr = make_reader(page, cap, c, r);
+    const int t_first = t_begin + wave * kBlockTokens;
+    const int t_stop = owner ? pos : t_end;
+    BlockLoads bl;
+    if (t_first < t_stop) issue_block(pr, t_first, bl);
 
     // The new row: convert, rotate k, quantize, append; forward (k^ . q', v^).
     if (owner && wave == 0) {
@@ -302,12 +335,10 @@ __global__ __launch_bounds__(kAttendWaves * 64) void step_kernel(StepArgs a) {
         }
     }
 
-    // Scan of the cached tokens of this split (the new token excluded).
     float qf[16];
     query_chunk<Q17>(a, b, h, c, pos, qf);
     float m_run, l_run, acc[16];
-    scan_range(make_reader(page, cap, c, r), qf, t_begin + wave * kBlockTokens, owner ? pos : t_end,
-               kAttendWaves * kBlockTokens, r, m_run, l_run, acc);
+    scan_range(pr, bl, qf, t_first, t_stop, kAttendWaves * kBlockTokens, r, m_run, l_run, acc);
     if (r == 0) {
 #pragma unroll
         for (int j = 0; j < 16; ++j) s_acc[wave][c * 16 + j] = acc[j];

@@ -93,6 +93,19 @@ def run_gpu(skv, ctx, batch, context, layers, steps, warmup, seed, outliers=Fals
     ms = ctx.timer_elapsed_ms(0, 1)
     counts, kms = ctx.profile_collect()
     ctx.profile(False)
+    # The same step recorded once into a HIP graph and replayed: the GPU-side
+    # time of the 32 per-layer calls without host launch overhead.
+    ctx.capture_begin()
+    one_step()
+    graph = ctx.capture_end()
+    for _ in range(warmup):
+        graph.launch()
+    ctx.timer_record(2)
+    for _ in range(steps):
+        graph.launch()
+    ctx.timer_record(3)
+    ms_graph = ctx.timer_elapsed_ms(2, 3)
+    graph.close()
     o = out.download(np.float32, (batch, 4096))
     assert np.isfinite(o).all(), "non-finite attention output"
     for b in qkv + [out, aq, asc]:
@@ -111,6 +124,10 @@ def run_gpu(skv, ctx, batch, context, layers, steps, warmup, seed, outliers=Fals
                           for k, t, c in zip(["append", "step", "combine"], kms, counts)},
     }
     res["pct_of_peak"] = 100.0 * res["gbps"] / HBM_PEAK_GBPS
+    res["graph"] = {"us_per_layer": 1000.0 * ms_graph / steps / layers,
+                    "gbps": total_bytes / (ms_graph / 1e3) / 1e9,
+                    "tokens_per_s": batch * steps / (ms_graph / 1e3)}
+    res["graph"]["pct_of_peak"] = 100.0 * res["graph"]["gbps"] / HBM_PEAK_GBPS
     # dominant kernel: the step kernel moves the whole step's algorithmic bytes
     # (cached tokens, appended row, q/k/v in, output out)
     step_avg_s = kms[1] / counts[1] / 1e3
@@ -196,11 +213,13 @@ def main():
     ctx.set_split_tokens(args.split)
     log(f"[bench] {skv.version()}")
     main_res = run_gpu(skv, ctx, args.batch, args.context, args.layers, args.steps, args.warmup, seed=2026)
-    log(f"[bench] batch {args.batch}: {main_res['us_per_layer']:.1f} us/layer, {main_res['gbps']:.0f} GB/s")
+    log(f"[bench] batch {args.batch}: {main_res['us_per_layer']:.1f} us/layer, {main_res['gbps']:.0f} GB/s "
+        f"(graph replay {main_res['graph']['us_per_layer']:.1f} us/layer)")
     b1 = None
     if not args.no_batch1:
         b1 = run_gpu(skv, ctx, 1, args.context, args.layers, max(args.steps, 20), args.warmup, seed=2027)
-        log(f"[bench] batch 1: {b1['us_per_layer']:.2f} us/layer, {b1['gbps']:.0f} GB/s")
+        log(f"[bench] batch 1: {b1['us_per_layer']:.2f} us/layer, {b1['gbps']:.0f} GB/s "
+            f"(graph replay {b1['graph']['us_per_layer']:.2f} us/layer)")
     ctx.close()
 
     cpu = None
@@ -236,6 +255,7 @@ def main():
         "tokens_per_s": round(main_res["tokens_per_s"], 1),
         "pct_of_peak": round(main_res["pct_of_peak"], 2),
         "kernel_avg_us": {k: (round(v, 2) if v else v) for k, v in main_res["kernel_avg_us"].items()},
+        "graph_replay": {k: round(v, 2) for k, v in main_res["graph"].items()},
         "roofline": {"bound": "hbm", "achieved": round(main_res["step_kernel_gbps"], 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(main_res["step_kernel_gbps"] / HBM_PEAK_GBPS, 4),
@@ -247,7 +267,8 @@ def main():
     if b1:
         line["batch1"] = {"us_per_layer": round(b1["us_per_layer"], 3), "gbps": round(b1["gbps"], 1),
                           "pct_of_peak": round(b1["pct_of_peak"], 2), "tokens_per_s": round(b1["tokens_per_s"], 1),
-                          "kernel_avg_us": {k: (round(v, 2) if v else v) for k, v in b1["kernel_avg_us"].items()}}
+                          "kernel_avg_us": {k: (round(v, 2) if v else v) for k, v in b1["kernel_avg_us"].items()},
+                          "graph_replay": {k: round(v, 3) for k, v in b1["graph"].items()}}
     print(json.dumps(line), flush=True)
 
 

@@ -69,6 +69,7 @@ extern "C" {
 typedef struct swiftkv_context swiftkv_context;
 typedef struct swiftkv_kv_cache swiftkv_kv_cache;
 typedef struct swiftkv_rope_lut swiftkv_rope_lut;
+typedef struct swiftkv_graph swiftkv_graph;
 
 /* Thread-local description of the last failure ("" after success). */
 const char* swiftkv_last_error(void);
@@ -206,6 +207,20 @@ int swiftkv_memset_d(swiftkv_context* ctx, void* dst, int value, size_t bytes);
 /* Elementwise FP32 -> Q15.17 on the device (the conversion of step 1),
  * n elements, device pointers.  Exposed for exhaustive conversion tests. */
 int swiftkv_convert_f32_q17(swiftkv_context* ctx, const float* in, int32_t* out, size_t n);
+
+/* --------------------------------------------------------------------------
+ * HIP graphs: record a sequence of asynchronous calls (steps, appends,
+ * synthetic fills) once and replay it with one launch, e.g. the 32 per-layer
+ * calls of a decode step.  The recording keeps every argument, including the
+ * positions, so a replay repeats exactly the recorded work.  Run each
+ * recorded call once outside capture first: the split workspace must already
+ * be large enough.  While capturing, calls that synchronize, copy, allocate
+ * or memset return SWIFTKV_ESTATE.
+ * ------------------------------------------------------------------------ */
+int swiftkv_capture_begin(swiftkv_context* ctx);
+int swiftkv_capture_end(swiftkv_context* ctx, swiftkv_graph** out);
+int swiftkv_graph_launch(swiftkv_context* ctx, const swiftkv_graph* graph);
+int swiftkv_graph_destroy(swiftkv_graph* graph);
 
 /* --------------------------------------------------------------------------
  * Timing (hipEvents on the context stream).  Stands in for the host's
