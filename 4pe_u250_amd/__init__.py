@@ -43,7 +43,8 @@ TOKEN_BYTES = 288          # algorithmic bytes per cached token-head: 2 x 128 co
 
 OK, EINVAL, ERANGE, EHIP, ENOMEM, ESTATE = 0, -1, -2, -3, -4, -5
 DIST_NORMAL, DIST_STUDENT_T3 = 0, 1
-KERNEL_APPEND, KERNEL_STEP, KERNEL_COMBINE = 0, 1, 2
+KERNEL_APPEND, KERNEL_STEP = 0, 1
+KERNEL_KINDS = 2
 _STATUS_NAMES = {EINVAL: "EINVAL", ERANGE: "ERANGE", EHIP: "EHIP", ENOMEM: "ENOMEM", ESTATE: "ESTATE"}
 
 
@@ -233,8 +234,8 @@ class Context:
         _check(lib().swiftkv_profile_enable(self.handle, 1 if on else 0))
 
     def profile_collect(self):
-        counts = (C.c_int64 * 3)()
-        ms = (C.c_double * 3)()
+        counts = (C.c_int64 * KERNEL_KINDS)()
+        ms = (C.c_double * KERNEL_KINDS)()
         _check(lib().swiftkv_profile_collect(self.handle, counts, ms))
         return list(counts), list(ms)
 

@@ -74,6 +74,7 @@ struct swiftkv_context {
     // split-context workspace
     float* partials = nullptr;
     size_t partial_elems = 0;
+    uint32_t* counters = nullptr;   // [kMaxBatchPerLaunch][32] split arrivals, zero between launches
     // timing
     hipEvent_t timers[kTimerSlots] = {};
     bool profiling = false;
@@ -193,10 +194,10 @@ int upload_lut(swiftkv_context* ctx, std::vector<int2>&& host, int32_t positions
 
 // Tokens per split.  Aim for about 2048 workgroups (a few residency rounds on
 // 256 CUs): split a head only when batch x 32 heads is below that, and never
-// below one 256-token quantum.  A head held by one split needs no combine
-// launch, which is worth more than the finer tail of smaller splits (batch
-// 64 at context 4096: one split per head runs 378 us/layer, 1024-token
-// splits 385 us/layer including their combine).
+// below one 256-token quantum.  A head held by one split skips the partial
+// exchange, which is worth more than the finer tail of smaller splits (batch
+// 64 at context 4096: one split per head ran 378 us/layer, 1024-token splits
+// 385 us/layer including their merge).
 int32_t choose_split(const swiftkv_context* ctx, const int32_t* positions, int32_t batch) {
     if (ctx->split_tokens > 0) return ctx->split_tokens;
     int32_t max_len = 1;
@@ -276,6 +277,7 @@ int run_step(swiftkv_context* ctx, const void* q, const void* k, const void* v, 
                          static_cast<size_t>(nb) * kHeads * grid_splits * kPartialStride)))
             return rc;
         a.partials = ctx->partials;
+        a.counters = ctx->counters;
         a.out = out + row0;
         a.act_q = act_q ? act_q + static_cast<size_t>(b0) * kHeads * kGroupsPerHead * SWIFTKV_A14_WORD_BYTES
                         : nullptr;
@@ -284,11 +286,6 @@ int run_step(swiftkv_context* ctx, const void* q, const void* k, const void* v, 
         ProfilePair* p = profile_begin(ctx, SWIFTKV_KERNEL_STEP);
         SKV_HIP(launch_step(a, grid_splits, q17, ctx->stream));
         profile_end(ctx, p);
-        if (grid_splits > 1) {   // some head spans several splits
-            p = profile_begin(ctx, SWIFTKV_KERNEL_COMBINE);
-            SKV_HIP(launch_combine(a, ctx->stream));
-            profile_end(ctx, p);
-        }
     }
     return ok();
 }
@@ -342,6 +339,9 @@ int swiftkv_context_create(int device, swiftkv_context** out) {
     ctx->device = device;
     hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
     for (int i = 0; e == hipSuccess && i < kTimerSlots; ++i) e = hipEventCreate(&ctx->timers[i]);
+    const size_t counter_bytes = sizeof(uint32_t) * kMaxBatchPerLaunch * kHeads;
+    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&ctx->counters), counter_bytes);
+    if (e == hipSuccess) e = hipMemset(ctx->counters, 0, counter_bytes);
     if (e != hipSuccess) {
         swiftkv_context_destroy(ctx);
         return fail(SWIFTKV_EHIP, "stream/event creation: %s", hipGetErrorString(e));
@@ -360,6 +360,7 @@ int swiftkv_context_destroy(swiftkv_context* ctx) {
     (void)hipSetDevice(ctx->device);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     if (ctx->partials) (void)hipFree(ctx->partials);
+    if (ctx->counters) (void)hipFree(ctx->counters);
     for (auto& t : ctx->timers)
         if (t) (void)hipEventDestroy(t);
     for (auto& p : ctx->profile_pool) {

@@ -63,6 +63,7 @@ struct StepArgs {
     int32_t split_tokens;     // multiple of kSplitQuantum
     int32_t max_splits;       // partial slots per (sequence, head)
     float* partials;          // [batch][32][max_splits][kPartialStride]
+    uint32_t* counters;       // [batch][32] split arrivals, zero between launches
     float* out;               // [batch][4096]
     uint8_t* act_q;           // [batch][128][56] or null
     uint8_t* act_scale;       // [batch][128] or null
@@ -84,7 +85,6 @@ struct BulkArgs {
 
 // Launchers (swiftkv_kernels.hip).
 hipError_t launch_step(const StepArgs& a, int grid_splits, bool q17, hipStream_t s);
-hipError_t launch_combine(const StepArgs& a, hipStream_t s);
 hipError_t launch_append_bulk(const BulkArgs& a, bool q17, hipStream_t s);
 hipError_t launch_convert(const float* in, int32_t* out, size_t n, hipStream_t s);
 // Synthetic inputs (swiftkv_synth.hip).

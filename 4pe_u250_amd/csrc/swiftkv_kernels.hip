@@ -17,10 +17,9 @@
 //      chunk lanes with DPP, the running (max, sum, acc) stays in VGPRs;
 //   4. waves (plus the forwarded row) merge through LDS;
 //   5. a head held by one split is finished in place (FP32 output and the
-//      optional A14/E8M0 words); otherwise the split stores its partial
-//      (m, l, acc[128]).
-// combine kernel (only when some head spans several splits): log-sum-exp
-// merge of the partials of each (sequence, head), then the same epilogue.
+//      optional A14/E8M0 words); otherwise each split publishes its partial
+//      (m, l, acc[128]) and the last split of the head to arrive merges them
+//      (log-sum-exp) and finishes the head.
 //
 // No MFMA: q_len = 1 multi-head attention is a memory-bound GEMV.
 #include "swiftkv_device.hpp"
@@ -30,7 +29,7 @@ namespace {
 
 using namespace dev;
 
-static_assert(kMaxSplits <= kHeadDim, "one combine thread per split statistic");
+static_assert(kMaxSplits <= kHeadDim, "one merge thread per split statistic");
 
 // Scores are kept in the log2 domain: the query is pre-scaled by
 // 1/sqrt(128) * log2(e) so the softmax uses v_exp_f32 (2^x) directly.
@@ -242,6 +241,19 @@ __device__ __forceinline__ void finalize_head(const StepArgs& a, int b, int h, f
     }
 }
 
+// Split partials are exchanged through device memory inside one launch.
+// Writers publish with agent-scope atomic stores (write-through to the
+// device coherence point, no dirty L2 lines) and wait for their completion;
+// the last split of a head, identified by a device-scope counter, reads them
+// back with agent-scope atomic loads.  No L2 writeback or invalidation is
+// needed on either side.
+__device__ __forceinline__ void publish(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float fetch(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Log-sum-exp merge of n split partials; threads d < 128 get output channel d.
 // Split statistics are fetched in parallel (thread j loads split j), so the
 // merge costs two dependent memory round trips whatever n is.
@@ -250,8 +262,8 @@ __device__ __forceinline__ float merge_partials(const float* part, int n) {
     __shared__ float s_m[kMaxSplits], s_l[kMaxSplits], s_w[kMaxSplits];
     __shared__ float s_mx, s_den;
     if (d < n) {
-        s_m[d] = part[d * kPartialStride];
-        s_l[d] = part[d * kPartialStride + 1];
+        s_m[d] = fetch(part + d * kPartialStride);
+        s_l[d] = fetch(part + d * kPartialStride + 1);
     }
     __syncthreads();
     if (d == 0) {
@@ -270,7 +282,7 @@ __device__ __forceinline__ float merge_partials(const float* part, int n) {
     float num = 0.0f;
     if (d < kHeadDim) {
 #pragma unroll 8
-        for (int j = 0; j < n; ++j) num += s_w[j] * part[j * kPartialStride + 4 + d];
+        for (int j = 0; j < n; ++j) num += s_w[j] * fetch(part + j * kPartialStride + 4 + d);
     }
     __syncthreads();
     return num / s_den;
@@ -366,26 +378,29 @@ __global__ __launch_bounds__(kAttendWaves * 64) void step_kernel(StepArgs a) {
         return;
     }
 
-    float* part = a.partials + ((static_cast<size_t>(b) * kHeads + h) * a.max_splits + split) * kPartialStride;
+    // Several splits: publish this split's partial, count arrivals, and let
+    // the last split of the head merge all partials and finish the head.
+    const size_t head_row = static_cast<size_t>(b) * kHeads + h;
+    float* parts = a.partials + head_row * a.max_splits * kPartialStride;
     if (d < kHeadDim) {
-        part[4 + d] = o;
+        float* part = parts + static_cast<size_t>(split) * kPartialStride;
+        publish(part + 4 + d, o);
         if (d == 0) {
-            part[0] = mx;
-            part[1] = l;
+            publish(part, mx);
+            publish(part + 1, l);
         }
     }
-}
-
-// ---------------------------------------------------------------- combine
-
-// Grid (32 heads, batch), 128 threads: thread d = output channel d.
-__global__ __launch_bounds__(kHeadDim) void combine_kernel(StepArgs a) {
-    const int h = blockIdx.x, b = blockIdx.y;
-    const int len = a.positions[b] + 1;
-    const int n = (len + a.split_tokens - 1) / a.split_tokens;
-    if (n == 1) return;   // finished by its only split in the step kernel
-    const float* parts = a.partials + (static_cast<size_t>(b) * kHeads + h) * a.max_splits * kPartialStride;
-    finalize_head(a, b, h, merge_partials(parts, n));
+    __builtin_amdgcn_s_waitcnt(0);   // this thread's stores are complete before the barrier
+    __syncthreads();
+    __shared__ int s_last;
+    if (threadIdx.x == 0)
+        s_last = __hip_atomic_fetch_add(a.counters + head_row, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 static_cast<unsigned>(nsplit - 1);
+    __syncthreads();
+    if (!s_last) return;
+    finalize_head(a, b, h, merge_partials(parts, nsplit));
+    if (threadIdx.x == 0)   // ready for the next launch
+        __hip_atomic_store(a.counters + head_row, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------- utilities
@@ -421,11 +436,6 @@ hipError_t launch_step(const StepArgs& a, int grid_splits, bool q17, hipStream_t
     const dim3 grid(grid_splits, kHeads, a.batch);
     if (q17) step_kernel<true><<<grid, kAttendWaves * 64, 0, s>>>(a);
     else step_kernel<false><<<grid, kAttendWaves * 64, 0, s>>>(a);
-    return hipGetLastError();
-}
-
-hipError_t launch_combine(const StepArgs& a, hipStream_t s) {
-    combine_kernel<<<dim3(kHeads, a.batch), kHeadDim, 0, s>>>(a);
     return hipGetLastError();
 }
 

@@ -119,9 +119,8 @@ def run_gpu(skv, ctx, batch, context, layers, steps, warmup, seed, outliers=Fals
         "us_per_layer": 1000.0 * ms_step / layers,
         "gbps": total_bytes / (ms / 1e3) / 1e9,
         "tokens_per_s": batch * steps / (ms / 1e3),
-        "kernel_launches": dict(zip(["append", "step", "combine"], counts)),
-        "kernel_avg_us": {k: (1000.0 * t / c if c else None)
-                          for k, t, c in zip(["append", "step", "combine"], kms, counts)},
+        "kernel_launches": dict(zip(["append", "step"], counts)),
+        "kernel_avg_us": {k: (1000.0 * t / c if c else None) for k, t, c in zip(["append", "step"], kms, counts)},
     }
     res["pct_of_peak"] = 100.0 * res["gbps"] / HBM_PEAK_GBPS
     res["graph"] = {"us_per_layer": 1000.0 * ms_graph / steps / layers,

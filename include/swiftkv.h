@@ -235,9 +235,8 @@ int swiftkv_timer_elapsed(swiftkv_context* ctx, int32_t slot_begin, int32_t slot
  * kind, the launch count and the summed duration in ms, then clears the
  * record. */
 #define SWIFTKV_KERNEL_APPEND 0  /* bulk append (prefill) */
-#define SWIFTKV_KERNEL_STEP 1    /* the step kernel: append + split scan (+ output) */
-#define SWIFTKV_KERNEL_COMBINE 2 /* split combine, launched when a head spans splits */
-#define SWIFTKV_KERNEL_KINDS 3
+#define SWIFTKV_KERNEL_STEP 1    /* the step kernel: append, split scan, merge, output */
+#define SWIFTKV_KERNEL_KINDS 2
 int swiftkv_profile_enable(swiftkv_context* ctx, int32_t on);
 int swiftkv_profile_collect(swiftkv_context* ctx, int64_t counts[SWIFTKV_KERNEL_KINDS],
                             double ms[SWIFTKV_KERNEL_KINDS]);

@@ -54,8 +54,8 @@ def test_null_and_range_checks_without_device(skv):
     assert L.swiftkv_rope_lut_generate(None, 4096, 10000.0, C.byref(h)) == skv.EINVAL
     assert L.swiftkv_kv_cache_create(None, 1, 1, 1, C.byref(h)) == skv.EINVAL
     assert L.swiftkv_timer_record(None, 0) == skv.EINVAL
-    counts = (C.c_int64 * 3)()
-    ms = (C.c_double * 3)()
+    counts = (C.c_int64 * skv.KERNEL_KINDS)()
+    ms = (C.c_double * skv.KERNEL_KINDS)()
     assert L.swiftkv_profile_collect(None, counts, ms) == skv.EINVAL
     # destroy functions accept null like free()
     assert L.swiftkv_context_destroy(None) == skv.OK
