@@ -81,7 +81,7 @@ _SIGNATURES = {
     "swiftkv_attention_f32": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _vp]),
     "swiftkv_attention_q17": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _vp]),
     "swiftkv_append_tokens": (C.c_int, [_vp, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _i32]),
-    "swiftkv_fill_synthetic_f32": (C.c_int, [_vp, _vp, _sz, C.c_uint64, C.c_uint64, _i32, _i32]),
+    "swiftkv_fill_synthetic_f32": (C.c_int, [_vp, _vp, _sz, C.c_uint64, C.c_uint64, C.c_uint64, _i32, _i32]),
     "swiftkv_kv_cache_fill_synthetic": (C.c_int, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, C.c_uint64,
                                                   _i32, _i32]),
     "swiftkv_device_alloc": (C.c_int, [_vp, _sz, C.POINTER(_vp)]),
@@ -240,9 +240,9 @@ class Context:
         return list(counts), list(ms)
 
     def fill_synthetic(self, dst: DeviceBuffer, n: int, seed: int, stream: int, dist: int = DIST_NORMAL,
-                       outliers: bool = False) -> None:
-        """Elements [0, n) of the synthetic stream (seed, stream) as FP32 into dst."""
-        _check(lib().swiftkv_fill_synthetic_f32(self.handle, C.c_void_p(dst.ptr), n, seed, stream, dist,
+                       outliers: bool = False, first: int = 0) -> None:
+        """Elements [first, first+n) of the synthetic stream (seed, stream) as FP32 into dst."""
+        _check(lib().swiftkv_fill_synthetic_f32(self.handle, C.c_void_p(dst.ptr), n, first, seed, stream, dist,
                                                 1 if outliers else 0))
 
     def convert_f32_q17(self, src: DeviceBuffer, dst: DeviceBuffer, n: int) -> None:

@@ -661,14 +661,15 @@ int swiftkv_append_tokens(swiftkv_context* ctx, const void* k, const void* v, in
 
 // ---------------------------------------------------------------- synthetic data
 
-int swiftkv_fill_synthetic_f32(swiftkv_context* ctx, float* out, size_t n, uint64_t seed, uint64_t stream,
-                               int32_t distribution, int32_t outliers) {
+int swiftkv_fill_synthetic_f32(swiftkv_context* ctx, float* out, size_t n, uint64_t first, uint64_t seed,
+                               uint64_t stream, int32_t distribution, int32_t outliers) {
     if (!ctx || (n && !out)) return fail(SWIFTKV_EINVAL, "null argument");
+    if (first & 1u) return fail(SWIFTKV_EINVAL, "first element %llu must be even", (unsigned long long)first);
     if (distribution != SWIFTKV_DIST_NORMAL && distribution != SWIFTKV_DIST_STUDENT_T3)
         return fail(SWIFTKV_EINVAL, "unknown distribution %d", distribution);
     int rc = set_device(ctx);
     if (rc) return rc;
-    SKV_HIP(launch_fill_f32(out, n, seed, stream, distribution, outliers != 0, ctx->stream));
+    SKV_HIP(launch_fill_f32(out, n, first, seed, stream, distribution, outliers != 0, ctx->stream));
     return ok();
 }
 

@@ -88,8 +88,8 @@ hipError_t launch_step(const StepArgs& a, int grid_splits, bool q17, hipStream_t
 hipError_t launch_append_bulk(const BulkArgs& a, bool q17, hipStream_t s);
 hipError_t launch_convert(const float* in, int32_t* out, size_t n, hipStream_t s);
 // Synthetic inputs (swiftkv_synth.hip).
-hipError_t launch_fill_f32(float* out, size_t n, uint64_t seed, uint64_t stream, int dist, int outliers,
-                           hipStream_t s);
+hipError_t launch_fill_f32(float* out, size_t n, uint64_t first, uint64_t seed, uint64_t stream, int dist,
+                           int outliers, hipStream_t s);
 hipError_t launch_fill_cache(const CacheView& kv, const int2* lut, uint64_t seed, int layer0, int nlayers,
                              int slot0, int nslots, int ntok, int dist, int k_outliers, hipStream_t s);
 

@@ -6,7 +6,7 @@
 // unit-variance Student-t(3).  With `outliers` set, element i is multiplied by
 // 20 when its channel i % 4096 is one of the ~1% channels selected by the seed.
 //
-// Two consumers: swiftkv_fill_synthetic_f32 writes elements [0, n) of a stream
+// Two consumers: swiftkv_fill_synthetic_f32 writes elements [first, first+n) of a stream
 // (q/k/v step inputs, or a copy of a cache's source rows for checking), and
 // swiftkv_kv_cache_fill_synthetic feeds rows of the streams
 //   K: stream 2*(slot*64 + layer),  V: stream 2*(slot*64 + layer) + 1,
@@ -77,12 +77,14 @@ __device__ __forceinline__ Stream make_stream(uint64_t seed, uint64_t stream, in
     return st;
 }
 
-__global__ __launch_bounds__(256) void fill_f32_kernel(float* __restrict__ out, size_t npairs, uint64_t seed,
-                                                       uint64_t stream, int dist, int outliers, int odd_tail) {
+// Elements [2*pair0, 2*pair0 + n) of a stream (n may be odd).
+__global__ __launch_bounds__(256) void fill_f32_kernel(float* __restrict__ out, size_t npairs, uint64_t pair0,
+                                                       uint64_t seed, uint64_t stream, int dist, int outliers,
+                                                       int odd_tail) {
     const Stream st = make_stream(seed, stream, dist, outliers);
     const size_t step = static_cast<size_t>(gridDim.x) * blockDim.x;
     for (size_t j = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; j < npairs; j += step) {
-        const float2 x = stream_pair(st, j);
+        const float2 x = stream_pair(st, pair0 + j);
         if (odd_tail && j + 1 == npairs) {
             out[2 * j] = x.x;
         } else {
@@ -122,14 +124,14 @@ __global__ __launch_bounds__(256) void fill_cache_kernel(FillArgs a) {
 
 }  // namespace
 
-hipError_t launch_fill_f32(float* out, size_t n, uint64_t seed, uint64_t stream, int dist, int outliers,
-                           hipStream_t s) {
+hipError_t launch_fill_f32(float* out, size_t n, uint64_t first, uint64_t seed, uint64_t stream, int dist,
+                           int outliers, hipStream_t s) {
     if (n == 0) return hipSuccess;
     const size_t npairs = (n + 1) / 2;
     size_t blocks = (npairs + 255) / 256;
     if (blocks > 16384) blocks = 16384;
-    fill_f32_kernel<<<static_cast<unsigned>(blocks), 256, 0, s>>>(out, npairs, seed, stream, dist, outliers,
-                                                                   static_cast<int>(n & 1));
+    fill_f32_kernel<<<static_cast<unsigned>(blocks), 256, 0, s>>>(out, npairs, first / 2, seed, stream, dist,
+                                                                   outliers, static_cast<int>(n & 1));
     return hipGetLastError();
 }
 

@@ -183,9 +183,10 @@ int swiftkv_append_tokens(swiftkv_context* ctx, const void* k, const void* v, in
  * ------------------------------------------------------------------------ */
 #define SWIFTKV_DIST_NORMAL 0
 #define SWIFTKV_DIST_STUDENT_T3 1
-/* Elements [0, n) of stream (seed, stream) into device memory. */
-int swiftkv_fill_synthetic_f32(swiftkv_context* ctx, float* out, size_t n, uint64_t seed, uint64_t stream,
-                               int32_t distribution, int32_t outliers);
+/* Elements [first, first+n) of stream (seed, stream) into device memory;
+ * `first` must be even. */
+int swiftkv_fill_synthetic_f32(swiftkv_context* ctx, float* out, size_t n, uint64_t first, uint64_t seed,
+                               uint64_t stream, int32_t distribution, int32_t outliers);
 /* Tokens [0, ntok) of sequences [seq0, seq0+nseq) x layers [layer0,
  * layer0+nlayers) through the append rule, K row t of (slot s, layer l) =
  * elements [4096t, 4096t+4096) of stream 2*(64s + l) (with k_outliers),

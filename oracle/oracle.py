@@ -55,6 +55,8 @@ def lib() -> C.CDLL:
     L.oracle_g32_code.restype = C.c_int8
     L.oracle_g32_code.argtypes = [C.c_int32, C.c_uint8]
     L.oracle_quantize_row.argtypes = [_i32p, _i8p, _u8p]
+    L.oracle_quantize_rows.argtypes = [_i32p, C.c_int64, _i8p, _u8p]
+    L.oracle_rope_rotate_rows.argtypes = [_i32p, C.c_int64, _i32p, _i32p]
     L.oracle_shift_scale.restype = C.c_float
     L.oracle_shift_scale.argtypes = [C.c_uint8]
     L.oracle_pack_record.argtypes = [_i8p, _u8p, _i8p, _u8p, _u8p]
@@ -118,16 +120,15 @@ def rope_unpack(buf: np.ndarray):
 
 
 def rope_rotate(x: np.ndarray, cos64: np.ndarray, sin64: np.ndarray) -> np.ndarray:
-    """Rotate every 128-channel head row of x (int32, [..., 128])."""
+    """Rotate every 128-channel head row of x (int32, [..., 128]).  cos64/sin64
+    are one table row [64] for all rows, or one per row [..., 64]."""
     x = np.array(x, dtype=np.int32, copy=True)
-    rows = x.reshape(-1, HD)
-    c = np.ascontiguousarray(cos64, np.int32)
-    s = np.ascontiguousarray(sin64, np.int32)
-    for r in range(rows.shape[0]):
-        row = np.ascontiguousarray(rows[r])
-        lib().oracle_rope_rotate(row, c, s)
-        rows[r] = row
-    return x
+    rows = np.ascontiguousarray(x.reshape(-1, HD))
+    n = rows.shape[0]
+    c = np.ascontiguousarray(np.broadcast_to(np.asarray(cos64, np.int32).reshape(-1, PAIRS), (n, PAIRS)))
+    s = np.ascontiguousarray(np.broadcast_to(np.asarray(sin64, np.int32).reshape(-1, PAIRS), (n, PAIRS)))
+    lib().oracle_rope_rotate_rows(rows.reshape(-1), n, c.reshape(-1), s.reshape(-1))
+    return rows.reshape(x.shape)
 
 
 def quantize_rows(x: np.ndarray):
@@ -136,12 +137,7 @@ def quantize_rows(x: np.ndarray):
     rows = x.reshape(-1, HD)
     codes = np.empty(rows.shape, np.int8)
     shifts = np.empty((rows.shape[0], NGROUPS), np.uint8)
-    for r in range(rows.shape[0]):
-        cr = np.empty(HD, np.int8)
-        sr = np.empty(NGROUPS, np.uint8)
-        lib().oracle_quantize_row(np.ascontiguousarray(rows[r]), cr, sr)
-        codes[r] = cr
-        shifts[r] = sr
+    lib().oracle_quantize_rows(rows.reshape(-1), rows.shape[0], codes.reshape(-1), shifts.reshape(-1))
     return codes.reshape(x.shape), shifts.reshape(x.shape[:-1] + (NGROUPS,))
 
 

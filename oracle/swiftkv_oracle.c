@@ -15,7 +15,7 @@
  * AP_RND_CONV is round-half-to-even; because ties-to-even is symmetric it is
  * the same on the two's-complement value and on sign/magnitude.
  *
- * Pinning (what checks each function; see tests/test_oracle_*.py):
+ * Pinning (what checks each function; see tests/test_oracle.py):
  *   f2q17            exhaustive 2^32 sweep against an independent rint()-based
  *                    formula, and against the compiled reference emulator.
  *   rope_lut_*       sha256 of the packed 4096-position table equals the
@@ -99,8 +99,8 @@ void oracle_f2q17_array(const float* in, int32_t* out, int64_t n) {
 }
 
 /* Order-independent digest of f2q17 over the bit patterns [lo, hi):
- * sum over i of mix(i, f2q17(bits=i)).  Used as a "checksum of checksums"
- * against the device conversion over all 2^32 patterns. */
+ * sum over i of mix(i, f2q17(bits=i)).  Summed over all 2^32 patterns it is
+ * compared with the same digest of an independent float64 rint() formula. */
 static uint64_t mix64(uint64_t z) {
     z += 0x9e3779b97f4a7c15ull;
     z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
@@ -193,6 +193,11 @@ void oracle_rope_rotate(int32_t* x, const int32_t* cos64, const int32_t* sin64) 
     }
 }
 
+/* Rows [nrows][128], each rotated with its own table row cos/sin [nrows][64]. */
+void oracle_rope_rotate_rows(int32_t* x, int64_t nrows, const int32_t* cos_rows, const int32_t* sin_rows) {
+    for (int64_t r = 0; r < nrows; ++r) oracle_rope_rotate(x + r * HD, cos_rows + r * PAIRS, sin_rows + r * PAIRS);
+}
+
 /* ------------------------------------------------------------------------ */
 /* a4: G32 power-of-two quantization (cpp:348-414, emulator:543-564)          */
 /* ------------------------------------------------------------------------ */
@@ -223,6 +228,11 @@ void oracle_quantize_row(const int32_t* x, int8_t* codes, uint8_t* shifts) {
         shifts[g] = s;
         for (int i = 0; i < G32; ++i) codes[g * G32 + i] = oracle_g32_code(x[g * G32 + i], s);
     }
+}
+
+/* Many rows at once: x [nrows][128] -> codes [nrows][128], shifts [nrows][4]. */
+void oracle_quantize_rows(const int32_t* x, int64_t nrows, int8_t* codes, uint8_t* shifts) {
+    for (int64_t r = 0; r < nrows; ++r) oracle_quantize_row(x + r * HD, codes + r * HD, shifts + r * NGROUPS);
 }
 
 /* FP32 value of a G32 scale: 2^(s-17), exactly representable. */

@@ -1,0 +1,166 @@
+"""GPU parity at the workload's full sizes.
+
+Caches of these sizes (2.4 GB to 4.8 GB) are filled on the device from
+synthetic streams through the append rule; the tests regenerate the FP32
+source rows of sampled sequences, rebuild them with the oracle and compare:
+  - every cached and appended row of the sampled sequences, bit-exact;
+  - the appended row of every sequence, bit-exact;
+  - the outputs of the sampled sequences within max-abs 2e-5 + rel 1e-4.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle as O
+from gpu_cases import H, assert_close, assert_rows_equal
+
+pytestmark = pytest.mark.gpu
+
+
+def _note(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _source_rows(skv, ctx, seed, slot, layer, t0, n, dist=0, k_outliers=False):
+    """FP32 K/V rows [t0, t0+n) that the synthetic filler used for (slot, layer)."""
+    sid = 2 * (slot * 64 + layer)
+    buf = ctx.alloc(n * 4096 * 4)
+    ctx.fill_synthetic(buf, n * 4096, seed, sid, dist, k_outliers, first=t0 * 4096)
+    k = buf.download(np.float32, (n, 4096))
+    ctx.fill_synthetic(buf, n * 4096, seed, sid + 1, dist, False, first=t0 * 4096)
+    v = buf.download(np.float32, (n, 4096))
+    buf.free()
+    return k, v
+
+
+def _oracle_cache(skv, ctx, cos, sin, seed, slot, layer, ntok, cap, dist=0, k_outliers=False, chunk=4096):
+    sc = O.SequenceCache(H, cap)
+    for t0 in range(0, ntok, chunk):
+        n = min(chunk, ntok - t0)
+        k, v = _source_rows(skv, ctx, seed, slot, layer, t0, n, dist, k_outliers)
+        sc.fill_q17(O.f2q17(k), O.f2q17(v), t0, cos, sin)
+    return sc
+
+
+def _appended_rows_match(kv, slot, layer, pos, k_f32, v_f32, cos, sin):
+    """The row appended at `pos` for every head equals the oracle's append rule."""
+    krot = O.rope_rotate(O.f2q17(k_f32).reshape(H, 128), cos[pos], sin[pos])
+    kc, ks = O.quantize_rows(krot)
+    vc, vs = O.quantize_rows(O.f2q17(v_f32).reshape(H, 128))
+    for h in range(H):
+        gk, gv, gks, gvs = kv.read(slot, layer, h, pos, 1)
+        assert (gk[0] == kc[h]).all() and (gv[0] == vc[h]).all(), f"slot {slot} head {h} position {pos}: codes"
+        assert (gks[0].view(np.uint32) == O.shift_scale_bits(ks[h])).all(), f"slot {slot} head {h}: K scales"
+        assert (gvs[0].view(np.uint32) == O.shift_scale_bits(vs[h])).all(), f"slot {slot} head {h}: V scales"
+
+
+def _inputs(skv, ctx, seed, batch, k_outliers=False, dist=0):
+    bufs, host = [], []
+    for i in range(3):
+        b = ctx.alloc(batch * 4096 * 4)
+        ctx.fill_synthetic(b, batch * 4096, seed, 9000 + i, dist, k_outliers and i == 1)
+        bufs.append(b)
+        host.append(b.download(np.float32, (batch, 4096)))
+    return bufs, host
+
+
+def _step(skv, ctx, kv, lut, positions, bufs, out, aq=None, asc=None):
+    skv.swiftkv_attention(ctx, bufs[0], bufs[1], bufs[2], kv, lut, aq, asc, 0, positions, out)
+    ctx.synchronize()
+
+
+@pytest.mark.parametrize("ragged", [False, True], ids=["position4095", "ragged256to4095"])
+def test_batch64_context4096(skv, ctx, rope_tables, ragged):
+    cos, sin = rope_tables
+    seed = 4242 + int(ragged)
+    rng = np.random.default_rng(seed)
+    positions = (rng.integers(255, 4096, 64) if ragged else np.full(64, 4095)).astype(np.int32)
+    _note(f"case: batch 64, capacity 4096, {'ragged' if ragged else 'all'} positions, outliers={not ragged}")
+    lut = skv.RopeLut.generate(ctx, 4096)
+    kv = skv.KVCache(ctx, layers=1, max_batch=64, max_seq_len=4096)
+    kv.fill_synthetic(lut, ntok=4095, seed=seed, k_outliers=not ragged)
+    bufs, (q, k, v) = _inputs(skv, ctx, seed + 1, 64, k_outliers=not ragged)
+    out = ctx.alloc(64 * 4096 * 4)
+    aq, asc = ctx.alloc(64 * 128 * 56), ctx.alloc(64 * 128)
+    _step(skv, ctx, kv, lut, positions, bufs, out, aq, asc)
+    o = out.download(np.float32, (64, H, 128))
+    assert np.isfinite(o).all()
+    for b in range(64):
+        _appended_rows_match(kv, b, 0, int(positions[b]), k[b], v[b], cos, sin)
+    sample = sorted({0, 63, int(np.argmin(positions)), int(np.argmax(positions)), 21})
+    for b in sample:
+        p = int(positions[b])
+        _note(f"  oracle check of slot {b}, position {p}")
+        sc = _oracle_cache(skv, ctx, cos, sin, seed, b, 0, p, p + 1, k_outliers=not ragged)
+        res = sc.step_q17(O.f2q17(q[b]), O.f2q17(k[b]), O.f2q17(v[b]), p, cos[p], sin[p], fp=True)
+        assert_rows_equal(kv, sc, b, 0, 0, p + 1)
+        assert_close(o[b], res["fp"], f"slot {b} position {p}")
+    words = aq.download(np.uint8, (64, 128, 56))
+    codes = asc.download(np.uint8, (64, 128))
+    for b in (0, 63):
+        q14, e8 = O.a14(o[b].reshape(128, 32))
+        assert (codes[b] == e8).all() and (words[b] == O.pack_a14(q14)).all()
+    for x in bufs + [out, aq, asc]:
+        x.free()
+    kv.close()
+    lut.close()
+
+
+def test_batch16_context32k_512_steps(skv, ctx):
+    """Config-5 shape: 16 sequences, unit-variance Student-t(3) rows, cache
+    pre-filled to 32256 tokens, then 512 consecutive decode steps to 32767
+    (beyond the reference's 4096 limit: RoPE table extended by its closed
+    form, FP32 formula as the oracle)."""
+    B, start, steps, cap = 16, 32256, 512, 32768
+    seed = 5150
+    _note(f"case: batch {B}, context {start}..{start + steps}, Student-t(3), {steps} steps")
+    cos, sin = O.rope_values(cap)
+    lut = skv.RopeLut.generate(ctx, cap)
+    kv = skv.KVCache(ctx, layers=1, max_batch=B, max_seq_len=cap)
+    kv.fill_synthetic(lut, ntok=start, seed=seed, dist=skv.DIST_STUDENT_T3)
+    n = steps * B * 4096
+    qkv = [ctx.alloc(n * 4) for _ in range(3)]
+    for i, b in enumerate(qkv):
+        ctx.fill_synthetic(b, n, seed + 1, 7000 + i, skv.DIST_STUDENT_T3)
+    outs = ctx.alloc(steps * B * 4096 * 4)
+    stride = B * 4096 * 4
+    for j in range(steps):
+        off = j * stride
+        skv.swiftkv_attention(ctx, qkv[0].ptr + off, qkv[1].ptr + off, qkv[2].ptr + off, kv, lut, None, None, 0,
+                              np.full(B, start + j, np.int32), outs.ptr + off)
+        if j % 128 == 127:
+            ctx.synchronize()
+            _note(f"  step {j + 1}/{steps}")
+    ctx.synchronize()
+    q, k, v = (b.download(np.float32, (steps, B, 4096)) for b in qkv)
+    o = outs.download(np.float32, (steps, B, H, 128))
+    assert np.isfinite(o).all()
+    # every appended row of every sequence
+    _note("  checking appended rows")
+    for b in range(B):
+        for h in range(H):
+            gk, gv, gks, gvs = kv.read(b, 0, h, start, steps)
+            krot = O.rope_rotate(O.f2q17(k[:, b, h * 128:(h + 1) * 128]), cos[start:start + steps],
+                                 sin[start:start + steps])
+            kc, ks = O.quantize_rows(krot)
+            vc, vs = O.quantize_rows(O.f2q17(v[:, b, h * 128:(h + 1) * 128]))
+            assert (gk == kc).all() and (gv == vc).all(), f"slot {b} head {h}: appended codes"
+            assert (gks.view(np.uint32) == O.shift_scale_bits(ks)).all()
+            assert (gvs.view(np.uint32) == O.shift_scale_bits(vs)).all()
+    # outputs of the first and the last step for one sequence
+    _note("  oracle check of slot 5")
+    b = 5
+    sc = _oracle_cache(skv, ctx, cos, sin, seed, b, 0, start, cap, dist=skv.DIST_STUDENT_T3)
+    res = sc.step_q17(O.f2q17(q[0, b]), O.f2q17(k[0, b]), O.f2q17(v[0, b]), start, cos[start], sin[start])
+    assert_close(o[0, b], res["fp"], "first step")
+    sc.fill_q17(O.f2q17(k[1:steps - 1, b]), O.f2q17(v[1:steps - 1, b]), start + 1, cos, sin)
+    last = start + steps - 1
+    res = sc.step_q17(O.f2q17(q[-1, b]), O.f2q17(k[-1, b]), O.f2q17(v[-1, b]), last, cos[last], sin[last])
+    assert_close(o[-1, b], res["fp"], "last step")
+    assert_rows_equal(kv, sc, b, 0, 0, last + 1, heads=(0, 9, 31))
+    for x in qkv + [outs]:
+        x.free()
+    kv.close()
+    lut.close()
