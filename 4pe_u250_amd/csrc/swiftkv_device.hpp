@@ -118,6 +118,17 @@ __device__ __forceinline__ int2 load_pair(const void* base, size_t elem) {
     }
 }
 
+// Raw 64-bit pair (FP32 or Q15.17 bits) and its later conversion, so a load
+// can be issued well before the value is needed.
+__device__ __forceinline__ int2 load_bits_pair(const void* base, size_t elem) {
+    return *reinterpret_cast<const int2*>(static_cast<const int32_t*>(base) + elem);
+}
+template <bool Q17>
+__device__ __forceinline__ int2 bits_to_q17(int2 bits) {
+    if constexpr (Q17) return bits;
+    else return make_int2(f32_to_q17(__int_as_float(bits.x)), f32_to_q17(__int_as_float(bits.y)));
+}
+
 // Quantize this wave's (k rotated, v) row and write it at token `pos` of
 // `page`.  Lane l holds channels 2l, 2l+1; G32 group g = lanes 16g..16g+15.
 // Returns the dequantized values code * 2^(s-17) of the lane's channels.

@@ -75,15 +75,30 @@ __device__ __forceinline__ void axpy16(float* acc, float w, v4i v) {
 // ---------------------------------------------------------------- pieces
 
 // Rotated, pre-scaled query channels [16c, 16c+16) of head h (pairs 8c..8c+7).
-template <bool Q17>
-__device__ __forceinline__ void query_chunk(const StepArgs& a, int b, int h, int c, int pos, float* qf) {
+// Split in two so the 16 loads go out first (before the cache block, because
+// vmcnt retires in issue order) and the conversion, which branches, runs
+// once they have landed.
+struct QueryLoads {
+    int2 q[8], cs[8];
+};
+
+__device__ __forceinline__ void query_loads(const StepArgs& a, int b, int h, int c, int pos, QueryLoads& ql) {
     const size_t base = static_cast<size_t>(b) * kModelDim + h * kHeadDim + c * 16;
     const int2* cs = a.lut + static_cast<size_t>(pos) * kRopePairs + c * 8;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-        const int2 qi = load_pair<Q17>(a.q, base + 2 * j);
+        ql.q[j] = load_bits_pair(a.q, base + 2 * j);
+        ql.cs[j] = cs[j];
+    }
+}
+
+template <bool Q17>
+__device__ __forceinline__ void query_chunk(const QueryLoads& ql, float* qf) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int2 qi = bits_to_q17<Q17>(ql.q[j]);
         int32_t x0, x1;
-        rope_pair(qi.x, qi.y, cs[j], x0, x1);
+        rope_pair(qi.x, qi.y, ql.cs[j], x0, x1);
         qf[2 * j] = (static_cast<float>(x0) * 0x1p-17f) * kScoreScale;
         qf[2 * j + 1] = (static_cast<float>(x1) * 0x1p-17f) * kScoreScale;
     }
@@ -314,25 +329,41 @@ __global__ __launch_bounds__(kAttendWaves * 64) void step_kernel(StepArgs a) {
     __shared__ float s_acc[kAttendWaves + 1][kHeadDim];
     __shared__ float s_m[kAttendWaves + 1], s_l[kAttendWaves + 1];
 
-    // First block's loads go out before anything else, so the query rotation
-    // and the new row overlap their latency.  The new token is excluded from
-    // the scan (it is forwarded below).
+    // Loads go out before any math, in the order they are needed: the query
+    // chunk, the first cache block, the new row.  The query rotation then
+    // overlaps the block's flight.  The new token is excluded from the scan
+    // (it is forwarded below).
+    QueryLoads ql;
+    query_loads(a, b, h, c, pos, ql);
     const PageReader pr = make_reader(page, cap, c, r);
     const int t_first = t_begin + wave * kBlockTokens;
     const int t_stop = owner ? pos : t_end;
     BlockLoads bl;
     if (t_first < t_stop) issue_block(pr, t_first, bl);
 
-    // The new row: convert, rotate k, quantize, append; forward (k^ . q', v^).
-    if (owner && wave == 0) {
-        const size_t elem = static_cast<size_t>(b) * kModelDim + h * kHeadDim + 2 * lane;
-        const int2 cs = a.lut[static_cast<size_t>(pos) * kRopePairs + lane];
-        const int2 qi = load_pair<Q17>(a.q, elem);
-        const int2 ki = load_pair<Q17>(a.k, elem);
-        const int2 vi = load_pair<Q17>(a.v, elem);
+    // The new row's inputs are fetched now; its math runs after the scan, so
+    // the fetch latency hides under the cache stream.
+    // (Unconditional, always in bounds: a conditional load would make the
+    // compiler wait for the prefetched block at the branch join.)
+    const bool row_wave = owner && wave == 0;
+    const size_t row_elem = static_cast<size_t>(b) * kModelDim + h * kHeadDim + 2 * lane;
+    const int2 row_cs = a.lut[static_cast<size_t>(pos) * kRopePairs + lane];
+    const int2 row_q = load_bits_pair(a.q, row_elem);
+    const int2 row_k = load_bits_pair(a.k, row_elem);
+    const int2 row_v = load_bits_pair(a.v, row_elem);
+
+    float qf[16];
+    query_chunk<Q17>(ql, qf);
+    float m_run, l_run, acc[16];
+    scan_range(pr, bl, qf, t_first, t_stop, kAttendWaves * kBlockTokens, r, m_run, l_run, acc);
+
+    // The new row: convert, rotate k, quantize, append; forward (k^ . q', v^)
+    // into the merge as one more partial.
+    if (row_wave) {
+        const int2 qi = bits_to_q17<Q17>(row_q), ki = bits_to_q17<Q17>(row_k), vi = bits_to_q17<Q17>(row_v);
         int32_t q0, q1, k0, k1;
-        rope_pair(qi.x, qi.y, cs, q0, q1);
-        rope_pair(ki.x, ki.y, cs, k0, k1);
+        rope_pair(qi.x, qi.y, row_cs, q0, q1);
+        rope_pair(ki.x, ki.y, row_cs, k0, k1);
         float kh0, kh1, vh0, vh1;
         append_row_dequant(page, a.kv.seq_cap, pos, lane, k0, k1, vi.x, vi.y, kh0, kh1, vh0, vh1);
         float sp = ((static_cast<float>(q0) * 0x1p-17f) * kScoreScale) * kh0 +
@@ -346,11 +377,6 @@ __global__ __launch_bounds__(kAttendWaves * 64) void step_kernel(StepArgs a) {
             s_l[kAttendWaves] = 1.0f;
         }
     }
-
-    float qf[16];
-    query_chunk<Q17>(a, b, h, c, pos, qf);
-    float m_run, l_run, acc[16];
-    scan_range(pr, bl, qf, t_first, t_stop, kAttendWaves * kBlockTokens, r, m_run, l_run, acc);
     if (r == 0) {
 #pragma unroll
         for (int j = 0; j < 16; ++j) s_acc[wave][c * 16 + j] = acc[j];
