@@ -43,8 +43,8 @@ TOKEN_BYTES = 288          # algorithmic bytes per cached token-head: 2 x 128 co
 
 OK, EINVAL, ERANGE, EHIP, ENOMEM, ESTATE = 0, -1, -2, -3, -4, -5
 DIST_NORMAL, DIST_STUDENT_T3 = 0, 1
-KERNEL_APPEND, KERNEL_STEP = 0, 1
-KERNEL_KINDS = 2
+KERNEL_APPEND, KERNEL_STEP, KERNEL_EXACT = 0, 1, 2
+KERNEL_KINDS = 3
 _STATUS_NAMES = {EINVAL: "EINVAL", ERANGE: "ERANGE", EHIP: "EHIP", ENOMEM: "ENOMEM", ESTATE: "ESTATE"}
 
 
@@ -80,6 +80,7 @@ _SIGNATURES = {
     "swiftkv_kv_cache_import_records": (C.c_int, [_vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp]),
     "swiftkv_attention_f32": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _vp]),
     "swiftkv_attention_q17": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _vp]),
+    "swiftkv_attention_exact": (C.c_int, [_vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _vp]),
     "swiftkv_append_tokens": (C.c_int, [_vp, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _i32]),
     "swiftkv_fill_synthetic_f32": (C.c_int, [_vp, _vp, _sz, C.c_uint64, C.c_uint64, C.c_uint64, _i32, _i32]),
     "swiftkv_kv_cache_fill_synthetic": (C.c_int, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, C.c_uint64,
@@ -378,6 +379,25 @@ def swiftkv_attention(ctx: Context, q, k, v, kv_cache: KVCache, rope_lut: RopeLu
     _check(fn(ctx.handle, _ptr(q), _ptr(k), _ptr(v), kv_cache.handle, rope_lut.handle,
               _ptr(activation_q), _ptr(activation_scale), int(layer_index), _host_ptr(pos), int(pos.size),
               _ptr(out)))
+
+
+def swiftkv_attention_exact(ctx: Context, q, k, v, kv_cache: KVCache, rope_lut: RopeLut,
+                            activation_q, activation_scale, layer_index: int, position,
+                            out_q17, q17: bool = False) -> None:
+    """The decode step in the reference's own Q15.17 integer arithmetic.
+
+    Same append and arguments as swiftkv_attention, but the attention is the
+    single-pass (max, Z, Y) recurrence of int4_swiftkv_attention_peN
+    (swiftkv_attention.cpp:934-1880), so activation_q / activation_scale are
+    bit-identical to the reference's.  out_q17: device [batch][4096] int32,
+    the normalized Q15.17 state.  A verification path: one workgroup per
+    (sequence, head), sequential in the token index.
+    """
+    pos = np.ascontiguousarray(np.atleast_1d(np.asarray(position, dtype=np.int32)))
+    _check(lib().swiftkv_attention_exact(ctx.handle, _ptr(q), _ptr(k), _ptr(v), 1 if q17 else 0,
+                                         kv_cache.handle, rope_lut.handle, _ptr(activation_q),
+                                         _ptr(activation_scale), int(layer_index), _host_ptr(pos),
+                                         int(pos.size), _ptr(out_q17)))
 
 
 def swiftkv_append_tokens(ctx: Context, k, v, kv_cache: KVCache, rope_lut: RopeLut, layer_index: int,

@@ -30,7 +30,7 @@ HIP_FLAGS = [
     "-Wall",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
-SOURCES = ["swiftkv_kernels.hip", "swiftkv_synth.hip", "swiftkv_capi.cpp"]
+SOURCES = ["swiftkv_kernels.hip", "swiftkv_synth.hip", "swiftkv_exact.hip", "swiftkv_capi.cpp"]
 
 
 def _run(cmd, cwd=None):

@@ -290,6 +290,50 @@ int run_step(swiftkv_context* ctx, const void* q, const void* k, const void* v, 
     return ok();
 }
 
+// Q30 exp2 table RNE(2^(30 + i/32)), i = 0..32 (swiftkv_attention.cpp:185-195).
+const uint32_t* exp2_table() {
+    static const std::vector<uint32_t> table = [] {
+        std::vector<uint32_t> t(33);
+        for (int i = 0; i < 33; ++i)
+            t[i] = static_cast<uint32_t>(std::nearbyint(std::ldexp(std::pow(2.0, i / 32.0), 30)));
+        return t;
+    }();
+    return table.data();
+}
+
+int run_exact(swiftkv_context* ctx, const void* q, const void* k, const void* v, bool q17,
+              swiftkv_kv_cache* kv, const swiftkv_rope_lut* lut, uint8_t* act_q, uint8_t* act_scale,
+              int32_t layer, const int32_t* positions, int32_t batch, int32_t* out) {
+    int rc = validate_step(ctx, q, k, v, kv, lut, act_q, act_scale, layer, positions, batch,
+                           reinterpret_cast<const float*>(out));
+    if (rc) return rc;
+    if ((rc = set_device(ctx))) return rc;
+    for (int32_t b0 = 0; b0 < batch; b0 += kMaxBatchPerLaunch) {
+        const int32_t nb = std::min<int32_t>(kMaxBatchPerLaunch, batch - b0);
+        StepArgs a;
+        std::memset(&a, 0, sizeof(a));
+        const size_t row0 = static_cast<size_t>(b0) * kModelDim;
+        a.q = static_cast<const char*>(q) + row0 * 4;
+        a.k = static_cast<const char*>(k) + row0 * 4;
+        a.v = static_cast<const char*>(v) + row0 * 4;
+        a.kv = CacheView{kv->base, kv->page_bytes, kv->seq_cap, kv->layers};
+        a.lut = lut->table;
+        a.lut_positions = lut->positions;
+        a.layer = layer;
+        a.batch = nb;
+        a.slot0 = b0;
+        for (int32_t b = 0; b < nb; ++b) a.positions[b] = positions[b0 + b];
+        a.out = reinterpret_cast<float*>(out + row0);
+        a.act_q = act_q ? act_q + static_cast<size_t>(b0) * kHeads * kGroupsPerHead * SWIFTKV_A14_WORD_BYTES
+                        : nullptr;
+        a.act_scale = act_scale ? act_scale + static_cast<size_t>(b0) * kHeads * kGroupsPerHead : nullptr;
+        ProfilePair* p = profile_begin(ctx, SWIFTKV_KERNEL_EXACT);
+        SKV_HIP(launch_exact(a, exp2_table(), q17, ctx->stream));
+        profile_end(ctx, p);
+    }
+    return ok();
+}
+
 int check_cache_range(const swiftkv_context* ctx, const swiftkv_kv_cache* kv, int32_t seq, int32_t layer,
                       int32_t head, int32_t tok0, int32_t n) {
     if (!ctx) return fail(SWIFTKV_EINVAL, "null context");
@@ -628,6 +672,14 @@ int swiftkv_attention_q17(swiftkv_context* ctx, const int32_t* q, const int32_t*
                           int32_t batch, float* out) {
     return run_step(ctx, q, k, v, true, kv_cache, rope_lut, activation_q, activation_scale, layer_index,
                     positions, batch, out);
+}
+
+int swiftkv_attention_exact(swiftkv_context* ctx, const void* q, const void* k, const void* v, int32_t q17,
+                            swiftkv_kv_cache* kv_cache, const swiftkv_rope_lut* rope_lut, uint8_t* activation_q,
+                            uint8_t* activation_scale, int32_t layer_index, const int32_t* positions,
+                            int32_t batch, int32_t* out_q17) {
+    return run_exact(ctx, q, k, v, q17 != 0, kv_cache, rope_lut, activation_q, activation_scale, layer_index,
+                     positions, batch, out_q17);
 }
 
 int swiftkv_append_tokens(swiftkv_context* ctx, const void* k, const void* v, int32_t q17,

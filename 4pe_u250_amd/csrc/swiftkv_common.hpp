@@ -86,6 +86,9 @@ struct BulkArgs {
 // Launchers (swiftkv_kernels.hip).
 hipError_t launch_step(const StepArgs& a, int grid_splits, bool q17, hipStream_t s);
 hipError_t launch_append_bulk(const BulkArgs& a, bool q17, hipStream_t s);
+// Integer-compatibility step (one workgroup per (sequence, head)); a.out is
+// int32 Q15.17; exp_lut holds the 33 Q30 exp2 entries.
+hipError_t launch_exact(const StepArgs& a, const uint32_t* exp_lut, bool q17, hipStream_t s);
 hipError_t launch_convert(const float* in, int32_t* out, size_t n, hipStream_t s);
 // Synthetic inputs (swiftkv_synth.hip).
 hipError_t launch_fill_f32(float* out, size_t n, uint64_t first, uint64_t seed, uint64_t stream, int dist,

@@ -131,10 +131,14 @@ __device__ __forceinline__ int2 bits_to_q17(int2 bits) {
 
 // Quantize this wave's (k rotated, v) row and write it at token `pos` of
 // `page`.  Lane l holds channels 2l, 2l+1; G32 group g = lanes 16g..16g+15.
-// Returns the dequantized values code * 2^(s-17) of the lane's channels.
-__device__ __forceinline__ void append_row_dequant(int8_t* page, int seq_cap, int pos, int lane, int32_t k0,
-                                                   int32_t k1, int32_t v0, int32_t v1, float& kh0, float& kh1,
-                                                   float& vh0, float& vh1) {
+// Returns the lane's code bytes and its group's shifts.
+struct RowCodes {
+    uint32_t k0, k1, v0, v1;   // code bytes
+    uint32_t sk, sv;           // G32 shifts of the lane's group
+};
+
+__device__ __forceinline__ RowCodes append_row_codes(int8_t* page, int seq_cap, int pos, int lane, int32_t k0,
+                                                     int32_t k1, int32_t v0, int32_t v1) {
     uint32_t mk = max(magnitude(k0), magnitude(k1));
     uint32_t mv = max(magnitude(v0), magnitude(v1));
 #pragma unroll
@@ -142,23 +146,35 @@ __device__ __forceinline__ void append_row_dequant(int8_t* page, int seq_cap, in
         mk = max(mk, static_cast<uint32_t>(__shfl_xor(static_cast<int>(mk), d)));
         mv = max(mv, static_cast<uint32_t>(__shfl_xor(static_cast<int>(mv), d)));
     }
-    const uint32_t sk = g32_shift(mk), sv = g32_shift(mv);
-    const uint32_t ck0 = g32_code_byte(k0, sk), ck1 = g32_code_byte(k1, sk);
-    const uint32_t cv0 = g32_code_byte(v0, sv), cv1 = g32_code_byte(v1, sv);
+    RowCodes rc;
+    rc.sk = g32_shift(mk);
+    rc.sv = g32_shift(mv);
+    rc.k0 = g32_code_byte(k0, rc.sk);
+    rc.k1 = g32_code_byte(k1, rc.sk);
+    rc.v0 = g32_code_byte(v0, rc.sv);
+    rc.v1 = g32_code_byte(v1, rc.sv);
     const int64_t row = static_cast<int64_t>(pos) * kCodeBytes;
-    reinterpret_cast<uint16_t*>(page + row)[lane] = static_cast<uint16_t>(ck0 | (ck1 << 8));
+    reinterpret_cast<uint16_t*>(page + row)[lane] = static_cast<uint16_t>(rc.k0 | (rc.k1 << 8));
     reinterpret_cast<uint16_t*>(page + static_cast<int64_t>(seq_cap) * kCodeBytes + row)[lane] =
-        static_cast<uint16_t>(cv0 | (cv1 << 8));
-    const float fk = shift_scale(sk), fv = shift_scale(sv);
+        static_cast<uint16_t>(rc.v0 | (rc.v1 << 8));
     if ((lane & 15) == 0) {
         float2* sc = reinterpret_cast<float2*>(page + static_cast<int64_t>(seq_cap) * (2 * kCodeBytes) +
                                                static_cast<int64_t>(pos) * kScaleBytes);
-        sc[lane >> 4] = make_float2(fk, fv);
+        sc[lane >> 4] = make_float2(shift_scale(rc.sk), shift_scale(rc.sv));
     }
-    kh0 = static_cast<float>(static_cast<int8_t>(ck0)) * fk;
-    kh1 = static_cast<float>(static_cast<int8_t>(ck1)) * fk;
-    vh0 = static_cast<float>(static_cast<int8_t>(cv0)) * fv;
-    vh1 = static_cast<float>(static_cast<int8_t>(cv1)) * fv;
+    return rc;
+}
+
+// The same, returning the dequantized values code * 2^(s-17) of the lane's channels.
+__device__ __forceinline__ void append_row_dequant(int8_t* page, int seq_cap, int pos, int lane, int32_t k0,
+                                                   int32_t k1, int32_t v0, int32_t v1, float& kh0, float& kh1,
+                                                   float& vh0, float& vh1) {
+    const RowCodes rc = append_row_codes(page, seq_cap, pos, lane, k0, k1, v0, v1);
+    const float fk = shift_scale(rc.sk), fv = shift_scale(rc.sv);
+    kh0 = static_cast<float>(static_cast<int8_t>(rc.k0)) * fk;
+    kh1 = static_cast<float>(static_cast<int8_t>(rc.k1)) * fk;
+    vh0 = static_cast<float>(static_cast<int8_t>(rc.v0)) * fv;
+    vh1 = static_cast<float>(static_cast<int8_t>(rc.v1)) * fv;
 }
 
 __device__ __forceinline__ void append_row(int8_t* page, int seq_cap, int pos, int lane, int32_t k0, int32_t k1,

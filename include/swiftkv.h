@@ -163,6 +163,25 @@ int swiftkv_attention_q17(swiftkv_context* ctx, const int32_t* q, const int32_t*
                           uint8_t* activation_scale, int32_t layer_index,
                           const int32_t* positions, int32_t batch, float* out);
 
+/* Integer-compatibility step: the same append, then the reference's own
+ * Q15.17 arithmetic instead of the FP32 formula -- 44-bit wrapped G32 dot
+ * products, score * RNE(2^17/sqrt(128)) >> 24, the single-pass (max, Z, Y)
+ * recurrence with the 33-entry Q30 exp2 table, the Q13.17 normalizer with
+ * its 30-bit wrap, the 18-bit reciprocal and Y * 1/Z
+ * (swiftkv_attention.cpp:934-1880; llama2_decoder_sw_emulator.cpp:633-711),
+ * and the integer-path A14/E8M0 epilogue (swiftkv_attention.cpp:1694-1771).
+ * activation_q / activation_scale equal what int4_swiftkv_attention_peN
+ * writes, bit for bit.  The recurrence is sequential in the token index, so
+ * this entry is a compatibility and verification path (one workgroup per
+ * (sequence, head)), not the fast path.
+ *   q, k, v   device [batch][4096], FP32 when q17 == 0, Q15.17 int32 otherwise
+ *   out_q17   device [batch][4096] int32: the normalized Q15.17 state
+ * Other arguments as for swiftkv_attention_f32. */
+int swiftkv_attention_exact(swiftkv_context* ctx, const void* q, const void* k, const void* v,
+                            int32_t q17, swiftkv_kv_cache* kv_cache, const swiftkv_rope_lut* rope_lut,
+                            uint8_t* activation_q, uint8_t* activation_scale, int32_t layer_index,
+                            const int32_t* positions, int32_t batch, int32_t* out_q17);
+
 /* Bulk append (prompt prefill): apply the append rule -- conversion, RoPE of
  * k at its own position, G32 quantization -- to n tokens [pos0, pos0+n) of
  * one sequence without attending.  k, v: device [n][4096], FP32 when
@@ -237,7 +256,8 @@ int swiftkv_timer_elapsed(swiftkv_context* ctx, int32_t slot_begin, int32_t slot
  * record. */
 #define SWIFTKV_KERNEL_APPEND 0  /* bulk append (prefill) */
 #define SWIFTKV_KERNEL_STEP 1    /* the step kernel: append, split scan, merge, output */
-#define SWIFTKV_KERNEL_KINDS 2
+#define SWIFTKV_KERNEL_EXACT 2   /* the integer-compatibility step */
+#define SWIFTKV_KERNEL_KINDS 3
 int swiftkv_profile_enable(swiftkv_context* ctx, int32_t on);
 int swiftkv_profile_collect(swiftkv_context* ctx, int64_t counts[SWIFTKV_KERNEL_KINDS],
                             double ms[SWIFTKV_KERNEL_KINDS]);

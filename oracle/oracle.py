@@ -183,6 +183,21 @@ def a14(x: np.ndarray):
     return q.reshape(x.shape), e.reshape(x.shape[:-1])
 
 
+def a14_q17(raw: np.ndarray):
+    """Integer-path A14/E8M0 of Q15.17 values [..., 32] -> (int16 [..., 32], uint8 [...])."""
+    raw = np.ascontiguousarray(raw, np.int32)
+    rows = raw.reshape(-1, G32)
+    q = np.empty(rows.shape, np.int16)
+    e = np.empty(rows.shape[0], np.uint8)
+    for r in range(rows.shape[0]):
+        qr = np.empty(G32, np.int16)
+        er = np.empty(1, np.uint8)
+        lib().oracle_a14_group_q17(np.ascontiguousarray(rows[r]), qr, er)
+        q[r] = qr
+        e[r] = er[0]
+    return q.reshape(raw.shape), e.reshape(raw.shape[:-1])
+
+
 def pack_a14(q14: np.ndarray) -> np.ndarray:
     rows = np.ascontiguousarray(q14, np.int16).reshape(-1, G32)
     out = np.empty((rows.shape[0], 56), np.uint8)
