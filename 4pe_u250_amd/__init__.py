@@ -80,6 +80,7 @@ _SIGNATURES = {
     "swiftkv_kv_cache_import_records": (C.c_int, [_vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp]),
     "swiftkv_attention_f32": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _vp]),
     "swiftkv_attention_q17": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _vp]),
+    "swiftkv_set_host_io": (C.c_int, [_vp, _i32]),
     "swiftkv_attention_exact": (C.c_int, [_vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _vp]),
     "swiftkv_append_tokens": (C.c_int, [_vp, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _i32]),
     "swiftkv_fill_synthetic_f32": (C.c_int, [_vp, _vp, _sz, C.c_uint64, C.c_uint64, C.c_uint64, _i32, _i32]),
@@ -191,6 +192,7 @@ class Context:
         _check(lib().swiftkv_context_create(device, C.byref(h)))
         self.handle = h.value
         self.device = device
+        self.host_io = False
 
     def close(self) -> None:
         if self.handle:
@@ -208,6 +210,13 @@ class Context:
 
     def set_split_tokens(self, n: int) -> None:
         _check(lib().swiftkv_set_split_tokens(self.handle, int(n)))
+
+    def set_host_io(self, enable: bool) -> None:
+        """Host-memory I/O: step and append tensors are numpy arrays, staged
+        through the device by the library; each call returns with its outputs
+        written back."""
+        _check(lib().swiftkv_set_host_io(self.handle, 1 if enable else 0))
+        self.host_io = bool(enable)
 
     def alloc(self, nbytes: int) -> DeviceBuffer:
         return DeviceBuffer(self, nbytes)
@@ -360,7 +369,37 @@ def _ptr(x) -> Optional[int]:
         return None
     if isinstance(x, DeviceBuffer):
         return x.ptr
+    if isinstance(x, np.ndarray):
+        raise TypeError("a numpy array is host memory: pass a DeviceBuffer, or enable ctx.set_host_io(True)")
     return int(x)
+
+
+def _io_ptr(ctx: "Context", x, dtype=None, writable: bool = False) -> Optional[int]:
+    """Pointer for a step/append tensor: device memory normally, C-contiguous
+    numpy arrays (of `dtype`) in host-memory I/O mode."""
+    if x is None:
+        return None
+    if not ctx.host_io:
+        return _ptr(x)
+    if not isinstance(x, np.ndarray):
+        raise TypeError("host-memory I/O mode takes numpy arrays")
+    if not x.flags["C_CONTIGUOUS"] or (writable and not x.flags["WRITEABLE"]):
+        raise ValueError("host arrays must be C-contiguous (and writable for outputs)")
+    if dtype is not None and x.dtype != np.dtype(dtype):
+        raise TypeError(f"expected {np.dtype(dtype)}, got {x.dtype}")
+    return x.ctypes.data
+
+
+def _check_io_sizes(ctx: Context, batch: int, q, k, v, out, aq, asc) -> None:
+    """In host-memory I/O mode the library copies whole [batch][...] rows:
+    refuse host arrays too small for them."""
+    if not ctx.host_io:
+        return
+    need = [(q, batch * 4096), (k, batch * 4096), (v, batch * 4096), (out, batch * 4096),
+            (aq, batch * 128 * 56), (asc, batch * 128)]
+    for x, n in need:
+        if isinstance(x, np.ndarray) and x.size < n:
+            raise ValueError(f"host array holds {x.size} values, the step needs {n}")
 
 
 def swiftkv_attention(ctx: Context, q, k, v, kv_cache: KVCache, rope_lut: RopeLut,
@@ -376,9 +415,12 @@ def swiftkv_attention(ctx: Context, q, k, v, kv_cache: KVCache, rope_lut: RopeLu
     """
     pos = np.ascontiguousarray(np.atleast_1d(np.asarray(position, dtype=np.int32)))
     fn = lib().swiftkv_attention_q17 if q17 else lib().swiftkv_attention_f32
-    _check(fn(ctx.handle, _ptr(q), _ptr(k), _ptr(v), kv_cache.handle, rope_lut.handle,
-              _ptr(activation_q), _ptr(activation_scale), int(layer_index), _host_ptr(pos), int(pos.size),
-              _ptr(out)))
+    _check_io_sizes(ctx, pos.size, q, k, v, out, activation_q, activation_scale)
+    it = np.int32 if q17 else np.float32
+    _check(fn(ctx.handle, _io_ptr(ctx, q, it), _io_ptr(ctx, k, it), _io_ptr(ctx, v, it), kv_cache.handle,
+              rope_lut.handle, _io_ptr(ctx, activation_q, np.uint8, True),
+              _io_ptr(ctx, activation_scale, np.uint8, True), int(layer_index), _host_ptr(pos), int(pos.size),
+              _io_ptr(ctx, out, np.float32, True)))
 
 
 def swiftkv_attention_exact(ctx: Context, q, k, v, kv_cache: KVCache, rope_lut: RopeLut,
@@ -394,17 +436,26 @@ def swiftkv_attention_exact(ctx: Context, q, k, v, kv_cache: KVCache, rope_lut: 
     (sequence, head), sequential in the token index.
     """
     pos = np.ascontiguousarray(np.atleast_1d(np.asarray(position, dtype=np.int32)))
-    _check(lib().swiftkv_attention_exact(ctx.handle, _ptr(q), _ptr(k), _ptr(v), 1 if q17 else 0,
-                                         kv_cache.handle, rope_lut.handle, _ptr(activation_q),
-                                         _ptr(activation_scale), int(layer_index), _host_ptr(pos),
-                                         int(pos.size), _ptr(out_q17)))
+    _check_io_sizes(ctx, pos.size, q, k, v, out_q17, activation_q, activation_scale)
+    it = np.int32 if q17 else np.float32
+    _check(lib().swiftkv_attention_exact(ctx.handle, _io_ptr(ctx, q, it), _io_ptr(ctx, k, it),
+                                         _io_ptr(ctx, v, it), 1 if q17 else 0, kv_cache.handle, rope_lut.handle,
+                                         _io_ptr(ctx, activation_q, np.uint8, True),
+                                         _io_ptr(ctx, activation_scale, np.uint8, True), int(layer_index),
+                                         _host_ptr(pos), int(pos.size), _io_ptr(ctx, out_q17, np.int32, True)))
 
 
 def swiftkv_append_tokens(ctx: Context, k, v, kv_cache: KVCache, rope_lut: RopeLut, layer_index: int,
                           seq: int, pos0: int, n: int, q17: bool = False) -> None:
     """Bulk append (prefill) of n tokens [pos0, pos0+n) of one sequence."""
-    _check(lib().swiftkv_append_tokens(ctx.handle, _ptr(k), _ptr(v), 1 if q17 else 0, kv_cache.handle,
-                                       rope_lut.handle, int(layer_index), int(seq), int(pos0), int(n)))
+    it = np.int32 if q17 else np.float32
+    if ctx.host_io:
+        for x in (k, v):
+            if isinstance(x, np.ndarray) and x.size < n * 4096:
+                raise ValueError(f"host array holds {x.size} values, need {n} x 4096")
+    _check(lib().swiftkv_append_tokens(ctx.handle, _io_ptr(ctx, k, it), _io_ptr(ctx, v, it), 1 if q17 else 0,
+                                       kv_cache.handle, rope_lut.handle, int(layer_index), int(seq), int(pos0),
+                                       int(n)))
 
 
 def unpack_a14(words: np.ndarray) -> np.ndarray:

@@ -81,6 +81,10 @@ struct swiftkv_context {
     std::vector<ProfilePair> profile_pool;
     size_t profile_used = 0;
     bool capturing = false;     // the stream is being recorded into a graph
+    // host-memory I/O mode: step inputs/outputs are host pointers staged here
+    bool host_io = false;
+    uint8_t* io_stage = nullptr;
+    size_t io_bytes = 0;
 };
 
 struct swiftkv_graph {
@@ -209,6 +213,15 @@ int32_t choose_split(const swiftkv_context* ctx, const int32_t* positions, int32
     return static_cast<int32_t>(std::min<int64_t>(quanta * kSplitQuantum, kMaxSeq));
 }
 
+// Longest-first dispatch order for one launch's sequences (stable, so a
+// uniform batch keeps its natural order).
+void set_order(StepArgs& a) {
+    int32_t idx[kMaxBatchPerLaunch];
+    for (int32_t b = 0; b < a.batch; ++b) idx[b] = b;
+    std::stable_sort(idx, idx + a.batch, [&](int32_t x, int32_t y) { return a.positions[x] > a.positions[y]; });
+    for (int32_t b = 0; b < a.batch; ++b) a.order[b] = static_cast<uint8_t>(idx[b]);
+}
+
 int validate_step(swiftkv_context* ctx, const void* q, const void* k, const void* v,
                   const swiftkv_kv_cache* kv, const swiftkv_rope_lut* lut, const uint8_t* act_q,
                   const uint8_t* act_scale, int32_t layer, const int32_t* positions, int32_t batch,
@@ -270,6 +283,7 @@ int run_step(swiftkv_context* ctx, const void* q, const void* k, const void* v, 
             a.positions[b] = positions[b0 + b];
             max_pos = std::max(max_pos, a.positions[b]);
         }
+        set_order(a);
         a.split_tokens = choose_split(ctx, a.positions, nb);
         const int32_t grid_splits = (max_pos + 1 + a.split_tokens - 1) / a.split_tokens;
         a.max_splits = grid_splits;
@@ -323,6 +337,7 @@ int run_exact(swiftkv_context* ctx, const void* q, const void* k, const void* v,
         a.batch = nb;
         a.slot0 = b0;
         for (int32_t b = 0; b < nb; ++b) a.positions[b] = positions[b0 + b];
+        set_order(a);
         a.out = reinterpret_cast<float*>(out + row0);
         a.act_q = act_q ? act_q + static_cast<size_t>(b0) * kHeads * kGroupsPerHead * SWIFTKV_A14_WORD_BYTES
                         : nullptr;
@@ -331,6 +346,53 @@ int run_exact(swiftkv_context* ctx, const void* q, const void* k, const void* v,
         SKV_HIP(launch_exact(a, exp2_table(), q17, ctx->stream));
         profile_end(ctx, p);
     }
+    return ok();
+}
+
+// Entry dispatch.  In host-memory I/O mode the step's q/k/v, output and
+// activation pointers are host memory: inputs are copied into a context-owned
+// device stage on the context stream, the step runs on the staged copies, the
+// outputs are copied back and the call waits for them, so the host buffers
+// are valid on return (the reference host does the same around each PE call:
+// DMA in, run, DMA out, decode_host.cpp:1358-1485).
+int dispatch_step(swiftkv_context* ctx, bool exact, const void* q, const void* k, const void* v, bool q17,
+                  swiftkv_kv_cache* kv, const swiftkv_rope_lut* lut, uint8_t* act_q, uint8_t* act_scale,
+                  int32_t layer, const int32_t* positions, int32_t batch, void* out) {
+    if (!ctx) return fail(SWIFTKV_EINVAL, "null context");
+    if (!ctx->host_io) {
+        return exact ? run_exact(ctx, q, k, v, q17, kv, lut, act_q, act_scale, layer, positions, batch,
+                                 static_cast<int32_t*>(out))
+                     : run_step(ctx, q, k, v, q17, kv, lut, act_q, act_scale, layer, positions, batch,
+                                static_cast<float*>(out));
+    }
+    int rc = validate_step(ctx, q, k, v, kv, lut, act_q, act_scale, layer, positions, batch,
+                           static_cast<const float*>(out));
+    if (rc) return rc;
+    if ((rc = set_device(ctx))) return rc;
+    auto align = [](size_t x) { return (x + 255) & ~static_cast<size_t>(255); };
+    const size_t row_bytes = static_cast<size_t>(batch) * kModelDim * 4;
+    const size_t aq_bytes = static_cast<size_t>(batch) * kHeads * kGroupsPerHead * SWIFTKV_A14_WORD_BYTES;
+    const size_t as_bytes = static_cast<size_t>(batch) * kHeads * kGroupsPerHead;
+    const size_t off_out = 3 * align(row_bytes), off_aq = off_out + align(row_bytes);
+    const size_t off_as = off_aq + align(aq_bytes), total = off_as + align(as_bytes);
+    if ((rc = ensure(ctx, ctx->io_stage, ctx->io_bytes, total))) return rc;
+    uint8_t* st = ctx->io_stage;
+    SKV_HIP(hipMemcpyAsync(st, q, row_bytes, hipMemcpyHostToDevice, ctx->stream));
+    SKV_HIP(hipMemcpyAsync(st + align(row_bytes), k, row_bytes, hipMemcpyHostToDevice, ctx->stream));
+    SKV_HIP(hipMemcpyAsync(st + 2 * align(row_bytes), v, row_bytes, hipMemcpyHostToDevice, ctx->stream));
+    uint8_t* d_aq = act_q ? st + off_aq : nullptr;
+    uint8_t* d_as = act_scale ? st + off_as : nullptr;
+    rc = exact ? run_exact(ctx, st, st + align(row_bytes), st + 2 * align(row_bytes), q17, kv, lut, d_aq, d_as,
+                           layer, positions, batch, reinterpret_cast<int32_t*>(st + off_out))
+               : run_step(ctx, st, st + align(row_bytes), st + 2 * align(row_bytes), q17, kv, lut, d_aq, d_as,
+                          layer, positions, batch, reinterpret_cast<float*>(st + off_out));
+    if (rc) return rc;
+    SKV_HIP(hipMemcpyAsync(out, st + off_out, row_bytes, hipMemcpyDeviceToHost, ctx->stream));
+    if (act_q) {
+        SKV_HIP(hipMemcpyAsync(act_q, d_aq, aq_bytes, hipMemcpyDeviceToHost, ctx->stream));
+        SKV_HIP(hipMemcpyAsync(act_scale, d_as, as_bytes, hipMemcpyDeviceToHost, ctx->stream));
+    }
+    SKV_HIP(hipStreamSynchronize(ctx->stream));
     return ok();
 }
 
@@ -405,6 +467,7 @@ int swiftkv_context_destroy(swiftkv_context* ctx) {
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     if (ctx->partials) (void)hipFree(ctx->partials);
     if (ctx->counters) (void)hipFree(ctx->counters);
+    if (ctx->io_stage) (void)hipFree(ctx->io_stage);
     for (auto& t : ctx->timers)
         if (t) (void)hipEventDestroy(t);
     for (auto& p : ctx->profile_pool) {
@@ -433,6 +496,14 @@ int swiftkv_set_split_tokens(swiftkv_context* ctx, int32_t split_tokens) {
         return fail(SWIFTKV_EINVAL, "split_tokens %d must be 0 or a multiple of %d in [%d, %d]", split_tokens,
                     kSplitQuantum, kSplitQuantum, kMaxSplitTokens);
     ctx->split_tokens = split_tokens;
+    return ok();
+}
+
+int swiftkv_set_host_io(swiftkv_context* ctx, int32_t enable) {
+    if (!ctx) return fail(SWIFTKV_EINVAL, "null context");
+    int rc = not_capturing(ctx, "swiftkv_set_host_io");
+    if (rc) return rc;
+    ctx->host_io = enable != 0;
     return ok();
 }
 
@@ -662,24 +733,24 @@ int swiftkv_attention_f32(swiftkv_context* ctx, const float* q, const float* k, 
                           swiftkv_kv_cache* kv_cache, const swiftkv_rope_lut* rope_lut, uint8_t* activation_q,
                           uint8_t* activation_scale, int32_t layer_index, const int32_t* positions,
                           int32_t batch, float* out) {
-    return run_step(ctx, q, k, v, false, kv_cache, rope_lut, activation_q, activation_scale, layer_index,
-                    positions, batch, out);
+    return dispatch_step(ctx, false, q, k, v, false, kv_cache, rope_lut, activation_q, activation_scale, layer_index,
+                         positions, batch, out);
 }
 
 int swiftkv_attention_q17(swiftkv_context* ctx, const int32_t* q, const int32_t* k, const int32_t* v,
                           swiftkv_kv_cache* kv_cache, const swiftkv_rope_lut* rope_lut, uint8_t* activation_q,
                           uint8_t* activation_scale, int32_t layer_index, const int32_t* positions,
                           int32_t batch, float* out) {
-    return run_step(ctx, q, k, v, true, kv_cache, rope_lut, activation_q, activation_scale, layer_index,
-                    positions, batch, out);
+    return dispatch_step(ctx, false, q, k, v, true, kv_cache, rope_lut, activation_q, activation_scale, layer_index,
+                         positions, batch, out);
 }
 
 int swiftkv_attention_exact(swiftkv_context* ctx, const void* q, const void* k, const void* v, int32_t q17,
                             swiftkv_kv_cache* kv_cache, const swiftkv_rope_lut* rope_lut, uint8_t* activation_q,
                             uint8_t* activation_scale, int32_t layer_index, const int32_t* positions,
                             int32_t batch, int32_t* out_q17) {
-    return run_exact(ctx, q, k, v, q17 != 0, kv_cache, rope_lut, activation_q, activation_scale, layer_index,
-                     positions, batch, out_q17);
+    return dispatch_step(ctx, true, q, k, v, q17 != 0, kv_cache, rope_lut, activation_q, activation_scale,
+                         layer_index, positions, batch, out_q17);
 }
 
 int swiftkv_append_tokens(swiftkv_context* ctx, const void* k, const void* v, int32_t q17,
@@ -695,6 +766,15 @@ int swiftkv_append_tokens(swiftkv_context* ctx, const void* k, const void* v, in
                     rope_lut->positions);
     if (n == 0) return ok();
     if ((rc = set_device(ctx))) return rc;
+    const size_t rows_bytes = static_cast<size_t>(n) * kModelDim * 4;
+    if (ctx->host_io) {   // stage the host rows (see dispatch_step)
+        const size_t half = (rows_bytes + 255) & ~static_cast<size_t>(255);
+        if ((rc = ensure(ctx, ctx->io_stage, ctx->io_bytes, 2 * half))) return rc;
+        SKV_HIP(hipMemcpyAsync(ctx->io_stage, k, rows_bytes, hipMemcpyHostToDevice, ctx->stream));
+        SKV_HIP(hipMemcpyAsync(ctx->io_stage + half, v, rows_bytes, hipMemcpyHostToDevice, ctx->stream));
+        k = ctx->io_stage;
+        v = ctx->io_stage + half;
+    }
     BulkArgs a;
     a.k = k;
     a.v = v;
@@ -708,6 +788,7 @@ int swiftkv_append_tokens(swiftkv_context* ctx, const void* k, const void* v, in
     ProfilePair* p = profile_begin(ctx, SWIFTKV_KERNEL_APPEND);
     SKV_HIP(launch_append_bulk(a, q17 != 0, ctx->stream));
     profile_end(ctx, p);
+    if (ctx->host_io) SKV_HIP(hipStreamSynchronize(ctx->stream));   // the stage is reused by the next call
     return ok();
 }
 
@@ -824,6 +905,7 @@ int swiftkv_convert_f32_q17(swiftkv_context* ctx, const float* in, int32_t* out,
 int swiftkv_capture_begin(swiftkv_context* ctx) {
     if (!ctx) return fail(SWIFTKV_EINVAL, "null context");
     if (ctx->capturing) return fail(SWIFTKV_ESTATE, "a capture is already in progress");
+    if (ctx->host_io) return fail(SWIFTKV_ESTATE, "host-memory I/O mode cannot be captured: switch it off first");
     int rc = set_device(ctx);
     if (rc) return rc;
     SKV_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));

@@ -68,7 +68,12 @@ struct StepArgs {
     uint8_t* act_q;           // [batch][128][56] or null
     uint8_t* act_scale;       // [batch][128] or null
     int32_t positions[kMaxBatchPerLaunch];
+    // Dispatch order: workgroup row z serves sequence order[z].  The host
+    // sorts by descending position (longest first) so ragged batches do not
+    // end on a tail of long heads.
+    uint8_t order[kMaxBatchPerLaunch];
 };
+static_assert(kMaxBatchPerLaunch <= 256, "order[] holds sequence indices in 8 bits");
 
 // Bulk append of n tokens of one sequence (prefill).
 struct BulkArgs {

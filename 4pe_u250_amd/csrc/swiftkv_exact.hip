@@ -135,7 +135,7 @@ struct ExactArgs {
 template <bool Q17>
 __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
     const StepArgs& a = ea.step;
-    const int h = blockIdx.x, b = blockIdx.y;
+    const int h = blockIdx.x, b = a.order[blockIdx.y];
     const int pos = a.positions[b];
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int lane = threadIdx.x & 63;

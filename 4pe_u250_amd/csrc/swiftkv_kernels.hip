@@ -305,10 +305,10 @@ __device__ __forceinline__ float merge_partials(const float* part, int n) {
 
 // ---------------------------------------------------------------- step
 
-// Grid (splits, 32 heads, batch), 256 threads.
+// Grid (splits, 32 heads, batch), 256 threads; row z serves sequence order[z].
 template <bool Q17>
 __global__ __launch_bounds__(kAttendWaves * 64) void step_kernel(StepArgs a) {
-    const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int split = blockIdx.x, h = blockIdx.y, b = a.order[blockIdx.z];
     const int pos = a.positions[b];
     const int len = pos + 1;
     const int C = a.split_tokens;

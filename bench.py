@@ -16,8 +16,14 @@ Prints ONE JSON line.  value = algorithmic bytes of the step / step time
 (GB/s), where per (sequence, layer) at position p the step moves
 9216*p + 9216 + 65536 bytes (288 B per cached token-head + the appended row +
 FP32 q/k/v/out).  Also reported: us/layer, tokens/s, % of 8 TB/s, the batch-1
-figures, the split-attention kernel's roofline from per-launch hipEvents, and
-the reference emulator's attention stage timed on this host (cpu_baseline).
+figures (1% of K channels x20), the step kernel's roofline from per-launch
+hipEvents, the integer-compatibility entry's time on the same workload, the
+reference emulator's attention stage timed on this host (cpu_baseline), and
+the secondary configurations under "configs": batch 1 at position 127 (one
+layer), batch 1 at position 2047 (32 layers), batch 64 with attended lengths
+drawn from U{256..4096} (32 layers), batch 16 decoding 512 steps from
+position 32256 to 32767 on Student-t(3) data (one layer), and the batch-64
+call with host-memory inputs and outputs (PCIe included; never `value`).
 """
 import argparse
 import json
@@ -57,62 +63,98 @@ def profiled_traffic(batch: int, context: int):
     return None, None
 
 
-def run_gpu(skv, ctx, batch, context, layers, steps, warmup, seed, outliers=False):
-    pos = context - 1
-    lut = skv.RopeLut.generate(ctx, max(context, 4096))
-    kv = skv.KVCache(ctx, layers=layers, max_batch=batch, max_seq_len=context)
+def run_gpu(skv, ctx, positions, layers, steps, warmup, seed, outliers=False, dist=0, exact_steps=0,
+            graph=True, advance=False):
+    """Time `steps` decode steps of `layers` calls each over sequences at `positions`.
+
+    The cache is filled on the device to max(positions) tokens per sequence;
+    q/k/v for every layer are resident before timing.  With advance=True step
+    s runs at positions + s (a decode run whose appends feed the next step);
+    otherwise every step repeats the same positions (the appended row is
+    rewritten with the same bits).
+    """
+    positions = np.asarray(positions, np.int32)
+    batch = positions.size
+    cap = int(positions.max()) + (steps if advance else 1)   # last written position + 1
+    lut = skv.RopeLut.generate(ctx, max(cap, 4096))
+    kv = skv.KVCache(ctx, layers=layers, max_batch=batch, max_seq_len=cap)
     t0 = time.time()
-    kv.fill_synthetic(lut, ntok=pos, seed=seed, k_outliers=outliers)
+    kv.fill_synthetic(lut, ntok=int(positions.max()), seed=seed, dist=dist, k_outliers=outliers)
     ctx.synchronize()
     log(f"[bench] batch {batch}: filled {kv.nbytes / 1e9:.1f} GB cache ({layers} layers x {batch} seq x "
-        f"{pos} tokens) in {time.time() - t0:.1f} s")
+        f"{int(positions.max())} tokens) in {time.time() - t0:.1f} s")
     n_in = layers * batch * 4096
     qkv = [ctx.alloc(n_in * 4) for _ in range(3)]
     for i, buf in enumerate(qkv):
-        ctx.fill_synthetic(buf, n_in, seed + 1, 1000 + i, outliers=(outliers and i == 1))
+        ctx.fill_synthetic(buf, n_in, seed + 1, 1000 + i, dist=dist, outliers=(outliers and i == 1))
     out = ctx.alloc(batch * 4096 * 4)
     aq = ctx.alloc(batch * 128 * 56)
     asc = ctx.alloc(batch * 128)
-    positions = np.full(batch, pos, np.int32)
     layer_stride = batch * 4096 * 4
 
-    def one_step():
+    def one_step(pos):
         for layer in range(layers):
             off = layer * layer_stride
             skv.swiftkv_attention(ctx, qkv[0].ptr + off, qkv[1].ptr + off, qkv[2].ptr + off, kv, lut, aq, asc,
-                                  layer, positions, out)
+                                  layer, pos, out)
 
-    for _ in range(warmup):
-        one_step()
+    for _ in range(0 if advance else warmup):
+        one_step(positions)
     ctx.synchronize()
     ctx.profile(True)
     ctx.timer_record(0)
-    for _ in range(steps):
-        one_step()
+    for s in range(steps):
+        one_step(positions + s if advance else positions)
     ctx.timer_record(1)
     ms = ctx.timer_elapsed_ms(0, 1)
     counts, kms = ctx.profile_collect()
     ctx.profile(False)
-    # The same step recorded once into a HIP graph and replayed: the GPU-side
-    # time of the 32 per-layer calls without host launch overhead.
-    ctx.capture_begin()
-    one_step()
-    graph = ctx.capture_end()
-    for _ in range(warmup):
-        graph.launch()
-    ctx.timer_record(2)
-    for _ in range(steps):
-        graph.launch()
-    ctx.timer_record(3)
-    ms_graph = ctx.timer_elapsed_ms(2, 3)
-    graph.close()
+    ms_graph = None
+    if graph:
+        # The same step recorded once into a HIP graph and replayed: the
+        # GPU-side time of the per-layer calls without host launch overhead.
+        ctx.capture_begin()
+        one_step(positions)
+        g = ctx.capture_end()
+        for _ in range(warmup):
+            g.launch()
+        ctx.timer_record(2)
+        for _ in range(steps):
+            g.launch()
+        ctx.timer_record(3)
+        ms_graph = ctx.timer_elapsed_ms(2, 3)
+        g.close()
     o = out.download(np.float32, (batch, 4096))
     assert np.isfinite(o).all(), "non-finite attention output"
+    exact = None
+    if exact_steps:
+        # The integer-compatibility entry on the same workload (sequential
+        # recurrence per head; reported beside the fast path, not as `value`).
+        out_i = ctx.alloc(batch * 4096 * 4)
+
+        def exact_step():
+            for layer in range(layers):
+                off = layer * layer_stride
+                skv.swiftkv_attention_exact(ctx, qkv[0].ptr + off, qkv[1].ptr + off, qkv[2].ptr + off, kv, lut,
+                                            aq, asc, layer, positions, out_i)
+        exact_step()
+        ctx.timer_record(4)
+        for _ in range(exact_steps):
+            exact_step()
+        ctx.timer_record(5)
+        ms_exact = ctx.timer_elapsed_ms(4, 5)
+        oi = out_i.download(np.int32, (batch, 4096))
+        out_i.free()
+        err = float(np.abs(oi * 2.0 ** -17 - o.astype(np.float64)).max())
+        exact = {"us_per_layer": 1000.0 * ms_exact / exact_steps / layers,
+                 "gbps": exact_steps * layers * sum(step_bytes(int(p)) for p in positions) / (ms_exact / 1e3) / 1e9,
+                 "max_abs_diff_vs_fp32_path": err}
     for b in qkv + [out, aq, asc]:
         b.free()
     kv.close()
     lut.close()
-    total_bytes = steps * layers * batch * step_bytes(pos)
+    step_total = [sum(step_bytes(int(p) + (s if advance else 0)) for p in positions) for s in range(steps)]
+    total_bytes = layers * sum(step_total)
     ms_step = ms / steps
     res = {
         "ms_per_step": ms_step,
@@ -121,18 +163,74 @@ def run_gpu(skv, ctx, batch, context, layers, steps, warmup, seed, outliers=Fals
         "tokens_per_s": batch * steps / (ms / 1e3),
         "kernel_launches": dict(zip(["append", "step"], counts)),
         "kernel_avg_us": {k: (1000.0 * t / c if c else None) for k, t, c in zip(["append", "step"], kms, counts)},
+        "exact": exact,
+        "sum_attended": int(sum(int(p) + 1 for p in positions)),
     }
     res["pct_of_peak"] = 100.0 * res["gbps"] / HBM_PEAK_GBPS
-    res["graph"] = {"us_per_layer": 1000.0 * ms_graph / steps / layers,
-                    "gbps": total_bytes / (ms_graph / 1e3) / 1e9,
-                    "tokens_per_s": batch * steps / (ms_graph / 1e3)}
-    res["graph"]["pct_of_peak"] = 100.0 * res["graph"]["gbps"] / HBM_PEAK_GBPS
+    if ms_graph is not None:
+        res["graph"] = {"us_per_layer": 1000.0 * ms_graph / steps / layers,
+                        "gbps": total_bytes / (ms_graph / 1e3) / 1e9,
+                        "tokens_per_s": batch * steps / (ms_graph / 1e3)}
+        res["graph"]["pct_of_peak"] = 100.0 * res["graph"]["gbps"] / HBM_PEAK_GBPS
     # dominant kernel: the step kernel moves the whole step's algorithmic bytes
     # (cached tokens, appended row, q/k/v in, output out)
     step_avg_s = kms[1] / counts[1] / 1e3
-    res["step_kernel_gbps"] = batch * step_bytes(pos) / step_avg_s / 1e9
-    res["dominant_bytes_per_launch"] = batch * step_bytes(pos)
+    res["dominant_bytes_per_launch"] = sum(step_total) // steps
+    res["step_kernel_gbps"] = res["dominant_bytes_per_launch"] / step_avg_s / 1e9
     return res
+
+
+def run_host_io(skv, ctx, batch, context, reps, seed):
+    """The per-layer call with host-memory q/k/v/out/A14 (pageable numpy
+    arrays): copies in, step, copies out, wait -- the PCIe-inclusive rate."""
+    pos = context - 1
+    lut = skv.RopeLut.generate(ctx, max(context, 4096))
+    kv = skv.KVCache(ctx, layers=1, max_batch=batch, max_seq_len=context)
+    kv.fill_synthetic(lut, ntok=pos, seed=seed)
+    ctx.synchronize()
+    rng = np.random.default_rng(seed)
+    q, k, v = (rng.standard_normal((batch, 4096)).astype(np.float32) for _ in range(3))
+    out = np.empty((batch, 4096), np.float32)
+    aq, asc = np.empty((batch, 128, 56), np.uint8), np.empty((batch, 128), np.uint8)
+    positions = np.full(batch, pos, np.int32)
+    ctx.set_host_io(True)
+    times = []
+    try:
+        for i in range(reps + 2):
+            t0 = time.perf_counter()
+            skv.swiftkv_attention(ctx, q, k, v, kv, lut, aq, asc, 0, positions, out)
+            if i >= 2:
+                times.append(time.perf_counter() - t0)
+    finally:
+        ctx.set_host_io(False)
+    kv.close()
+    lut.close()
+    assert np.isfinite(out).all()
+    t = float(np.median(times))
+    return {"us_per_layer": round(t * 1e6, 1), "gbps": round(batch * step_bytes(pos) / t / 1e9, 1),
+            "host_bytes_per_layer": int(q.nbytes * 3 + out.nbytes + aq.nbytes + asc.nbytes),
+            "sample": f"median of {reps} synchronous calls, one layer, pageable host arrays"}
+
+
+def summary(res, graph=True):
+    """The figures reported for a secondary configuration."""
+    d = {"us_per_layer": round(res["us_per_layer"], 3), "gbps": round(res["gbps"], 1),
+         "pct_of_peak": round(res["pct_of_peak"], 2), "tokens_per_s": round(res["tokens_per_s"], 1),
+         "step_kernel_avg_us": round(res["kernel_avg_us"]["step"], 2),
+         "step_kernel_gbps": round(res["step_kernel_gbps"], 1)}
+    if graph and "graph" in res:
+        d["graph_replay"] = {k: round(v, 3) for k, v in res["graph"].items()}
+    return d
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def cpu_baseline(target_seconds: float, position: int, omp: bool):
@@ -168,6 +266,8 @@ def cpu_baseline(target_seconds: float, position: int, omp: bool):
         "us_per_layer_batch1": per_call * 1e6,
         "us_per_layer_batch64": per_call * 64 * 1e6,
         "cores": R.L.ref_omp_threads(),
+        "cpu_model": cpu_model(),
+        "nproc": os.cpu_count(),
         "kind": "reference",
         "sample": (f"{len(times)} calls of the reference emulator's swiftkv_attention_4pe (32 heads, one "
                    f"sequence, one layer, position {position}), median; batch-64 figure = 64 x per-call"),
@@ -186,6 +286,10 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-batch1", action="store_true")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the secondary configurations (position 127, 2047, ragged, 32K)")
+    ap.add_argument("--exact-steps", type=int, default=1,
+                    help="steps of the integer-compatibility entry to time (0 = skip)")
     ap.add_argument("--calibrate", action="store_true",
                     help="only run the FP32->Q15.17 conversion kernel over 256 Mi elements (a copy of known "
                          "size: 1 GiB read, 1 GiB written per launch) to scale HBM byte counters")
@@ -211,14 +315,37 @@ def main():
         return
     ctx.set_split_tokens(args.split)
     log(f"[bench] {skv.version()}")
-    main_res = run_gpu(skv, ctx, args.batch, args.context, args.layers, args.steps, args.warmup, seed=2026)
+    main_res = run_gpu(skv, ctx, np.full(args.batch, args.context - 1), args.layers, args.steps, args.warmup,
+                       seed=2026, exact_steps=args.exact_steps)
     log(f"[bench] batch {args.batch}: {main_res['us_per_layer']:.1f} us/layer, {main_res['gbps']:.0f} GB/s "
         f"(graph replay {main_res['graph']['us_per_layer']:.1f} us/layer)")
     b1 = None
+    extra = {}
     if not args.no_batch1:
-        b1 = run_gpu(skv, ctx, 1, args.context, args.layers, max(args.steps, 20), args.warmup, seed=2027)
+        # batch-1 headline: 1% of K channels x20
+        b1 = run_gpu(skv, ctx, [args.context - 1], args.layers, max(args.steps, 20), args.warmup, seed=2027,
+                     outliers=True)
         log(f"[bench] batch 1: {b1['us_per_layer']:.2f} us/layer, {b1['gbps']:.0f} GB/s "
             f"(graph replay {b1['graph']['us_per_layer']:.2f} us/layer)")
+    if not args.no_configs:
+        r = run_gpu(skv, ctx, [127], 1, 200, args.warmup, seed=2028)
+        extra["batch1_position127_1layer"] = summary(r)
+        r = run_gpu(skv, ctx, [2047], 32, 20, args.warmup, seed=2029)
+        extra["batch1_position2047_32layers"] = summary(r)
+        rng = np.random.default_rng(4)
+        lengths = rng.integers(256, 4097, 64)
+        r = run_gpu(skv, ctx, lengths - 1, 32, args.steps, args.warmup, seed=2030)
+        extra["batch64_ragged_32layers"] = dict(summary(r), length_seed=4, sum_attended=r["sum_attended"],
+                                                lengths="U{256..4096}")
+        r = run_gpu(skv, ctx, np.full(16, 32256), 1, 512, 0, seed=2031, dist=skv.DIST_STUDENT_T3, graph=False,
+                    advance=True)
+        extra["batch16_positions32256to32767_1layer_t3"] = dict(summary(r, graph=False),
+                                                                 steps=512, ms_total=round(r["ms_per_step"] * 512, 2))
+        for k, v in extra.items():
+            log(f"[bench] {k}: {v['us_per_layer']:.2f} us/layer, {v['gbps']:.0f} GB/s")
+        extra["batch64_position4095_host_io"] = run_host_io(skv, ctx, args.batch, args.context, 20, seed=2032)
+        log(f"[bench] host-memory I/O, batch {args.batch}: "
+            f"{extra['batch64_position4095_host_io']['us_per_layer']:.1f} us/layer")
     ctx.close()
 
     cpu = None
@@ -263,11 +390,14 @@ def main():
                      "avg_launch_us": round(att, 2) if att else None},
         "cpu_baseline": cpu,
     }
+    if main_res["exact"]:
+        e = main_res["exact"]
+        line["integer_exact_path"] = {"us_per_layer": round(e["us_per_layer"], 1), "gbps": round(e["gbps"], 1),
+                                      "max_abs_diff_vs_fp32_path": e["max_abs_diff_vs_fp32_path"]}
     if b1:
-        line["batch1"] = {"us_per_layer": round(b1["us_per_layer"], 3), "gbps": round(b1["gbps"], 1),
-                          "pct_of_peak": round(b1["pct_of_peak"], 2), "tokens_per_s": round(b1["tokens_per_s"], 1),
-                          "kernel_avg_us": {k: (round(v, 2) if v else v) for k, v in b1["kernel_avg_us"].items()},
-                          "graph_replay": {k: round(v, 3) for k, v in b1["graph"].items()}}
+        line["batch1"] = dict(summary(b1), workload="32 layers x batch 1 x position 4095, 1% of K channels x20")
+    if extra:
+        line["configs"] = extra
     print(json.dumps(line), flush=True)
 
 

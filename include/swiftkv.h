@@ -182,6 +182,16 @@ int swiftkv_attention_exact(swiftkv_context* ctx, const void* q, const void* k, 
                             uint8_t* activation_q, uint8_t* activation_scale, int32_t layer_index,
                             const int32_t* positions, int32_t batch, int32_t* out_q17);
 
+/* Host-memory I/O mode (default off).  When on, the q/k/v, out and
+ * activation pointers of swiftkv_attention_f32/_q17/_exact and the k/v of
+ * swiftkv_append_tokens are host memory: the call stages them through a
+ * context-owned device buffer on the context stream and returns after its
+ * outputs are back in host memory (the reference host's DMA-in / run /
+ * DMA-out around each PE call, decode_host.cpp:1358-1485).  Pinned host
+ * memory copies fastest.  Not allowed during graph capture, and a capture
+ * cannot begin while it is on (SWIFTKV_ESTATE). */
+int swiftkv_set_host_io(swiftkv_context* ctx, int32_t enable);
+
 /* Bulk append (prompt prefill): apply the append rule -- conversion, RoPE of
  * k at its own position, G32 quantization -- to n tokens [pos0, pos0+n) of
  * one sequence without attending.  k, v: device [n][4096], FP32 when

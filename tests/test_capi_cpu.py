@@ -57,6 +57,9 @@ def test_null_and_range_checks_without_device(skv):
     counts = (C.c_int64 * skv.KERNEL_KINDS)()
     ms = (C.c_double * skv.KERNEL_KINDS)()
     assert L.swiftkv_profile_collect(None, counts, ms) == skv.EINVAL
+    assert L.swiftkv_set_host_io(None, 1) == skv.EINVAL
+    assert L.swiftkv_attention_exact(None, None, None, None, 0, None, None, None, None, 0,
+                                     pos.ctypes.data_as(C.c_void_p), 1, None) == skv.EINVAL
     # destroy functions accept null like free()
     assert L.swiftkv_context_destroy(None) == skv.OK
     assert L.swiftkv_kv_cache_destroy(None) == skv.OK
@@ -82,3 +85,21 @@ def test_scale_bits(skv, oracle):
     s = np.arange(26, dtype=np.uint8)
     assert (skv.scale_bits(s) == oracle.shift_scale_bits(s)).all()
     assert (skv.scale_bits(s).view(np.float32) == np.ldexp(np.float32(1), s.astype(int) - 17)).all()
+
+
+def test_host_arrays_need_host_io_mode(skv):
+    """A numpy array is host memory: the mirror refuses to hand it to a kernel
+    unless the context is in host-memory I/O mode."""
+    with pytest.raises(TypeError):
+        skv._ptr(np.zeros(4, np.float32))
+
+    class FakeCtx:
+        host_io = True
+    a = np.zeros(8, np.float32)
+    assert skv._io_ptr(FakeCtx, a, np.float32) == a.ctypes.data
+    with pytest.raises(TypeError):
+        skv._io_ptr(FakeCtx, a, np.int32)
+    with pytest.raises(ValueError):
+        skv._io_ptr(FakeCtx, np.zeros((4, 4), np.float32)[:, ::2], np.float32)
+    with pytest.raises(ValueError):
+        skv._check_io_sizes(FakeCtx, 2, np.zeros(4096, np.float32), None, None, None, None, None)

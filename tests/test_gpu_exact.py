@@ -154,3 +154,51 @@ def test_exact_and_fast_path_agree(skv, ctx, lut4096, rope_tables):
     kv.close()
     err = np.abs(out_i[0] * 2.0 ** -17 - out_f[0].astype(np.float64))
     assert err.max() < 2e-3 * max(1.0, np.abs(out_f).max()), err.max()
+
+
+def test_host_io_mode_matches_device_mode(skv, ctx, lut4096):
+    """Host-memory I/O stages through the device and returns the same bits as
+    the device-pointer call, for the FP32, Q15.17 and exact entries and the
+    bulk append."""
+    _note("case: host-memory I/O vs device pointers, batch 3")
+    positions = [5, 300, 64]
+    B = len(positions)
+    kv = skv.KVCache(ctx, layers=1, max_batch=B, max_seq_len=301)
+    kvh = skv.KVCache(ctx, layers=1, max_batch=B, max_seq_len=301)
+    for b, p in enumerate(positions):
+        kh, vh = history(70 + b, p)
+        prefill(skv, ctx, kv, lut4096, 0, b, kh, vh)
+        ctx.set_host_io(True)
+        try:
+            skv.swiftkv_append_tokens(ctx, np.ascontiguousarray(kh), np.ascontiguousarray(vh), kvh, lut4096, 0,
+                                      b, 0, p)
+        finally:
+            ctx.set_host_io(False)
+    q, k, v = (f32_normal(80 + i, (B, 4096)) for i in range(3))
+    ref = []
+    for fn, args, odt in ((skv.swiftkv_attention, (q, k, v), np.float32),
+                          (skv.swiftkv_attention, tuple(O.f2q17(x) for x in (q, k, v)), np.float32),
+                          (skv.swiftkv_attention_exact, (q, k, v), np.int32)):
+        q17 = args[0].dtype == np.int32
+        dq, dk, dv = (ctx.to_device(x) for x in args)
+        out, aq, asc = ctx.alloc(B * 4096 * 4), ctx.alloc(B * 128 * 56), ctx.alloc(B * 128)
+        fn(ctx, dq, dk, dv, kv, lut4096, aq, asc, 0, positions, out, q17=q17)
+        ctx.synchronize()
+        ref = (out.download(odt, (B, 4096)), aq.download(np.uint8, (B, 128, 56)), asc.download(np.uint8, (B, 128)))
+        for buf in (dq, dk, dv, out, aq, asc):
+            buf.free()
+        hout, haq, hasc = np.zeros((B, 4096), odt), np.zeros((B, 128, 56), np.uint8), np.zeros((B, 128), np.uint8)
+        ctx.set_host_io(True)
+        try:
+            fn(ctx, *(np.ascontiguousarray(x) for x in args), kvh, lut4096, haq, hasc, 0, positions, hout, q17=q17)
+            with pytest.raises(skv.SwiftKVError):
+                ctx.capture_begin()
+        finally:
+            ctx.set_host_io(False)
+        assert (hout == ref[0]).all() and (haq == ref[1]).all() and (hasc == ref[2]).all(), fn.__name__
+    for b, p in enumerate(positions):
+        for h in (0, 17, 31):
+            got, want = kvh.read(b, 0, h, 0, p + 1), kv.read(b, 0, h, 0, p + 1)
+            assert all((x == y).all() for x, y in zip(got, want)), f"seq {b} head {h}"
+    kv.close()
+    kvh.close()
