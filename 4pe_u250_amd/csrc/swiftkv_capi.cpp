@@ -74,7 +74,7 @@ struct swiftkv_context {
     // split-context workspace
     float* partials = nullptr;
     size_t partial_elems = 0;
-    uint32_t* counters = nullptr;   // [kMaxBatchPerLaunch][32] split arrivals, zero between launches
+    uint32_t* counters = nullptr;   // [kMaxBatchPerLaunch][32] split arrivals (kCounterStride apart), zero between launches
     // timing
     hipEvent_t timers[kTimerSlots] = {};
     bool profiling = false;
@@ -200,26 +200,31 @@ int upload_lut(swiftkv_context* ctx, std::vector<int2>&& host, int32_t positions
 // 256 CUs): split a head only when batch x 32 heads is below that, and never
 // below one 256-token quantum.  A head held by one split skips the partial
 // exchange, which is worth more than the finer tail of smaller splits (batch
-// 64 at context 4096: one split per head ran 378 us/layer, 1024-token splits
-// 385 us/layer including their merge).
+// 64 at context 4096: one split per head ran 369 us/layer, 2048-token splits
+// 377 and 1024-token splits 395 us/layer).  At most kMaxSplitsPerHead splits:
+// at batch 1 the merge's latency grows with the split count faster than the
+// shorter scans save (context 4096: 8 splits 14.5 us, 16 splits 15.7 us).
+constexpr int64_t kMaxSplitsPerHead = 8;
+
 int32_t choose_split(const swiftkv_context* ctx, const int32_t* positions, int32_t batch) {
     if (ctx->split_tokens > 0) return ctx->split_tokens;
     int32_t max_len = 1;
     for (int32_t b = 0; b < batch; ++b) max_len = std::max(max_len, positions[b] + 1);
     const int64_t heads = static_cast<int64_t>(batch) * kHeads;
-    const int64_t splits_per_head = std::max<int64_t>(1, (2048 + heads - 1) / heads);
+    const int64_t splits_per_head =
+        std::min<int64_t>(kMaxSplitsPerHead, std::max<int64_t>(1, (2048 + heads - 1) / heads));
     const int64_t tokens = (max_len + splits_per_head - 1) / splits_per_head;
     const int64_t quanta = std::max<int64_t>(1, (tokens + kSplitQuantum - 1) / kSplitQuantum);
     return static_cast<int32_t>(std::min<int64_t>(quanta * kSplitQuantum, kMaxSeq));
 }
 
-// Longest-first dispatch order for one launch's sequences (stable, so a
-// uniform batch keeps its natural order).
-void set_order(StepArgs& a) {
+// Dispatch rows of one launch: (position, sequence) longest first (stable,
+// so a uniform batch keeps its natural order).
+void set_rows(StepArgs& a, const int32_t* positions) {
     int32_t idx[kMaxBatchPerLaunch];
     for (int32_t b = 0; b < a.batch; ++b) idx[b] = b;
-    std::stable_sort(idx, idx + a.batch, [&](int32_t x, int32_t y) { return a.positions[x] > a.positions[y]; });
-    for (int32_t b = 0; b < a.batch; ++b) a.order[b] = static_cast<uint8_t>(idx[b]);
+    std::stable_sort(idx, idx + a.batch, [&](int32_t x, int32_t y) { return positions[x] > positions[y]; });
+    for (int32_t z = 0; z < a.batch; ++z) a.rows[z] = pack_row(idx[z], positions[idx[z]]);
 }
 
 int validate_step(swiftkv_context* ctx, const void* q, const void* k, const void* v,
@@ -279,12 +284,9 @@ int run_step(swiftkv_context* ctx, const void* q, const void* k, const void* v, 
         a.batch = nb;
         a.slot0 = b0;
         int32_t max_pos = 0;
-        for (int32_t b = 0; b < nb; ++b) {
-            a.positions[b] = positions[b0 + b];
-            max_pos = std::max(max_pos, a.positions[b]);
-        }
-        set_order(a);
-        a.split_tokens = choose_split(ctx, a.positions, nb);
+        for (int32_t b = 0; b < nb; ++b) max_pos = std::max(max_pos, positions[b0 + b]);
+        set_rows(a, positions + b0);
+        a.split_tokens = choose_split(ctx, positions + b0, nb);
         const int32_t grid_splits = (max_pos + 1 + a.split_tokens - 1) / a.split_tokens;
         a.max_splits = grid_splits;
         if ((rc = ensure(ctx, ctx->partials, ctx->partial_elems,
@@ -336,8 +338,7 @@ int run_exact(swiftkv_context* ctx, const void* q, const void* k, const void* v,
         a.layer = layer;
         a.batch = nb;
         a.slot0 = b0;
-        for (int32_t b = 0; b < nb; ++b) a.positions[b] = positions[b0 + b];
-        set_order(a);
+        set_rows(a, positions + b0);
         a.out = reinterpret_cast<float*>(out + row0);
         a.act_q = act_q ? act_q + static_cast<size_t>(b0) * kHeads * kGroupsPerHead * SWIFTKV_A14_WORD_BYTES
                         : nullptr;
@@ -445,7 +446,7 @@ int swiftkv_context_create(int device, swiftkv_context** out) {
     ctx->device = device;
     hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
     for (int i = 0; e == hipSuccess && i < kTimerSlots; ++i) e = hipEventCreate(&ctx->timers[i]);
-    const size_t counter_bytes = sizeof(uint32_t) * kMaxBatchPerLaunch * kHeads;
+    const size_t counter_bytes = sizeof(uint32_t) * kMaxBatchPerLaunch * kHeads * kCounterStride;
     if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&ctx->counters), counter_bytes);
     if (e == hipSuccess) e = hipMemset(ctx->counters, 0, counter_bytes);
     if (e != hipSuccess) {

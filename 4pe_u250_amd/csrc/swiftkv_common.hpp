@@ -32,6 +32,10 @@ constexpr int kPartialStride = 4 + kHeadDim;     // (m, l, pad, pad, acc[128]) f
 constexpr int kMaxSeq = 32768;                   // longest cache this build accepts
 constexpr int kMaxSplits = kMaxSeq / kSplitQuantum;   // 128 partials per (sequence, head)
 
+// Split-arrival counters sit one per 128-byte cache line: the splits of all
+// heads finish together, and counters sharing a line serialize their atomics.
+constexpr int kCounterStride = 32;               // uint32 words
+
 // Sequences per launch: positions travel by value in the kernel arguments.
 constexpr int kMaxBatchPerLaunch = 256;
 
@@ -63,17 +67,22 @@ struct StepArgs {
     int32_t split_tokens;     // multiple of kSplitQuantum
     int32_t max_splits;       // partial slots per (sequence, head)
     float* partials;          // [batch][32][max_splits][kPartialStride]
-    uint32_t* counters;       // [batch][32] split arrivals, zero between launches
+    uint32_t* counters;       // [batch][32] split arrivals, one per kCounterStride words; zero between launches
     float* out;               // [batch][4096]
     uint8_t* act_q;           // [batch][128][56] or null
     uint8_t* act_scale;       // [batch][128] or null
-    int32_t positions[kMaxBatchPerLaunch];
-    // Dispatch order: workgroup row z serves sequence order[z].  The host
-    // sorts by descending position (longest first) so ragged batches do not
-    // end on a tail of long heads.
-    uint8_t order[kMaxBatchPerLaunch];
+    // Dispatch row z serves sequence rows[z] & 0xff at position rows[z] >> 8
+    // (one scalar load gives both).  The host orders rows by descending
+    // position, longest first, so ragged batches do not end on a tail of long
+    // heads.
+    uint32_t rows[kMaxBatchPerLaunch];
 };
-static_assert(kMaxBatchPerLaunch <= 256, "order[] holds sequence indices in 8 bits");
+static_assert(kMaxBatchPerLaunch <= 256, "rows[] holds sequence indices in 8 bits");
+static_assert(kMaxSeq <= (1 << 24), "rows[] holds positions in 24 bits");
+
+__host__ __device__ inline uint32_t pack_row(int seq, int pos) {
+    return (static_cast<uint32_t>(pos) << 8) | static_cast<uint32_t>(seq);
+}
 
 // Bulk append of n tokens of one sequence (prefill).
 struct BulkArgs {

@@ -11,27 +11,23 @@ namespace dev {
 
 // ---------------------------------------------------------------- numerics
 
-// FP32 -> Q15.17 with round-half-even and saturation, on the bit pattern
-// (int4_linear_controller.cpp:38-83): |x| < 2^-18 -> 0, |x| >= 2^14 (and
-// inf/nan) -> saturate by sign.
+// FP32 -> Q15.17 with round-half-even and saturation.  The reference states
+// it on the bit pattern (int4_linear_controller.cpp:38-83): exponent < 109
+// (|x| < 2^-18) -> 0, exponent >= 141 (|x| >= 2^14, inf, nan) -> saturate by
+// sign, otherwise RNE of sig >> (133 - e) or sig << (e - 133).  The same
+// value, branch-free: x * 2^17 is exact (a power-of-two scaling; it overflows
+// to inf only where the rule saturates anyway), v_rndne_f32 rounds it
+// half-even to an integer exactly, and v_cvt_i32_f32 clamps out-of-range
+// values to INT32_MIN/INT32_MAX.  Every |x| < 2^-18 rounds to 0 and every
+// |x| >= 2^14 clamps, so only NaN (which the conversion maps to 0) needs
+// its sign-saturated value put back.
 __device__ __forceinline__ int32_t f32_to_q17(float x) {
+    const float r = __builtin_rintf(x * 131072.0f);
+    int32_t v;
+    asm("v_cvt_i32_f32 %0, %1" : "=v"(v) : "v"(r));
     const uint32_t b = __float_as_uint(x);
-    const uint32_t e = (b >> 23) & 0xffu;
-    const bool neg = (b >> 31) != 0u;
-    if (e < 109u) return 0;
-    if (e >= 141u) return neg ? INT32_MIN : INT32_MAX;
-    const uint32_t sig = (1u << 23) | (b & 0x7fffffu);
-    uint32_t mag;
-    if (e >= 133u) {
-        mag = sig << (e - 133u);                 // < 2^31 for e <= 140
-    } else {
-        const uint32_t sh = 133u - e;            // 1..24
-        const uint32_t half = 1u << (sh - 1u);
-        const uint32_t rem = sig & ((half << 1) - 1u);
-        mag = sig >> sh;
-        mag += (rem > half || (rem == half && (mag & 1u))) ? 1u : 0u;
-    }
-    return neg ? -static_cast<int32_t>(mag) : static_cast<int32_t>(mag);
+    if ((b & 0x7fffffffu) > 0x7f800000u) v = (b >> 31) ? INT32_MIN : INT32_MAX;
+    return v;
 }
 
 __device__ __forceinline__ int32_t sat32(int64_t x) {

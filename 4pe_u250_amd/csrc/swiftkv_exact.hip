@@ -135,8 +135,9 @@ struct ExactArgs {
 template <bool Q17>
 __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
     const StepArgs& a = ea.step;
-    const int h = blockIdx.x, b = a.order[blockIdx.y];
-    const int pos = a.positions[b];
+    const uint32_t row = a.rows[blockIdx.y];
+    const int h = blockIdx.x, b = static_cast<int>(row & 0xffu);
+    const int pos = static_cast<int>(row >> 8);
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int lane = threadIdx.x & 63;
     const int c = lane & 7, r = lane >> 3;

@@ -305,11 +305,12 @@ __device__ __forceinline__ float merge_partials(const float* part, int n) {
 
 // ---------------------------------------------------------------- step
 
-// Grid (splits, 32 heads, batch), 256 threads; row z serves sequence order[z].
+// Grid (splits, 32 heads, batch), 256 threads; grid row z serves rows[z].
 template <bool Q17>
 __global__ __launch_bounds__(kAttendWaves * 64) void step_kernel(StepArgs a) {
-    const int split = blockIdx.x, h = blockIdx.y, b = a.order[blockIdx.z];
-    const int pos = a.positions[b];
+    const uint32_t row = a.rows[blockIdx.z];
+    const int split = blockIdx.x, h = blockIdx.y, b = static_cast<int>(row & 0xffu);
+    const int pos = static_cast<int>(row >> 8);
     const int len = pos + 1;
     const int C = a.split_tokens;
     const int t_begin = split * C;
@@ -338,8 +339,11 @@ __global__ __launch_bounds__(kAttendWaves * 64) void step_kernel(StepArgs a) {
     const PageReader pr = make_reader(page, cap, c, r);
     const int t_first = t_begin + wave * kBlockTokens;
     const int t_stop = owner ? pos : t_end;
+    // A wave with no tokens loads the split's first block (always in the page)
+    // and discards it: every path then has the same loads in flight, so the
+    // wait for the query does not also wait for this block.
     BlockLoads bl;
-    if (t_first < t_stop) issue_block(pr, t_first, bl);
+    issue_block(pr, t_first < t_stop ? t_first : t_begin, bl);
 
     // The new row's inputs are fetched now; its math runs after the scan, so
     // the fetch latency hides under the cache stream.
@@ -420,13 +424,13 @@ __global__ __launch_bounds__(kAttendWaves * 64) void step_kernel(StepArgs a) {
     __syncthreads();
     __shared__ int s_last;
     if (threadIdx.x == 0)
-        s_last = __hip_atomic_fetch_add(a.counters + head_row, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+        s_last = __hip_atomic_fetch_add(a.counters + head_row * kCounterStride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                  static_cast<unsigned>(nsplit - 1);
     __syncthreads();
     if (!s_last) return;
     finalize_head(a, b, h, merge_partials(parts, nsplit));
     if (threadIdx.x == 0)   // ready for the next launch
-        __hip_atomic_store(a.counters + head_row, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(a.counters + head_row * kCounterStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------- utilities
