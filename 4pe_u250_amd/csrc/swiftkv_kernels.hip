@@ -270,37 +270,43 @@ __device__ __forceinline__ float fetch(const float* p) {
 }
 
 // Log-sum-exp merge of n split partials; threads d < 128 get output channel d.
-// Split statistics are fetched in parallel (thread j loads split j), so the
-// merge costs two dependent memory round trips whatever n is.
+// Every load of the merge goes out at once -- the split statistics (thread j
+// loads split j) and thread d's accumulator column of the first kMergeInline
+// splits -- so up to kMergeInline splits cost one memory round trip and one
+// barrier.  Further splits (only when a caller forces small splits) are
+// fetched in a second pass.  Every thread reduces the statistics in the same
+// order, so all agree on the maximum and the denominator.
+constexpr int kMergeInline = 8;
+
 __device__ __forceinline__ float merge_partials(const float* part, int n) {
     const int d = threadIdx.x;
-    __shared__ float s_m[kMaxSplits], s_l[kMaxSplits], s_w[kMaxSplits];
-    __shared__ float s_mx, s_den;
+    __shared__ float s_m[kMaxSplits], s_l[kMaxSplits];
+    float col[kMergeInline];
     if (d < n) {
         s_m[d] = fetch(part + d * kPartialStride);
         s_l[d] = fetch(part + d * kPartialStride + 1);
     }
+#pragma unroll
+    for (int j = 0; j < kMergeInline; ++j)
+        col[j] = (d < kHeadDim && j < n) ? fetch(part + j * kPartialStride + 4 + d) : 0.0f;
     __syncthreads();
-    if (d == 0) {
-        float mx = s_m[0];
-        for (int j = 1; j < n; ++j) mx = fmaxf(mx, s_m[j]);
-        s_mx = mx;
+    float mx = s_m[0];
+    for (int j = 1; j < n; ++j) mx = fmaxf(mx, s_m[j]);
+    float den = 0.0f, num = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kMergeInline; ++j) {
+        if (j < n) {
+            const float w = fast_exp2(s_m[j] - mx);
+            den += w * s_l[j];
+            num += w * col[j];
+        }
     }
-    __syncthreads();
-    if (d < n) s_w[d] = fast_exp2(s_m[d] - s_mx);
-    __syncthreads();
-    if (d == 0) {
-        float den = 0.0f;
-        for (int j = 0; j < n; ++j) den += s_w[j] * s_l[j];
-        s_den = den;
+    for (int j = kMergeInline; j < n; ++j) {
+        const float w = fast_exp2(s_m[j] - mx);
+        den += w * s_l[j];
+        if (d < kHeadDim) num += w * fetch(part + j * kPartialStride + 4 + d);
     }
-    float num = 0.0f;
-    if (d < kHeadDim) {
-#pragma unroll 8
-        for (int j = 0; j < n; ++j) num += s_w[j] * fetch(part + j * kPartialStride + 4 + d);
-    }
-    __syncthreads();
-    return num / s_den;
+    return num / den;
 }
 
 // ---------------------------------------------------------------- step
