@@ -133,6 +133,29 @@ def test_exact_matches_oracle_integer_recurrence(skv, ctx, lut4096, rope_tables,
     kv.close()
 
 
+def test_exact_batch_over_one_launch(skv, ctx, lut4096, rope_tables):
+    """The exact entry over 260 sequences (two launches), against the oracle's
+    integer recurrence on a sample of sequences from both launches."""
+    _note("case: exact, batch 260, positions 0..40")
+    cos, sin = rope_tables
+    positions = [int(p) for p in np.random.default_rng(260).integers(0, 41, 260)]
+    B = len(positions)
+    kv = skv.KVCache(ctx, layers=1, max_batch=B, max_seq_len=64)
+    hist = [history(7000 + 10 * b, p) for b, p in enumerate(positions)]
+    for b, (kh, vh) in enumerate(hist):
+        prefill(skv, ctx, kv, lut4096, 0, b, kh, vh)
+    q, k, v = (O.f2q17(f32_normal(7001 + i, (B, 4096))) for i in range(3))
+    out, aq, asc = exact_step(skv, ctx, kv, lut4096, 0, positions, q, k, v, q17=True)
+    for b in (0, 1, 128, 255, 256, 257, 259):
+        p = positions[b]
+        sc = oracle_sequence(cos, sin, hist[b][0], hist[b][1], p + 1)
+        res = sc.step_q17(q[b], k[b], v[b], p, cos[p], sin[p], fp=False, integer=True)
+        assert (out[b] == res["int"].reshape(4096)).all(), f"seq {b} position {p}"
+        q14, e8 = O.a14_q17(res["int"].reshape(128, 32))
+        assert (asc[b] == e8).all() and (aq[b] == O.pack_a14(q14)).all(), f"seq {b}: A14"
+    kv.close()
+
+
 def test_exact_and_fast_path_agree(skv, ctx, lut4096, rope_tables):
     """Same cache, same inputs: the integer recurrence (LUT exp, 18-bit
     reciprocal) and the FP32 path land within the integer path's own error."""

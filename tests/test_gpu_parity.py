@@ -85,6 +85,15 @@ def test_batch_positions_edges(skv, ctx, lut4096, rope_tables, split):
               cap=320, split=split)
 
 
+def test_batch_over_one_launch(skv, ctx, lut4096, rope_tables):
+    """300 ragged sequences: two launches of at most 256 sequences each, every
+    launch ordering its rows longest first."""
+    _note("case: batch 300, positions 0..95")
+    positions = [int(p) for p in np.random.default_rng(300).integers(0, 96, 300)]
+    positions[0], positions[255], positions[256], positions[299] = 95, 0, 64, 1
+    _scenario(skv, ctx, lut4096, rope_tables, positions, seed=5000)
+
+
 def test_q17_entry(skv, ctx, lut4096, rope_tables):
     _note("case: Q15.17 entry, batch 2")
     _scenario(skv, ctx, lut4096, rope_tables, [5, 200], seed=31, q17=True)
