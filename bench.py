@@ -402,6 +402,13 @@ def main():
                                       "max_abs_diff_vs_fp32_path": e["max_abs_diff_vs_fp32_path"]}
     if b1:
         line["batch1"] = dict(summary(b1), workload="32 layers x batch 1 x position 4095, 1% of K channels x20")
+        t1, t1_src = profiled_traffic(1, args.context)
+        line["batch1"]["roofline"] = {"bound": "hbm (latency-bound at this size)",
+                                      "achieved": round(b1["step_kernel_gbps"], 1), "peak": HBM_PEAK_GBPS,
+                                      "unit": "GB/s", "frac": round(b1["step_kernel_gbps"] / HBM_PEAK_GBPS, 4),
+                                      "traffic": t1, "traffic_source": t1_src,
+                                      "bytes_per_launch": b1["dominant_bytes_per_launch"],
+                                      "avg_launch_us": round(b1["kernel_avg_us"]["step"], 2)}
     if extra:
         line["configs"] = extra
     print(json.dumps(line), flush=True)
