@@ -3,8 +3,9 @@
 // Owns the HIP stream, the device-resident RoPE table and KV arena, the
 // split-context workspace and the argument validation that the reference's
 // XRT host performs before each launch (host/decode_host.cpp:1340-1349).
-// Kernels live in swiftkv_kernels.hip; this file only validates, sizes and
-// enqueues.  No exception crosses the C boundary: every entry point converts
+// Kernels live in swiftkv_kernels.hip (the step, bulk append, conversion),
+// swiftkv_exact.hip (the integer-compatibility step) and swiftkv_synth.hip
+// (synthetic inputs); this file only validates, sizes and enqueues.  No exception crosses the C boundary: every entry point converts
 // failures to a negative status and a thread-local message.
 #include "../../include/swiftkv.h"
 

@@ -1,6 +1,6 @@
 // swiftkv_common.hpp -- geometry, cache layout and kernel argument blocks
 // shared by the host C-ABI (swiftkv_capi.cpp) and the HIP kernels
-// (swiftkv_kernels.hip).
+// (swiftkv_kernels.hip, swiftkv_exact.hip, swiftkv_synth.hip).
 #pragma once
 
 #include <hip/hip_runtime.h>

@@ -2,10 +2,13 @@
 // stage.
 //
 // step kernel (one launch per decode step and layer), grid (splits, 32 heads,
-// batch) of 256-thread workgroups; workgroup (j, h, b) owns tokens
-// [j*C, min((j+1)*C, position+1)) of sequence b, head h:
+// batch rows) of 256-thread workgroups; workgroup (j, h, z) owns tokens
+// [j*C, min((j+1)*C, position+1)) of head h of the sequence that row z names
+// (rows come longest first, so a ragged batch does not end on long heads):
 //   1. every lane rotates the 16 query channels it needs (integer RoPE from
-//      the Q1.17 table, FP32 -> Q15.17 first for FP32 inputs);
+//      the Q1.17 table, FP32 -> Q15.17 first for FP32 inputs); the query,
+//      the first cache block and the new row's inputs are all issued before
+//      any math;
 //   2. the workgroup whose range holds `position` also converts, rotates and
 //      G32-quantizes the new K/V row, appends it to the cache, and forwards it
 //      into its own merge as one more partial -- the new token is written once
@@ -19,7 +22,7 @@
 //   5. a head held by one split is finished in place (FP32 output and the
 //      optional A14/E8M0 words); otherwise each split publishes its partial
 //      (m, l, acc[128]) and the last split of the head to arrive merges them
-//      (log-sum-exp) and finishes the head.
+//      (log-sum-exp) and finishes the head -- no second kernel.
 //
 // No MFMA: q_len = 1 multi-head attention is a memory-bound GEMV.
 #include "swiftkv_device.hpp"
