@@ -1,7 +1,7 @@
 """Build recipe for libswiftkv.so (gfx950) and the CPU oracle.
 
-    python 4pe_u250_amd/build.py          # library + oracle (+ oracle/_ref when
-                                          # the reference sources are present)
+    python 4pe_u250_amd/build.py          # library, host driver and oracle (+ oracle/_ref
+                                          # when the reference sources are present)
 
 The library is compiled in-tree with hipcc for gfx950 only.  All HIP code is
 built with packed-FP32 instruction selection disabled.
@@ -31,6 +31,8 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 SOURCES = ["swiftkv_kernels.hip", "swiftkv_synth.hip", "swiftkv_exact.hip", "swiftkv_capi.cpp"]
+HOST_SRC = os.path.join(PKG_DIR, "host", "swiftkv_host.cpp")
+HOST_BIN = os.path.join(PKG_DIR, "swiftkv_host")
 
 
 def _run(cmd, cwd=None):
@@ -54,6 +56,21 @@ def build_library(verbose: bool = False) -> str:
     return LIB
 
 
+def build_host(verbose: bool = False) -> str:
+    """The native host driver: plain C++ over the C ABI, linked against the
+    library next to it (run path $ORIGIN)."""
+    cxx = shutil.which("g++")
+    if cxx is None:
+        raise RuntimeError("g++ not found")
+    tmp = HOST_BIN + ".tmp"
+    out = _run([cxx, "-O2", "-std=c++17", "-Wall", "-Wextra", "-I", os.path.join(REPO, "include"), HOST_SRC,
+                "-L", PKG_DIR, "-lswiftkv", "-Wl,-rpath,$ORIGIN", "-o", tmp])
+    if verbose and out.strip():
+        print(out)
+    os.replace(tmp, HOST_BIN)
+    return HOST_BIN
+
+
 def build_oracle(verbose: bool = False) -> None:
     make = shutil.which("make")
     if make is None:
@@ -66,6 +83,7 @@ def build_oracle(verbose: bool = False) -> None:
 def main() -> int:
     build_oracle(verbose=True)
     print(build_library(verbose=True))
+    print(build_host(verbose=True))
     return 0
 
 
