@@ -94,6 +94,25 @@ def test_batch_over_one_launch(skv, ctx, lut4096, rope_tables):
     _scenario(skv, ctx, lut4096, rope_tables, positions, seed=5000)
 
 
+@pytest.mark.parametrize("case", range(6))
+def test_randomized_configurations(skv, ctx, lut4096, rope_tables, case):
+    """Seeded random shapes: batch 1..24, ragged positions up to 1500, forced
+    or heuristic split, layer 0..2 of 3, FP32 or Q15.17 entry, N(0,1) or
+    Student-t(3) data, with or without outlier channels."""
+    rng = np.random.default_rng(9100 + case)
+    B = int(rng.integers(1, 25))
+    positions = [int(p) for p in rng.integers(0, 1501, B)]
+    split = int(rng.choice([0, 0, 256, 512, 1024, 4096]))
+    layer = int(rng.integers(0, 3))
+    dist = "t3" if rng.random() < 0.5 else "normal"
+    outl = outlier_channels(9200 + case) if rng.random() < 0.5 else None
+    q17 = bool(rng.random() < 0.5)
+    _note(f"case {case}: batch {B}, max position {max(positions)}, split {split}, layer {layer}, {dist}, "
+          f"outliers {outl is not None}, q17 {q17}")
+    _scenario(skv, ctx, lut4096, rope_tables, positions, seed=9300 + 100 * case, layers=3, layer=layer,
+              dist=dist, outliers=outl, split=split, q17=q17)
+
+
 def test_q17_entry(skv, ctx, lut4096, rope_tables):
     _note("case: Q15.17 entry, batch 2")
     _scenario(skv, ctx, lut4096, rope_tables, [5, 200], seed=31, q17=True)
