@@ -80,6 +80,8 @@ _SIGNATURES = {
     "swiftkv_kv_cache_import_records": (C.c_int, [_vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp]),
     "swiftkv_attention_f32": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _vp]),
     "swiftkv_attention_q17": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _vp]),
+    "swiftkv_attention_partials": (C.c_int, [_vp, _vp, _vp, _vp, _i32, C.c_int64, _vp, _vp, _vp, _vp, _i32, _vp,
+                                             _i32, _vp]),
     "swiftkv_set_host_io": (C.c_int, [_vp, _i32]),
     "swiftkv_attention_exact": (C.c_int, [_vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _vp]),
     "swiftkv_append_tokens": (C.c_int, [_vp, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _i32]),
@@ -92,6 +94,7 @@ _SIGNATURES = {
     "swiftkv_memcpy_d2h": (C.c_int, [_vp, _vp, _vp, _sz]),
     "swiftkv_memset_d": (C.c_int, [_vp, _vp, C.c_int, _sz]),
     "swiftkv_convert_f32_q17": (C.c_int, [_vp, _vp, _vp, _sz]),
+    "swiftkv_convert_partials_q17": (C.c_int, [_vp, _vp, _i32, C.c_int64, _vp, _sz]),
     "swiftkv_capture_begin": (C.c_int, [_vp]),
     "swiftkv_capture_end": (C.c_int, [_vp, C.POINTER(_vp)]),
     "swiftkv_graph_launch": (C.c_int, [_vp, _vp]),
@@ -258,6 +261,15 @@ class Context:
     def convert_f32_q17(self, src: DeviceBuffer, dst: DeviceBuffer, n: int) -> None:
         _check(lib().swiftkv_convert_f32_q17(self.handle, C.c_void_p(src.ptr), C.c_void_p(dst.ptr), n))
 
+    def convert_partials_q17(self, src: DeviceBuffer, dst: DeviceBuffer, n: int, parts: int,
+                             part_stride: Optional[int] = None) -> None:
+        """The linear stage's finalize: Q15.17 of `parts` FP32 partials reduced
+        in the reference's order; part p of element i at src[i + p * part_stride]
+        (default part_stride = n)."""
+        stride = n if part_stride is None else int(part_stride)
+        _check(lib().swiftkv_convert_partials_q17(self.handle, C.c_void_p(src.ptr), int(parts), stride,
+                                                  C.c_void_p(dst.ptr), n))
+
 
 class Graph:
     """A recorded sequence of asynchronous calls, replayed with one launch."""
@@ -390,12 +402,14 @@ def _io_ptr(ctx: "Context", x, dtype=None, writable: bool = False) -> Optional[i
     return x.ctypes.data
 
 
-def _check_io_sizes(ctx: Context, batch: int, q, k, v, out, aq, asc) -> None:
-    """In host-memory I/O mode the library copies whole [batch][...] rows:
-    refuse host arrays too small for them."""
+def _check_io_sizes(ctx: Context, batch: int, q, k, v, out, aq, asc, in_elems: Optional[int] = None) -> None:
+    """In host-memory I/O mode the library copies whole [batch][...] rows (and
+    for split-K partials `in_elems` elements per input): refuse host arrays
+    too small for them."""
     if not ctx.host_io:
         return
-    need = [(q, batch * 4096), (k, batch * 4096), (v, batch * 4096), (out, batch * 4096),
+    n_in = batch * 4096 if in_elems is None else in_elems
+    need = [(q, n_in), (k, n_in), (v, n_in), (out, batch * 4096),
             (aq, batch * 128 * 56), (asc, batch * 128)]
     for x, n in need:
         if isinstance(x, np.ndarray) and x.size < n:
@@ -421,6 +435,31 @@ def swiftkv_attention(ctx: Context, q, k, v, kv_cache: KVCache, rope_lut: RopeLu
               rope_lut.handle, _io_ptr(ctx, activation_q, np.uint8, True),
               _io_ptr(ctx, activation_scale, np.uint8, True), int(layer_index), _host_ptr(pos), int(pos.size),
               _io_ptr(ctx, out, np.float32, True)))
+
+
+def swiftkv_attention_partials(ctx: Context, q, k, v, parts: int, kv_cache: KVCache, rope_lut: RopeLut,
+                               activation_q, activation_scale, layer_index: int, position, out,
+                               part_stride: Optional[int] = None) -> None:
+    """The decode step fed by a split-K Q/K/V projection.
+
+    q, k, v each hold `parts` (1, 2 or 4) FP32 partial sums, part p at element
+    offset p * part_stride (default batch * 4096), each [batch][4096].  The
+    step reduces them as the reference's linear stage does -- fl(p0 + p1), or
+    fl(fl(p0 + p1) + fl(p2 + p3)) (int4_linear_controller.cpp:1039-1054,
+    1655-1667, 1089-1118) -- then converts to Q15.17 and proceeds as
+    swiftkv_attention.  Asynchronous on the context stream.
+    """
+    pos = np.ascontiguousarray(np.atleast_1d(np.asarray(position, dtype=np.int32)))
+    batch = int(pos.size)
+    stride = batch * 4096 if part_stride is None else int(part_stride)
+    _check_io_sizes(ctx, batch, q, k, v, out, activation_q, activation_scale,
+                    in_elems=(int(parts) - 1) * stride + batch * 4096 if int(parts) > 1 else None)
+    f = np.float32
+    _check(lib().swiftkv_attention_partials(ctx.handle, _io_ptr(ctx, q, f), _io_ptr(ctx, k, f), _io_ptr(ctx, v, f),
+                                            int(parts), stride, kv_cache.handle, rope_lut.handle,
+                                            _io_ptr(ctx, activation_q, np.uint8, True),
+                                            _io_ptr(ctx, activation_scale, np.uint8, True), int(layer_index),
+                                            _host_ptr(pos), batch, _io_ptr(ctx, out, np.float32, True)))
 
 
 def swiftkv_attention_exact(ctx: Context, q, k, v, kv_cache: KVCache, rope_lut: RopeLut,

@@ -228,6 +228,20 @@ void set_rows(StepArgs& a, const int32_t* positions) {
     for (int32_t z = 0; z < a.batch; ++z) a.rows[z] = pack_row(idx[z], positions[idx[z]]);
 }
 
+// How a step's q/k/v arrive: the format and, for split-K partials, the
+// element distance between consecutive partials of one tensor.
+struct StepInput {
+    InputFormat format;
+    int64_t part_stride;
+    int parts() const { return format == kInParts2 || format == kInParts4 ? static_cast<int>(format) : 1; }
+    // Elements one tensor spans for `batch` rows.
+    size_t extent(int32_t batch) const {
+        return static_cast<size_t>(parts() - 1) * static_cast<size_t>(part_stride) +
+               static_cast<size_t>(batch) * kModelDim;
+    }
+};
+constexpr StepInput kF32Input{kInF32, 0}, kQ17Input{kInQ17, 0};
+
 int validate_step(swiftkv_context* ctx, const void* q, const void* k, const void* v,
                   const swiftkv_kv_cache* kv, const swiftkv_rope_lut* lut, const uint8_t* act_q,
                   const uint8_t* act_scale, int32_t layer, const int32_t* positions, int32_t batch,
@@ -263,7 +277,7 @@ void profile_end(swiftkv_context* ctx, ProfilePair* p) {
     if (p) (void)hipEventRecord(p->end, ctx->stream);
 }
 
-int run_step(swiftkv_context* ctx, const void* q, const void* k, const void* v, bool q17,
+int run_step(swiftkv_context* ctx, const void* q, const void* k, const void* v, StepInput in,
              swiftkv_kv_cache* kv, const swiftkv_rope_lut* lut, uint8_t* act_q, uint8_t* act_scale,
              int32_t layer, const int32_t* positions, int32_t batch, float* out) {
     int rc = validate_step(ctx, q, k, v, kv, lut, act_q, act_scale, layer, positions, batch, out);
@@ -278,6 +292,7 @@ int run_step(swiftkv_context* ctx, const void* q, const void* k, const void* v, 
         a.q = static_cast<const char*>(q) + row0 * elem_bytes;
         a.k = static_cast<const char*>(k) + row0 * elem_bytes;
         a.v = static_cast<const char*>(v) + row0 * elem_bytes;
+        a.part_stride = in.part_stride;
         a.kv = CacheView{kv->base, kv->page_bytes, kv->seq_cap, kv->layers};
         a.lut = lut->table;
         a.lut_positions = lut->positions;
@@ -301,7 +316,7 @@ int run_step(swiftkv_context* ctx, const void* q, const void* k, const void* v, 
         a.act_scale = act_scale ? act_scale + static_cast<size_t>(b0) * kHeads * kGroupsPerHead : nullptr;
 
         ProfilePair* p = profile_begin(ctx, SWIFTKV_KERNEL_STEP);
-        SKV_HIP(launch_step(a, grid_splits, q17, ctx->stream));
+        SKV_HIP(launch_step(a, grid_splits, in.format, ctx->stream));
         profile_end(ctx, p);
     }
     return ok();
@@ -318,7 +333,7 @@ const uint32_t* exp2_table() {
     return table.data();
 }
 
-int run_exact(swiftkv_context* ctx, const void* q, const void* k, const void* v, bool q17,
+int run_exact(swiftkv_context* ctx, const void* q, const void* k, const void* v, StepInput in,
               swiftkv_kv_cache* kv, const swiftkv_rope_lut* lut, uint8_t* act_q, uint8_t* act_scale,
               int32_t layer, const int32_t* positions, int32_t batch, int32_t* out) {
     int rc = validate_step(ctx, q, k, v, kv, lut, act_q, act_scale, layer, positions, batch,
@@ -345,7 +360,7 @@ int run_exact(swiftkv_context* ctx, const void* q, const void* k, const void* v,
                         : nullptr;
         a.act_scale = act_scale ? act_scale + static_cast<size_t>(b0) * kHeads * kGroupsPerHead : nullptr;
         ProfilePair* p = profile_begin(ctx, SWIFTKV_KERNEL_EXACT);
-        SKV_HIP(launch_exact(a, exp2_table(), q17, ctx->stream));
+        SKV_HIP(launch_exact(a, exp2_table(), in.format == kInQ17, ctx->stream));
         profile_end(ctx, p);
     }
     return ok();
@@ -357,14 +372,14 @@ int run_exact(swiftkv_context* ctx, const void* q, const void* k, const void* v,
 // outputs are copied back and the call waits for them, so the host buffers
 // are valid on return (the reference host does the same around each PE call:
 // DMA in, run, DMA out, decode_host.cpp:1358-1485).
-int dispatch_step(swiftkv_context* ctx, bool exact, const void* q, const void* k, const void* v, bool q17,
+int dispatch_step(swiftkv_context* ctx, bool exact, const void* q, const void* k, const void* v, StepInput in,
                   swiftkv_kv_cache* kv, const swiftkv_rope_lut* lut, uint8_t* act_q, uint8_t* act_scale,
                   int32_t layer, const int32_t* positions, int32_t batch, void* out) {
     if (!ctx) return fail(SWIFTKV_EINVAL, "null context");
     if (!ctx->host_io) {
-        return exact ? run_exact(ctx, q, k, v, q17, kv, lut, act_q, act_scale, layer, positions, batch,
+        return exact ? run_exact(ctx, q, k, v, in, kv, lut, act_q, act_scale, layer, positions, batch,
                                  static_cast<int32_t*>(out))
-                     : run_step(ctx, q, k, v, q17, kv, lut, act_q, act_scale, layer, positions, batch,
+                     : run_step(ctx, q, k, v, in, kv, lut, act_q, act_scale, layer, positions, batch,
                                 static_cast<float*>(out));
     }
     int rc = validate_step(ctx, q, k, v, kv, lut, act_q, act_scale, layer, positions, batch,
@@ -372,22 +387,24 @@ int dispatch_step(swiftkv_context* ctx, bool exact, const void* q, const void* k
     if (rc) return rc;
     if ((rc = set_device(ctx))) return rc;
     auto align = [](size_t x) { return (x + 255) & ~static_cast<size_t>(255); };
+    const size_t in_bytes = in.extent(batch) * 4;   // one input tensor, all its partials
     const size_t row_bytes = static_cast<size_t>(batch) * kModelDim * 4;
     const size_t aq_bytes = static_cast<size_t>(batch) * kHeads * kGroupsPerHead * SWIFTKV_A14_WORD_BYTES;
     const size_t as_bytes = static_cast<size_t>(batch) * kHeads * kGroupsPerHead;
-    const size_t off_out = 3 * align(row_bytes), off_aq = off_out + align(row_bytes);
+    const size_t off_k = align(in_bytes), off_v = 2 * align(in_bytes), off_out = 3 * align(in_bytes);
+    const size_t off_aq = off_out + align(row_bytes);
     const size_t off_as = off_aq + align(aq_bytes), total = off_as + align(as_bytes);
     if ((rc = ensure(ctx, ctx->io_stage, ctx->io_bytes, total))) return rc;
     uint8_t* st = ctx->io_stage;
-    SKV_HIP(hipMemcpyAsync(st, q, row_bytes, hipMemcpyHostToDevice, ctx->stream));
-    SKV_HIP(hipMemcpyAsync(st + align(row_bytes), k, row_bytes, hipMemcpyHostToDevice, ctx->stream));
-    SKV_HIP(hipMemcpyAsync(st + 2 * align(row_bytes), v, row_bytes, hipMemcpyHostToDevice, ctx->stream));
+    SKV_HIP(hipMemcpyAsync(st, q, in_bytes, hipMemcpyHostToDevice, ctx->stream));
+    SKV_HIP(hipMemcpyAsync(st + off_k, k, in_bytes, hipMemcpyHostToDevice, ctx->stream));
+    SKV_HIP(hipMemcpyAsync(st + off_v, v, in_bytes, hipMemcpyHostToDevice, ctx->stream));
     uint8_t* d_aq = act_q ? st + off_aq : nullptr;
     uint8_t* d_as = act_scale ? st + off_as : nullptr;
-    rc = exact ? run_exact(ctx, st, st + align(row_bytes), st + 2 * align(row_bytes), q17, kv, lut, d_aq, d_as,
-                           layer, positions, batch, reinterpret_cast<int32_t*>(st + off_out))
-               : run_step(ctx, st, st + align(row_bytes), st + 2 * align(row_bytes), q17, kv, lut, d_aq, d_as,
-                          layer, positions, batch, reinterpret_cast<float*>(st + off_out));
+    rc = exact ? run_exact(ctx, st, st + off_k, st + off_v, in, kv, lut, d_aq, d_as, layer, positions, batch,
+                           reinterpret_cast<int32_t*>(st + off_out))
+               : run_step(ctx, st, st + off_k, st + off_v, in, kv, lut, d_aq, d_as, layer, positions, batch,
+                          reinterpret_cast<float*>(st + off_out));
     if (rc) return rc;
     SKV_HIP(hipMemcpyAsync(out, st + off_out, row_bytes, hipMemcpyDeviceToHost, ctx->stream));
     if (act_q) {
@@ -735,15 +752,30 @@ int swiftkv_attention_f32(swiftkv_context* ctx, const float* q, const float* k, 
                           swiftkv_kv_cache* kv_cache, const swiftkv_rope_lut* rope_lut, uint8_t* activation_q,
                           uint8_t* activation_scale, int32_t layer_index, const int32_t* positions,
                           int32_t batch, float* out) {
-    return dispatch_step(ctx, false, q, k, v, false, kv_cache, rope_lut, activation_q, activation_scale, layer_index,
-                         positions, batch, out);
+    return dispatch_step(ctx, false, q, k, v, kF32Input, kv_cache, rope_lut, activation_q, activation_scale,
+                         layer_index, positions, batch, out);
 }
 
 int swiftkv_attention_q17(swiftkv_context* ctx, const int32_t* q, const int32_t* k, const int32_t* v,
                           swiftkv_kv_cache* kv_cache, const swiftkv_rope_lut* rope_lut, uint8_t* activation_q,
                           uint8_t* activation_scale, int32_t layer_index, const int32_t* positions,
                           int32_t batch, float* out) {
-    return dispatch_step(ctx, false, q, k, v, true, kv_cache, rope_lut, activation_q, activation_scale, layer_index,
+    return dispatch_step(ctx, false, q, k, v, kQ17Input, kv_cache, rope_lut, activation_q, activation_scale,
+                         layer_index, positions, batch, out);
+}
+
+int swiftkv_attention_partials(swiftkv_context* ctx, const float* q, const float* k, const float* v,
+                               int32_t parts, int64_t part_stride, swiftkv_kv_cache* kv_cache,
+                               const swiftkv_rope_lut* rope_lut, uint8_t* activation_q, uint8_t* activation_scale,
+                               int32_t layer_index, const int32_t* positions, int32_t batch, float* out) {
+    if (!ctx) return fail(SWIFTKV_EINVAL, "null context");
+    if (parts != 1 && parts != 2 && parts != 4) return fail(SWIFTKV_EINVAL, "parts = %d: must be 1, 2 or 4", parts);
+    const int64_t rows_elems = static_cast<int64_t>(batch) * kModelDim;
+    if (parts > 1 && part_stride < rows_elems)
+        return fail(SWIFTKV_EINVAL, "part_stride %lld is below batch * 4096 = %lld: partials would overlap",
+                    static_cast<long long>(part_stride), static_cast<long long>(rows_elems));
+    const StepInput in{parts == 1 ? kInF32 : static_cast<InputFormat>(parts), parts == 1 ? 0 : part_stride};
+    return dispatch_step(ctx, false, q, k, v, in, kv_cache, rope_lut, activation_q, activation_scale, layer_index,
                          positions, batch, out);
 }
 
@@ -751,8 +783,8 @@ int swiftkv_attention_exact(swiftkv_context* ctx, const void* q, const void* k, 
                             swiftkv_kv_cache* kv_cache, const swiftkv_rope_lut* rope_lut, uint8_t* activation_q,
                             uint8_t* activation_scale, int32_t layer_index, const int32_t* positions,
                             int32_t batch, int32_t* out_q17) {
-    return dispatch_step(ctx, true, q, k, v, q17 != 0, kv_cache, rope_lut, activation_q, activation_scale,
-                         layer_index, positions, batch, out_q17);
+    return dispatch_step(ctx, true, q, k, v, q17 ? kQ17Input : kF32Input, kv_cache, rope_lut, activation_q,
+                         activation_scale, layer_index, positions, batch, out_q17);
 }
 
 int swiftkv_append_tokens(swiftkv_context* ctx, const void* k, const void* v, int32_t q17,
@@ -898,7 +930,20 @@ int swiftkv_convert_f32_q17(swiftkv_context* ctx, const float* in, int32_t* out,
     if (!ctx || (n && (!in || !out))) return fail(SWIFTKV_EINVAL, "null argument");
     int rc = set_device(ctx);
     if (rc) return rc;
-    SKV_HIP(launch_convert(in, out, n, ctx->stream));
+    SKV_HIP(launch_convert(in, 1, 0, out, n, ctx->stream));
+    return ok();
+}
+
+int swiftkv_convert_partials_q17(swiftkv_context* ctx, const float* in, int32_t parts, int64_t part_stride,
+                                 int32_t* out, size_t n) {
+    if (!ctx || (n && (!in || !out))) return fail(SWIFTKV_EINVAL, "null argument");
+    if (parts != 1 && parts != 2 && parts != 4) return fail(SWIFTKV_EINVAL, "parts = %d: must be 1, 2 or 4", parts);
+    if (parts > 1 && (part_stride < 0 || static_cast<uint64_t>(part_stride) < n))
+        return fail(SWIFTKV_EINVAL, "part_stride %lld is below n = %zu: partials would overlap",
+                    static_cast<long long>(part_stride), n);
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    SKV_HIP(launch_convert(in, parts, parts > 1 ? part_stride : 0, out, n, ctx->stream));
     return ok();
 }
 

@@ -39,6 +39,13 @@ constexpr int kCounterStride = 32;               // uint32 words
 // Sequences per launch: positions travel by value in the kernel arguments.
 constexpr int kMaxBatchPerLaunch = 256;
 
+// How the step's q/k/v arrive.  kInParts2/kInParts4: FP32 split-K partial sums
+// of the upstream Q/K/V linear stage, reduced in the reference's fixed order
+// before the Q15.17 conversion -- fl(p0 + p1), or fl(fl(p0 + p1) + fl(p2 +
+// p3)) (int4_linear_controller.cpp:1039-1054, 1655-1667, 1100-1118).  The
+// enumerator values of the partial formats are their part counts.
+enum InputFormat : int { kInF32 = 0, kInQ17 = 1, kInParts2 = 2, kInParts4 = 4 };
+
 static_assert(kTokenBytes == 288, "algorithmic bytes per token-head");
 static_assert(kGroupsPerHead == 4, "four G32 groups per head");
 
@@ -55,9 +62,10 @@ __host__ __device__ inline int8_t* page_ptr(const CacheView& v, int slot, int la
 
 // One decode step over a chunk of <= kMaxBatchPerLaunch sequences.
 struct StepArgs {
-    const void* q;            // [batch][4096] FP32 or Q15.17
+    const void* q;            // [batch][4096] FP32 or Q15.17; partial formats: part p at + p * part_stride
     const void* k;
     const void* v;
+    int64_t part_stride;      // elements between split-K partials (partial formats only)
     CacheView kv;
     const int2* lut;          // [lut_positions][64] (cos, sin) Q1.17
     int32_t lut_positions;
@@ -98,12 +106,15 @@ struct BulkArgs {
 };
 
 // Launchers (swiftkv_kernels.hip).
-hipError_t launch_step(const StepArgs& a, int grid_splits, bool q17, hipStream_t s);
+hipError_t launch_step(const StepArgs& a, int grid_splits, InputFormat in, hipStream_t s);
 hipError_t launch_append_bulk(const BulkArgs& a, bool q17, hipStream_t s);
 // Integer-compatibility step (one workgroup per (sequence, head)); a.out is
 // int32 Q15.17; exp_lut holds the 33 Q30 exp2 entries.
 hipError_t launch_exact(const StepArgs& a, const uint32_t* exp_lut, bool q17, hipStream_t s);
-hipError_t launch_convert(const float* in, int32_t* out, size_t n, hipStream_t s);
+// out[i] = Q15.17 of in[i] (parts = 1) or of the reduced split-K partials
+// in[i + p * part_stride] (parts = 2 or 4).
+hipError_t launch_convert(const float* in, int32_t parts, int64_t part_stride, int32_t* out, size_t n,
+                          hipStream_t s);
 // Synthetic inputs (swiftkv_synth.hip).
 hipError_t launch_fill_f32(float* out, size_t n, uint64_t first, uint64_t seed, uint64_t stream, int dist,
                            int outliers, hipStream_t s);

@@ -114,15 +114,61 @@ __device__ __forceinline__ int2 load_pair(const void* base, size_t elem) {
     }
 }
 
-// Raw 64-bit pair (FP32 or Q15.17 bits) and its later conversion, so a load
-// can be issued well before the value is needed.
-__device__ __forceinline__ int2 load_bits_pair(const void* base, size_t elem) {
-    return *reinterpret_cast<const int2*>(static_cast<const int32_t*>(base) + elem);
+// Split-K partial reduction of the upstream linear stage, in its fixed order:
+// the pair sums fl(p0 + p1) and fl(p2 + p3), then their sum
+// (int4_linear_controller.cpp:1039-1054 adds two FP32 lanes; :1655-1660 pairs
+// partials 0+1 and 2+3; :1100-1118 adds the two pair sums, then converts).
+// IEEE round-to-nearest-even adds, never reassociated or contracted.  The
+// conversion that follows saturates a NaN by its sign bit, so a NaN sum takes
+// a defined sign: that of a NaN operand (the first, if both are NaN), or, for
+// inf - inf, the negative default NaN that x86 SSE arithmetic (the platform of
+// the reference's C model) produces.
+__device__ __forceinline__ float add_partials(float a, float b) {
+    const float s = __fadd_rn(a, b);
+    if (!__builtin_isnan(s)) return s;
+    return __builtin_isnan(a) ? a : (__builtin_isnan(b) ? b : __uint_as_float(0xffc00000u));
 }
-template <bool Q17>
-__device__ __forceinline__ int2 bits_to_q17(int2 bits) {
-    if constexpr (Q17) return bits;
-    else return make_int2(f32_to_q17(__int_as_float(bits.x)), f32_to_q17(__int_as_float(bits.y)));
+
+template <int NP>
+__device__ __forceinline__ float reduce_parts(const float* p) {
+    static_assert(NP == 2 || NP == 4, "the reference reduces pairs, then pairs of pairs");
+    if constexpr (NP == 2) return add_partials(p[0], p[1]);
+    else return add_partials(add_partials(p[0], p[1]), add_partials(p[2], p[3]));
+}
+
+// Raw input bits of channels (elem, elem+1) -- FP32 or Q15.17, or the NP
+// split-K FP32 partials -- and their later conversion to Q15.17, so the loads
+// can be issued well before the values are needed.
+template <int IN>
+struct InPair {
+    int2 p[IN >= 2 ? IN : 1];
+};
+
+template <int IN>
+__device__ __forceinline__ InPair<IN> load_in(const void* base, size_t elem, int64_t part_stride) {
+    InPair<IN> r;
+    const int32_t* src = static_cast<const int32_t*>(base) + elem;
+#pragma unroll
+    for (int j = 0; j < (IN >= 2 ? IN : 1); ++j)
+        r.p[j] = *reinterpret_cast<const int2*>(src + j * part_stride);
+    return r;
+}
+
+template <int IN>
+__device__ __forceinline__ int2 in_to_q17(const InPair<IN>& in) {
+    if constexpr (IN == kInQ17) {
+        return in.p[0];
+    } else if constexpr (IN == kInF32) {
+        return make_int2(f32_to_q17(__int_as_float(in.p[0].x)), f32_to_q17(__int_as_float(in.p[0].y)));
+    } else {
+        float x[IN], y[IN];
+#pragma unroll
+        for (int j = 0; j < IN; ++j) {
+            x[j] = __int_as_float(in.p[j].x);
+            y[j] = __int_as_float(in.p[j].y);
+        }
+        return make_int2(f32_to_q17(reduce_parts<IN>(x)), f32_to_q17(reduce_parts<IN>(y)));
+    }
 }
 
 // Quantize this wave's (k rotated, v) row and write it at token `pos` of

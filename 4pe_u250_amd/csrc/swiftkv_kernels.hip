@@ -5,10 +5,11 @@
 // batch rows) of 256-thread workgroups; workgroup (j, h, z) owns tokens
 // [j*C, min((j+1)*C, position+1)) of head h of the sequence that row z names
 // (rows come longest first, so a ragged batch does not end on long heads):
-//   1. every lane rotates the 16 query channels it needs (integer RoPE from
-//      the Q1.17 table, FP32 -> Q15.17 first for FP32 inputs); the query,
-//      the first cache block and the new row's inputs are all issued before
-//      any math;
+//   1. every lane loads its channel pair of the new row's q/k/v (Q15.17,
+//      FP32, or the upstream linear stage's split-K FP32 partials, reduced in
+//      the reference's order), then the first cache block, before any math;
+//      it converts and rotates its q pair (integer RoPE from the Q1.17 table)
+//      and gathers the 16 query channels of its chunk from its neighbours;
 //   2. the workgroup whose range holds `position` also converts, rotates and
 //      G32-quantizes the new K/V row, appends it to the cache, and forwards it
 //      into its own merge as one more partial -- the new token is written once
@@ -76,36 +77,6 @@ __device__ __forceinline__ void axpy16(float* acc, float w, v4i v) {
 }
 
 // ---------------------------------------------------------------- pieces
-
-// Rotated, pre-scaled query channels [16c, 16c+16) of head h (pairs 8c..8c+7).
-// Split in two so the 16 loads go out first (before the cache block, because
-// vmcnt retires in issue order) and the conversion, which branches, runs
-// once they have landed.
-struct QueryLoads {
-    int2 q[8], cs[8];
-};
-
-__device__ __forceinline__ void query_loads(const StepArgs& a, int b, int h, int c, int pos, QueryLoads& ql) {
-    const size_t base = static_cast<size_t>(b) * kModelDim + h * kHeadDim + c * 16;
-    const int2* cs = a.lut + static_cast<size_t>(pos) * kRopePairs + c * 8;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        ql.q[j] = load_bits_pair(a.q, base + 2 * j);
-        ql.cs[j] = cs[j];
-    }
-}
-
-template <bool Q17>
-__device__ __forceinline__ void query_chunk(const QueryLoads& ql, float* qf) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int2 qi = bits_to_q17<Q17>(ql.q[j]);
-        int32_t x0, x1;
-        rope_pair(qi.x, qi.y, ql.cs[j], x0, x1);
-        qf[2 * j] = (static_cast<float>(x0) * 0x1p-17f) * kScoreScale;
-        qf[2 * j + 1] = (static_cast<float>(x1) * 0x1p-17f) * kScoreScale;
-    }
-}
 
 // A page is read through one buffer resource held in SGPRs: the per-lane
 // offset is fixed for the whole scan and the token offset is a wave-uniform
@@ -315,7 +286,7 @@ __device__ __forceinline__ float merge_partials(const float* part, int n) {
 // ---------------------------------------------------------------- step
 
 // Grid (splits, 32 heads, batch), 256 threads; grid row z serves rows[z].
-template <bool Q17>
+template <int IN>
 __global__ __launch_bounds__(kAttendWaves * 64) void step_kernel(StepArgs a) {
     const uint32_t row = a.rows[blockIdx.z];
     const int split = blockIdx.x, h = blockIdx.y, b = static_cast<int>(row & 0xffu);
@@ -339,48 +310,54 @@ __global__ __launch_bounds__(kAttendWaves * 64) void step_kernel(StepArgs a) {
     __shared__ float s_acc[kAttendWaves + 1][kHeadDim];
     __shared__ float s_m[kAttendWaves + 1], s_l[kAttendWaves + 1];
 
-    // Loads go out before any math, in the order they are needed: the query
-    // chunk, the first cache block, the new row.  The query rotation then
-    // overlaps the block's flight.  The new token is excluded from the scan
-    // (it is forwarded below).
-    QueryLoads ql;
-    query_loads(a, b, h, c, pos, ql);
+    // Loads go out before any math, in the order they are needed: this
+    // lane's channel pair (2*lane, 2*lane+1) of the new row's q, k, v and its
+    // RoPE pair, then the first cache block.  The conversions below wait only
+    // for the row loads (vector loads retire in issue order), so they overlap
+    // the block's flight.  All of them are unconditional and in bounds: a
+    // load under a branch makes the compiler wait for the prefetched block at
+    // the join.
+    const size_t row_elem = static_cast<size_t>(b) * kModelDim + h * kHeadDim + 2 * lane;
+    const int2 row_cs = a.lut[static_cast<size_t>(pos) * kRopePairs + lane];
+    const InPair<IN> row_q = load_in<IN>(a.q, row_elem, a.part_stride);
+    const InPair<IN> row_k = load_in<IN>(a.k, row_elem, a.part_stride);
+    const InPair<IN> row_v = load_in<IN>(a.v, row_elem, a.part_stride);
     const PageReader pr = make_reader(page, cap, c, r);
     const int t_first = t_begin + wave * kBlockTokens;
-    const int t_stop = owner ? pos : t_end;
+    const int t_stop = owner ? pos : t_end;       // the new token is forwarded, not scanned
     // A wave with no tokens loads the split's first block (always in the page)
-    // and discards it: every path then has the same loads in flight, so the
-    // wait for the query does not also wait for this block.
+    // and discards it: every path then has the same loads in flight.
     BlockLoads bl;
     issue_block(pr, t_first < t_stop ? t_first : t_begin, bl);
 
-    // The new row's inputs are fetched now; its math runs after the scan, so
-    // the fetch latency hides under the cache stream.
-    // (Unconditional, always in bounds: a conditional load would make the
-    // compiler wait for the prefetched block at the branch join.)
-    const bool row_wave = owner && wave == 0;
-    const size_t row_elem = static_cast<size_t>(b) * kModelDim + h * kHeadDim + 2 * lane;
-    const int2 row_cs = a.lut[static_cast<size_t>(pos) * kRopePairs + lane];
-    const int2 row_q = load_bits_pair(a.q, row_elem);
-    const int2 row_k = load_bits_pair(a.k, row_elem);
-    const int2 row_v = load_bits_pair(a.v, row_elem);
-
+    // Query: each lane converts and rotates its own pair, pre-scales it, and
+    // gathers the 16 channels of its chunk c (pairs 8c..8c+7, held by lanes
+    // 8c..8c+7).  The new row's k is rotated and v converted here too, which
+    // frees the raw row registers before the scan.
+    const int2 qi = in_to_q17<IN>(row_q);
+    int32_t q0, q1;
+    rope_pair(qi.x, qi.y, row_cs, q0, q1);
+    const float qs0 = (static_cast<float>(q0) * 0x1p-17f) * kScoreScale;
+    const float qs1 = (static_cast<float>(q1) * 0x1p-17f) * kScoreScale;
     float qf[16];
-    query_chunk<Q17>(ql, qf);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        qf[2 * j] = __shfl(qs0, 8 * c + j);
+        qf[2 * j + 1] = __shfl(qs1, 8 * c + j);
+    }
+    const int2 ki = in_to_q17<IN>(row_k), vi = in_to_q17<IN>(row_v);
+    int32_t k0, k1;
+    rope_pair(ki.x, ki.y, row_cs, k0, k1);
+
     float m_run, l_run, acc[16];
     scan_range(pr, bl, qf, t_first, t_stop, kAttendWaves * kBlockTokens, r, m_run, l_run, acc);
 
-    // The new row: convert, rotate k, quantize, append; forward (k^ . q', v^)
-    // into the merge as one more partial.
-    if (row_wave) {
-        const int2 qi = bits_to_q17<Q17>(row_q), ki = bits_to_q17<Q17>(row_k), vi = bits_to_q17<Q17>(row_v);
-        int32_t q0, q1, k0, k1;
-        rope_pair(qi.x, qi.y, row_cs, q0, q1);
-        rope_pair(ki.x, ki.y, row_cs, k0, k1);
+    // The new row: quantize, append; forward (k^ . q', v^) into the merge as
+    // one more partial.
+    if (owner && wave == 0) {
         float kh0, kh1, vh0, vh1;
         append_row_dequant(page, a.kv.seq_cap, pos, lane, k0, k1, vi.x, vi.y, kh0, kh1, vh0, vh1);
-        float sp = ((static_cast<float>(q0) * 0x1p-17f) * kScoreScale) * kh0 +
-                   ((static_cast<float>(q1) * 0x1p-17f) * kScoreScale) * kh1;
+        float sp = qs0 * kh0 + qs1 * kh1;
 #pragma unroll
         for (int s = 1; s < 64; s <<= 1) sp += __shfl_xor(sp, s);
         s_acc[kAttendWaves][2 * lane] = vh0;
@@ -460,21 +437,36 @@ __global__ __launch_bounds__(256) void append_bulk_kernel(BulkArgs a) {
     append_row(page_ptr(a.kv, a.slot, a.layer, h), a.kv.seq_cap, pos, lane, k0, k1, vi.x, vi.y);
 }
 
-__global__ __launch_bounds__(256) void convert_kernel(const float* __restrict__ in, int32_t* __restrict__ out,
-                                                      size_t n) {
+// out[i] = Q15.17 of in[i] (NP = 1) or of the NP reduced split-K partials.
+template <int NP>
+__global__ __launch_bounds__(256) void convert_kernel(const float* __restrict__ in, int64_t part_stride,
+                                                      int32_t* __restrict__ out, size_t n) {
     const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
-    for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
-        out[i] = f32_to_q17(in[i]);
+    for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
+        if constexpr (NP == 1) {
+            out[i] = f32_to_q17(in[i]);
+        } else {
+            float p[NP];
+#pragma unroll
+            for (int j = 0; j < NP; ++j) p[j] = in[i + j * part_stride];
+            out[i] = f32_to_q17(reduce_parts<NP>(p));
+        }
+    }
 }
 
 }  // namespace
 
 // ---------------------------------------------------------------- launchers
 
-hipError_t launch_step(const StepArgs& a, int grid_splits, bool q17, hipStream_t s) {
-    const dim3 grid(grid_splits, kHeads, a.batch);
-    if (q17) step_kernel<true><<<grid, kAttendWaves * 64, 0, s>>>(a);
-    else step_kernel<false><<<grid, kAttendWaves * 64, 0, s>>>(a);
+hipError_t launch_step(const StepArgs& a, int grid_splits, InputFormat in, hipStream_t s) {
+    const dim3 grid(grid_splits, kHeads, a.batch), block(kAttendWaves * 64);
+    switch (in) {
+    case kInF32: step_kernel<kInF32><<<grid, block, 0, s>>>(a); break;
+    case kInQ17: step_kernel<kInQ17><<<grid, block, 0, s>>>(a); break;
+    case kInParts2: step_kernel<kInParts2><<<grid, block, 0, s>>>(a); break;
+    case kInParts4: step_kernel<kInParts4><<<grid, block, 0, s>>>(a); break;
+    default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 
@@ -485,11 +477,18 @@ hipError_t launch_append_bulk(const BulkArgs& a, bool q17, hipStream_t s) {
     return hipGetLastError();
 }
 
-hipError_t launch_convert(const float* in, int32_t* out, size_t n, hipStream_t s) {
+hipError_t launch_convert(const float* in, int32_t parts, int64_t part_stride, int32_t* out, size_t n,
+                          hipStream_t s) {
     if (n == 0) return hipSuccess;
     size_t blocks = (n + 255) / 256;
     if (blocks > 65536) blocks = 65536;
-    convert_kernel<<<static_cast<unsigned>(blocks), 256, 0, s>>>(in, out, n);
+    const unsigned g = static_cast<unsigned>(blocks);
+    switch (parts) {
+    case 1: convert_kernel<1><<<g, 256, 0, s>>>(in, part_stride, out, n); break;
+    case 2: convert_kernel<2><<<g, 256, 0, s>>>(in, part_stride, out, n); break;
+    case 4: convert_kernel<4><<<g, 256, 0, s>>>(in, part_stride, out, n); break;
+    default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

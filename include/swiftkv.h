@@ -163,6 +163,25 @@ int swiftkv_attention_q17(swiftkv_context* ctx, const int32_t* q, const int32_t*
                           uint8_t* activation_scale, int32_t layer_index,
                           const int32_t* positions, int32_t batch, float* out);
 
+/* The step fed directly by a split-K Q/K/V projection: q, k, v are each
+ * `parts` FP32 partial sums, part p of a tensor at  base + p * part_stride
+ * (elements, >= batch * 4096), each part [batch][4096].  The step reduces
+ * them in the reference's fixed order -- fl(p0 + p1) for two parts,
+ * fl(fl(p0 + p1) + fl(p2 + p3)) for four -- and converts the sum to Q15.17,
+ * as the Q/K/V linear stage's pair reduction and finalize do before the
+ * attention stage sees its inputs (int4_linear_controller.cpp:1039-1054,
+ * 1655-1667, 1089-1118; finalize converts for the Q/K/V modes only, :129-132).
+ * The reduction happens in the step's own input loads, so no separate
+ * reduce/convert pass or intermediate buffer is needed.
+ *   parts        1 (same as swiftkv_attention_f32), 2 or 4; other values
+ *                SWIFTKV_EINVAL
+ * Other arguments as for swiftkv_attention_f32. */
+int swiftkv_attention_partials(swiftkv_context* ctx, const float* q, const float* k, const float* v,
+                               int32_t parts, int64_t part_stride, swiftkv_kv_cache* kv_cache,
+                               const swiftkv_rope_lut* rope_lut, uint8_t* activation_q,
+                               uint8_t* activation_scale, int32_t layer_index,
+                               const int32_t* positions, int32_t batch, float* out);
+
 /* Integer-compatibility step: the same append, then the reference's own
  * Q15.17 arithmetic instead of the FP32 formula -- 44-bit wrapped G32 dot
  * products, score * RNE(2^17/sqrt(128)) >> 24, the single-pass (max, Z, Y)
@@ -183,7 +202,7 @@ int swiftkv_attention_exact(swiftkv_context* ctx, const void* q, const void* k, 
                             const int32_t* positions, int32_t batch, int32_t* out_q17);
 
 /* Host-memory I/O mode (default off).  When on, the q/k/v, out and
- * activation pointers of swiftkv_attention_f32/_q17/_exact and the k/v of
+ * activation pointers of swiftkv_attention_f32/_q17/_partials/_exact and the k/v of
  * swiftkv_append_tokens are host memory: the call stages them through a
  * context-owned device buffer on the context stream and returns after its
  * outputs are back in host memory (the reference host's DMA-in / run /
@@ -237,6 +256,15 @@ int swiftkv_memset_d(swiftkv_context* ctx, void* dst, int value, size_t bytes);
 /* Elementwise FP32 -> Q15.17 on the device (the conversion of step 1),
  * n elements, device pointers.  Exposed for exhaustive conversion tests. */
 int swiftkv_convert_f32_q17(swiftkv_context* ctx, const float* in, int32_t* out, size_t n);
+
+/* The Q/K/V linear stage's finalize on the device: out[i] = Q15.17 of the
+ * `parts` FP32 partials in[i + p * part_stride] reduced in the reference's
+ * order (see swiftkv_attention_partials; int4_linear_controller.cpp:1089-1118).
+ * parts 1, 2 or 4; part_stride >= n for parts > 1; device pointers.  Feeds
+ * swiftkv_attention_exact (q17 = 1) with the inputs the reference's attention
+ * stage receives. */
+int swiftkv_convert_partials_q17(swiftkv_context* ctx, const float* in, int32_t parts,
+                                 int64_t part_stride, int32_t* out, size_t n);
 
 /* --------------------------------------------------------------------------
  * HIP graphs: record a sequence of asynchronous calls (steps, appends,

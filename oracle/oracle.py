@@ -40,6 +40,8 @@ def lib() -> C.CDLL:
     L.oracle_f2q17.restype = C.c_int32
     L.oracle_f2q17.argtypes = [C.c_float]
     L.oracle_f2q17_array.argtypes = [_f32p, _i32p, C.c_int64]
+    L.oracle_reduce_partials.argtypes = [_f32p, C.c_int, C.c_int64, _f32p, C.c_int64]
+    L.oracle_finalize_partials.argtypes = [_f32p, C.c_int, C.c_int64, _i32p, C.c_int64]
     L.oracle_f2q17_digest.restype = C.c_uint64
     L.oracle_f2q17_digest.argtypes = [C.c_uint64, C.c_uint64]
     L.oracle_rne_shift.restype = C.c_int64
@@ -88,6 +90,25 @@ def f2q17(x: np.ndarray) -> np.ndarray:
     x = np.ascontiguousarray(x, dtype=np.float32)
     out = np.empty(x.shape, np.int32)
     lib().oracle_f2q17_array(x.reshape(-1), out.reshape(-1), x.size)
+    return out
+
+
+def reduce_partials(parts: np.ndarray) -> np.ndarray:
+    """FP32 split-K partials [P][...] (P = 1, 2 or 4) reduced as the linear
+    stage does (int4_linear_controller.cpp:1039-1054, 1655-1667, 1100-1118)."""
+    p = np.ascontiguousarray(parts, dtype=np.float32)
+    n = p[0].size
+    out = np.empty(p.shape[1:], np.float32)
+    lib().oracle_reduce_partials(p.reshape(-1), p.shape[0], n, out.reshape(-1), n)
+    return out
+
+
+def finalize_partials(parts: np.ndarray) -> np.ndarray:
+    """Q15.17 of reduce_partials(parts): the Q/K/V finalize (:1100-1118)."""
+    p = np.ascontiguousarray(parts, dtype=np.float32)
+    n = p[0].size
+    out = np.empty(p.shape[1:], np.int32)
+    lib().oracle_finalize_partials(p.reshape(-1), p.shape[0], n, out.reshape(-1), n)
     return out
 
 

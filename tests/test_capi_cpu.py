@@ -58,6 +58,9 @@ def test_null_and_range_checks_without_device(skv):
     ms = (C.c_double * skv.KERNEL_KINDS)()
     assert L.swiftkv_profile_collect(None, counts, ms) == skv.EINVAL
     assert L.swiftkv_set_host_io(None, 1) == skv.EINVAL
+    assert L.swiftkv_attention_partials(None, None, None, None, 4, 4096, None, None, None, None, 0,
+                                        pos.ctypes.data_as(C.c_void_p), 1, None) == skv.EINVAL
+    assert L.swiftkv_convert_partials_q17(None, None, 2, 16, None, 16) == skv.EINVAL
     assert L.swiftkv_attention_exact(None, None, None, None, 0, None, None, None, None, 0,
                                      pos.ctypes.data_as(C.c_void_p), 1, None) == skv.EINVAL
     # destroy functions accept null like free()
