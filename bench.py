@@ -24,6 +24,8 @@ layer), batch 1 at position 2047 (32 layers), batch 64 with attended lengths
 drawn from U{256..4096} (32 layers), batch 16 decoding 512 steps from
 position 32256 to 32767 on Student-t(3) data (one layer), and the batch-64
 call with host-memory inputs and outputs (PCIe included; never `value`).
+The batch-64 and batch-1 workloads are also timed through the entry that
+takes the Q/K/V projection's split-K FP32 partials (--parts, default 4).
 """
 import argparse
 import json
@@ -41,9 +43,10 @@ METRIC = "decode-attn µs/layer + achieved HBM GB/s (% of peak), ctx 4096, batch
 TOKEN_HEAD_BYTES = 288
 
 
-def step_bytes(position: int) -> int:
-    """Algorithmic bytes of one (sequence, layer) step at `position`."""
-    return 32 * (position * TOKEN_HEAD_BYTES + TOKEN_HEAD_BYTES + 4 * 128 * 4)
+def step_bytes(position: int, parts: int = 1) -> int:
+    """Algorithmic bytes of one (sequence, layer) step at `position`; with
+    split-K partial inputs q/k/v each arrive as `parts` FP32 rows."""
+    return 32 * (position * TOKEN_HEAD_BYTES + TOKEN_HEAD_BYTES + (3 * parts + 1) * 128 * 4)
 
 
 def log(msg):
@@ -64,7 +67,7 @@ def profiled_traffic(batch: int, context: int):
 
 
 def run_gpu(skv, ctx, positions, layers, steps, warmup, seed, outliers=False, dist=0, exact_steps=0,
-            graph=True, advance=False):
+            graph=True, advance=False, parts=0):
     """Time `steps` decode steps of `layers` calls each over sequences at `positions`.
 
     The cache is filled on the device to max(positions) tokens per sequence;
@@ -155,6 +158,33 @@ def run_gpu(skv, ctx, positions, layers, steps, warmup, seed, outliers=False, di
         exact = {"us_per_layer": 1000.0 * ms_exact / exact_steps / layers,
                  "gbps": exact_steps * layers * sum(step_bytes(int(p)) for p in positions) / (ms_exact / 1e3) / 1e9,
                  "max_abs_diff_vs_fp32_path": err}
+    partials = None
+    if parts:
+        # The same steps fed by `parts`-way split-K FP32 partials through
+        # swiftkv_attention_partials: the upstream linear stage's reduction and
+        # finalize run inside the step's input loads.  Layout [part][layer][batch][4096].
+        pbuf = [ctx.alloc(parts * n_in * 4) for _ in range(3)]
+        for i, buf in enumerate(pbuf):
+            ctx.fill_synthetic(buf, parts * n_in, seed + 2, 2000 + i, dist=dist)
+
+        def parts_step():
+            for layer in range(layers):
+                off = layer * layer_stride
+                skv.swiftkv_attention_partials(ctx, pbuf[0].ptr + off, pbuf[1].ptr + off, pbuf[2].ptr + off, parts,
+                                               kv, lut, aq, asc, layer, positions, out, part_stride=n_in)
+        for _ in range(warmup):
+            parts_step()
+        ctx.timer_record(6)
+        for _ in range(steps):
+            parts_step()
+        ctx.timer_record(7)
+        ms_parts = ctx.timer_elapsed_ms(6, 7)
+        assert np.isfinite(out.download(np.float32, (batch, 4096))).all(), "non-finite output (partials)"
+        for b in pbuf:
+            b.free()
+        pbytes = steps * layers * sum(step_bytes(int(p), parts) for p in positions)
+        partials = {"parts": parts, "us_per_layer": 1000.0 * ms_parts / steps / layers,
+                    "gbps": pbytes / (ms_parts / 1e3) / 1e9}
     for b in qkv + [out, aq, asc]:
         b.free()
     kv.close()
@@ -170,6 +200,7 @@ def run_gpu(skv, ctx, positions, layers, steps, warmup, seed, outliers=False, di
         "kernel_launches": dict(zip(["append", "step"], counts)),
         "kernel_avg_us": {k: (1000.0 * t / c if c else None) for k, t, c in zip(["append", "step"], kms, counts)},
         "exact": exact,
+        "partials": partials,
         "sum_attended": int(sum(int(p) + 1 for p in positions)),
     }
     res["pct_of_peak"] = 100.0 * res["gbps"] / HBM_PEAK_GBPS
@@ -296,6 +327,8 @@ def main():
                     help="skip the secondary configurations (position 127, 2047, ragged, 32K)")
     ap.add_argument("--exact-steps", type=int, default=1,
                     help="steps of the integer-compatibility entry to time (0 = skip)")
+    ap.add_argument("--parts", type=int, default=4,
+                    help="also time the step fed by this many split-K FP32 partials (0 = skip)")
     ap.add_argument("--calibrate", action="store_true",
                     help="only run the FP32->Q15.17 conversion kernel over 256 Mi elements (a copy of known "
                          "size: 1 GiB read, 1 GiB written per launch) to scale HBM byte counters")
@@ -322,17 +355,22 @@ def main():
     ctx.set_split_tokens(args.split)
     log(f"[bench] {skv.version()}")
     main_res = run_gpu(skv, ctx, np.full(args.batch, args.context - 1), args.layers, args.steps, args.warmup,
-                       seed=2026, exact_steps=args.exact_steps)
+                       seed=2026, exact_steps=args.exact_steps, parts=args.parts)
     log(f"[bench] batch {args.batch}: {main_res['us_per_layer']:.1f} us/layer, {main_res['gbps']:.0f} GB/s "
         f"(graph replay {main_res['graph']['us_per_layer']:.1f} us/layer)")
+    if main_res["partials"]:
+        log(f"[bench] batch {args.batch}, {args.parts} split-K partials: "
+            f"{main_res['partials']['us_per_layer']:.1f} us/layer")
     b1 = None
     extra = {}
     if not args.no_batch1:
         # batch-1 headline: 1% of K channels x20
         b1 = run_gpu(skv, ctx, [args.context - 1], args.layers, max(args.steps, 20), args.warmup, seed=2027,
-                     outliers=True)
+                     outliers=True, parts=args.parts)
         log(f"[bench] batch 1: {b1['us_per_layer']:.2f} us/layer, {b1['gbps']:.0f} GB/s "
             f"(graph replay {b1['graph']['us_per_layer']:.2f} us/layer)")
+        if b1["partials"]:
+            log(f"[bench] batch 1, {args.parts} split-K partials: {b1['partials']['us_per_layer']:.2f} us/layer")
     if not args.no_configs:
         r = run_gpu(skv, ctx, [127], 1, 200, args.warmup, seed=2028)
         extra["batch1_position127_1layer"] = summary(r)
@@ -400,8 +438,17 @@ def main():
         e = main_res["exact"]
         line["integer_exact_path"] = {"us_per_layer": round(e["us_per_layer"], 1), "gbps": round(e["gbps"], 1),
                                       "max_abs_diff_vs_fp32_path": e["max_abs_diff_vs_fp32_path"]}
+    if main_res["partials"]:
+        p = main_res["partials"]
+        line["split_k_partials_input"] = {
+            "parts": p["parts"], "us_per_layer": round(p["us_per_layer"], 2), "gbps": round(p["gbps"], 1),
+            "note": "same workload through swiftkv_attention_partials; bytes count the parts x FP32 q/k/v rows"}
     if b1:
         line["batch1"] = dict(summary(b1), workload="32 layers x batch 1 x position 4095, 1% of K channels x20")
+        if b1["partials"]:
+            line["batch1"]["split_k_partials_input"] = {"parts": b1["partials"]["parts"],
+                                                        "us_per_layer": round(b1["partials"]["us_per_layer"], 3),
+                                                        "gbps": round(b1["partials"]["gbps"], 1)}
         t1, t1_src = profiled_traffic(1, args.context)
         line["batch1"]["roofline"] = {"bound": "hbm (latency-bound at this size)",
                                       "achieved": round(b1["step_kernel_gbps"], 1), "peak": HBM_PEAK_GBPS,
