@@ -12,13 +12,14 @@
 //
 // The stage has no weights of its own, so its inputs are synthetic: cached
 // rows go through the append rule from the library's seeded generators, and
-// q/k/v per layer come from the same generators (FP32, or converted to
-// Q15.17 on the device for --q17).
+// q/k/v per layer come from the same generators (FP32, converted to Q15.17
+// on the device for --q17, or as split-K FP32 partial sums for --parts).
 //
 //   swiftkv_host --batch 64 --context 4096 --steps 10
 //   swiftkv_host --batch 1 --graph
 //   swiftkv_host --decode --batch 16 --context 32257 --steps 512 --layers 1 --t3
 //   swiftkv_host --exact --batch 4 --context 1024 --rope-lut rope_lut.bin
+//   swiftkv_host --batch 64 --parts 4
 #include "swiftkv.h"
 
 #include <algorithm>
@@ -92,11 +93,12 @@ std::vector<std::uint8_t> read_file_checked(const std::string& path, std::size_t
 }
 
 // Algorithmic HBM bytes of one (sequence, layer) step at `position`: every
-// cached token-head read once, the new row written, FP32 q/k/v in and the
-// output out.
-std::uint64_t step_bytes(int position) {
+// cached token-head read once, the new row written, FP32 q/k/v in (each as
+// `parts` partial rows) and the output out.
+std::uint64_t step_bytes(int position, int parts) {
     return static_cast<std::uint64_t>(SWIFTKV_HEADS) *
-           (static_cast<std::uint64_t>(position) * kTokenHeadBytes + kTokenHeadBytes + 4ull * SWIFTKV_HEAD_DIM * 4);
+           (static_cast<std::uint64_t>(position) * kTokenHeadBytes + kTokenHeadBytes +
+            (3ull * static_cast<std::uint64_t>(parts) + 1ull) * SWIFTKV_HEAD_DIM * 4);
 }
 
 struct Config {
@@ -112,6 +114,7 @@ struct Config {
     std::uint64_t seed = 2026;
     bool q17 = false;         // Q15.17 inputs (swiftkv_attention_q17)
     bool exact = false;       // integer-compatibility entry
+    int parts = 1;            // split-K FP32 partials per input (swiftkv_attention_partials) when 2 or 4
     bool decode = false;      // step s runs at position context-1+s, appending as it goes
     bool graph = false;       // record one step as a HIP graph and replay it
     bool host_io = false;     // host-memory q/k/v and outputs
@@ -134,6 +137,8 @@ void print_usage(const char* program) {
         << "  --seed N         synthetic-data seed (2026)\n"
         << "  --q17            Q15.17 inputs (default FP32)\n"
         << "  --exact          the integer-compatibility entry (bit-exact A14 words)\n"
+        << "  --parts N        inputs as N = 2 or 4 split-K FP32 partial sums (swiftkv_attention_partials;\n"
+        << "                   with --exact they are finalized once by swiftkv_convert_partials_q17)\n"
         << "  --decode         advance the position every step (a real decode run)\n"
         << "  --graph          record one step as a HIP graph and time its replays\n"
         << "  --host-io        inputs and outputs in host memory (PCIe included)\n"
@@ -193,6 +198,9 @@ Config parse_args(int argc, char** argv, bool* help) {
             c.q17 = true;
         } else if (a == "--exact") {
             c.exact = true;
+        } else if (a == "--parts") {
+            c.parts = static_cast<int>(parse_integer(a, value(), 1, 4));
+            if (c.parts == 3) throw std::runtime_error("--parts must be 1, 2 or 4");
         } else if (a == "--decode") {
             c.decode = true;
         } else if (a == "--graph") {
@@ -210,6 +218,7 @@ Config parse_args(int argc, char** argv, bool* help) {
     if (c.decode && c.graph)
         throw std::runtime_error("--graph replays the recorded positions; it cannot advance them (--decode)");
     if (c.host_io && c.graph) throw std::runtime_error("--host-io calls synchronize; they cannot be recorded (--graph)");
+    if (c.parts > 1 && c.q17) throw std::runtime_error("--parts gives FP32 partial sums; it excludes --q17");
     const long long last = static_cast<long long>(c.context) - 1 + (c.decode ? c.steps - 1 : 0);
     if (last >= SWIFTKV_MAX_SEQ) {
         std::ostringstream msg;
@@ -275,22 +284,34 @@ int run(const Config& cfg) {
                                               cfg.outliers ? 1 : 0),
               "swiftkv_kv_cache_fill_synthetic");
 
-    // q/k/v of every layer, generated once on the device.
-    DeviceBuffer qkv_f32[3] = {{ctx.p, all_elems * 4}, {ctx.p, all_elems * 4}, {ctx.p, all_elems * 4}};
+    // q/k/v of every layer, generated once on the device: [layer][batch][4096]
+    // FP32, or with --parts [part][layer][batch][4096] partial sums (part
+    // stride all_elems).  --q17, and --exact with partials, convert them to
+    // Q15.17 once here, as the upstream finalize would.
+    const std::size_t in_elems = all_elems * static_cast<std::size_t>(cfg.parts);
+    DeviceBuffer qkv_f32[3] = {{ctx.p, in_elems * 4}, {ctx.p, in_elems * 4}, {ctx.p, in_elems * 4}};
     for (int i = 0; i < 3; ++i)
-        check(swiftkv_fill_synthetic_f32(ctx.p, static_cast<float*>(qkv_f32[i].p), all_elems, 0, cfg.seed + 1,
+        check(swiftkv_fill_synthetic_f32(ctx.p, static_cast<float*>(qkv_f32[i].p), in_elems, 0, cfg.seed + 1,
                                          1000 + i, dist, (cfg.outliers && i == 1) ? 1 : 0),
               "swiftkv_fill_synthetic_f32");
+    const bool finalized = cfg.q17 || (cfg.exact && cfg.parts > 1);
     std::unique_ptr<DeviceBuffer> qkv_q17[3];
-    if (cfg.q17) {
+    if (finalized) {
         for (int i = 0; i < 3; ++i) {
             qkv_q17[i] = std::make_unique<DeviceBuffer>(ctx.p, all_elems * 4);
-            check(swiftkv_convert_f32_q17(ctx.p, static_cast<const float*>(qkv_f32[i].p),
-                                          static_cast<std::int32_t*>(qkv_q17[i]->p), all_elems),
-                  "swiftkv_convert_f32_q17");
+            const float* src = static_cast<const float*>(qkv_f32[i].p);
+            std::int32_t* dst = static_cast<std::int32_t*>(qkv_q17[i]->p);
+            if (cfg.parts > 1)
+                check(swiftkv_convert_partials_q17(ctx.p, src, cfg.parts, static_cast<std::int64_t>(all_elems), dst,
+                                                   all_elems),
+                      "swiftkv_convert_partials_q17");
+            else
+                check(swiftkv_convert_f32_q17(ctx.p, src, dst, all_elems), "swiftkv_convert_f32_q17");
         }
     }
-    auto input = [&](int i) -> void* { return cfg.q17 ? qkv_q17[i]->p : qkv_f32[i].p; };
+    const int step_parts = finalized ? 1 : cfg.parts;   // partial rows each step call reads per input
+    const std::size_t feed_elems = finalized ? all_elems : in_elems;
+    auto input = [&](int i) -> void* { return finalized ? qkv_q17[i]->p : qkv_f32[i].p; };
 
     // Outputs: FP32 rows (or the Q15.17 state for --exact) and the A14/E8M0 words.
     DeviceBuffer out(ctx.p, row_elems * 4);
@@ -303,8 +324,8 @@ int run(const Config& cfg) {
     if (cfg.host_io) {
         check(swiftkv_synchronize(ctx.p), "swiftkv_synchronize");
         for (int i = 0; i < 3; ++i) {
-            host_in.emplace_back(all_elems * 4);
-            check(swiftkv_memcpy_d2h(ctx.p, host_in.back().data(), input(i), all_elems * 4), "swiftkv_memcpy_d2h");
+            host_in.emplace_back(feed_elems * 4);
+            check(swiftkv_memcpy_d2h(ctx.p, host_in.back().data(), input(i), feed_elems * 4), "swiftkv_memcpy_d2h");
         }
         host_out.resize(row_elems * 4);
         host_aq.resize(static_cast<std::size_t>(cfg.batch) * kGroupsPerSequence * SWIFTKV_A14_WORD_BYTES);
@@ -339,9 +360,15 @@ int run(const Config& cfg) {
                 as = static_cast<std::uint8_t*>(act_scale.p);
             }
             if (cfg.exact) {
-                check(swiftkv_attention_exact(ctx.p, q, k, v, cfg.q17 ? 1 : 0, kv.p, lut.p, aq, as, layer,
+                check(swiftkv_attention_exact(ctx.p, q, k, v, finalized ? 1 : 0, kv.p, lut.p, aq, as, layer,
                                               positions.data(), cfg.batch, static_cast<std::int32_t*>(o)),
                       "swiftkv_attention_exact");
+            } else if (step_parts > 1) {
+                check(swiftkv_attention_partials(ctx.p, static_cast<const float*>(q), static_cast<const float*>(k),
+                                                 static_cast<const float*>(v), step_parts,
+                                                 static_cast<std::int64_t>(all_elems), kv.p, lut.p, aq, as, layer,
+                                                 positions.data(), cfg.batch, static_cast<float*>(o)),
+                      "swiftkv_attention_partials");
             } else if (cfg.q17) {
                 check(swiftkv_attention_q17(ctx.p, static_cast<const std::int32_t*>(q),
                                             static_cast<const std::int32_t*>(k), static_cast<const std::int32_t*>(v),
@@ -414,7 +441,7 @@ int run(const Config& cfg) {
     const double ms = cfg.host_io ? wall_ms : static_cast<double>(device_ms);
     std::uint64_t bytes = 0;
     for (int s = 0; s < cfg.steps; ++s)
-        bytes += static_cast<std::uint64_t>(cfg.batch) * cfg.layers * step_bytes(cfg.decode ? p0 + s : p0);
+        bytes += static_cast<std::uint64_t>(cfg.batch) * cfg.layers * step_bytes(cfg.decode ? p0 + s : p0, step_parts);
     const double us_per_layer = 1000.0 * ms / cfg.steps / cfg.layers;
     const double gbps = static_cast<double>(bytes) / (ms * 1e-3) / 1e9;
     const double tokens_per_s = static_cast<double>(cfg.batch) * cfg.steps / (ms * 1e-3);
@@ -424,6 +451,7 @@ int run(const Config& cfg) {
               << "  batch " << cfg.batch << ", " << cfg.layers << " layers, position " << p0
               << (cfg.decode ? " advancing" : "") << ", " << cfg.steps << " steps"
               << (cfg.exact ? ", integer-compatibility entry" : (cfg.q17 ? ", Q15.17 inputs" : ", FP32 inputs"))
+              << (cfg.parts > 1 ? ", " + std::to_string(cfg.parts) + " split-K partials per input" : std::string())
               << (cfg.graph ? ", graph replay" : "") << (cfg.host_io ? ", host-memory I/O" : "") << "\n"
               << "  setup " << setup_ms << " ms; timed " << ms << " ms (" << (cfg.host_io ? "wall" : "device")
               << " clock; wall " << wall_ms << " ms)\n"

@@ -24,7 +24,8 @@ def test_help_and_argument_errors():
                         (["--steps", "x"], "--steps x"), (["--frobnicate"], "unknown option"),
                         (["--decode", "--graph"], "cannot advance"), (["--host-io", "--graph"], "cannot be recorded"),
                         (["--context", "32768", "--decode", "--steps", "2"], "beyond the cache limit"),
-                        (["--theta", "0.5"], "--theta")):
+                        (["--theta", "0.5"], "--theta"), (["--parts", "3"], "--parts must be"),
+                        (["--parts", "4", "--q17"], "excludes --q17")):
         r = run(*bad)
         assert r.returncode == 1, bad
         assert needle in r.stderr, (bad, r.stderr)
@@ -49,7 +50,8 @@ def _result(r):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("mode", [[], ["--q17"], ["--exact"], ["--graph"], ["--host-io"],
-                                  ["--decode", "--t3", "--outliers"]])
+                                  ["--decode", "--t3", "--outliers"], ["--parts", "4"], ["--parts", "2", "--host-io"],
+                                  ["--parts", "4", "--exact"]])
 def test_host_driver_modes(mode):
     print(f"case: swiftkv_host {' '.join(mode)}", flush=True)
     sys.stdout.flush()
