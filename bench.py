@@ -26,6 +26,10 @@ position 32256 to 32767 on Student-t(3) data (one layer), and the batch-64
 call with host-memory inputs and outputs (PCIe included; never `value`).
 The batch-64 and batch-1 workloads are also timed through the entry that
 takes the Q/K/V projection's split-K FP32 partials (--parts, default 4).
+On the host: the reference emulator's attention stage at position 4095 (one
+thread as shipped, and with its OpenMP pragmas), the FP32 tolerance oracle
+(reported apart from the reference), and the reference's attention loop at
+position 32256 extrapolated to the batch-16 512-step run.
 """
 import argparse
 import json
@@ -270,6 +274,27 @@ def cpu_model() -> str:
     return "unknown"
 
 
+_CPU_CACHES = {}
+
+
+def _cpu_cache(position: int):
+    """The oracle's host cache of one sequence filled to `position` tokens by
+    the append rule from seeded N(0,1) rows, with that step's q/k/v; built
+    once and shared by the CPU timings."""
+    if position not in _CPU_CACHES:
+        sys.path.insert(0, os.path.join(REPO, "oracle"))
+        sys.path.insert(0, os.path.join(REPO, "tests"))
+        import oracle as O
+        from helpers import f32_normal
+        cos, sin = O.rope_values(position + 1)
+        sc = O.SequenceCache(32, position + 1)
+        sc.fill_q17(O.f2q17(f32_normal(7, (position, 4096))), O.f2q17(f32_normal(8, (position, 4096))), 0, cos,
+                    sin)
+        qkv = [O.f2q17(f32_normal(9 + i, (4096,))) for i in range(3)]
+        _CPU_CACHES[position] = (cos, sin, sc, qkv)
+    return _CPU_CACHES[position]
+
+
 def cpu_baseline(target_seconds: float, position: int, omp: bool):
     """The reference emulator's attention stage (oracle/_ref, compiled from the
     reference source) on this host: one sequence x 32 heads per call at
@@ -277,17 +302,13 @@ def cpu_baseline(target_seconds: float, position: int, omp: bool):
     sys.path.insert(0, os.path.join(REPO, "oracle"))
     sys.path.insert(0, os.path.join(REPO, "tests"))
     import oracle as O
-    from helpers import f32_normal
     if not O.Reference.available(omp):
         return None
     R = O.Reference(omp=omp)
-    cos, sin = O.rope_values(position + 1)
+    cos, sin, sc, (q, k, v) = _cpu_cache(position)
     R.set_rope(cos, sin)
-    sc = O.SequenceCache(32, position + 1)
-    sc.fill_q17(O.f2q17(f32_normal(7, (position, 4096))), O.f2q17(f32_normal(8, (position, 4096))), 0, cos, sin)
     rc = R.cache(position + 1)
     rc.load_from(sc, position)
-    q, k, v = (O.f2q17(f32_normal(9 + i, (4096,))) for i in range(3))
     qr, kr = R.apply_rope(q, position), R.apply_rope(k, position)
     rc.attention(qr, kr, v, position)          # warm-up call
     times = []
@@ -309,6 +330,61 @@ def cpu_baseline(target_seconds: float, position: int, omp: bool):
         "sample": (f"{len(times)} calls of the reference emulator's swiftkv_attention_4pe (32 heads, one "
                    f"sequence, one layer, position {position}), median; batch-64 figure = 64 x per-call"),
     }
+
+
+def cpu_fp32_oracle(target_seconds: float, position: int):
+    """The FP32 tolerance oracle (oracle/swiftkv_oracle.c: the append rule,
+    then the FP32 softmax formula with double accumulation) on this host, one
+    thread, one sequence x 32 heads per call at `position`.  Timed separately
+    from the reference: it is the checker, not the reference."""
+    cos, sin, sc, (q, k, v) = _cpu_cache(position)
+    sc.step_q17(q, k, v, position, cos[position], sin[position], fp=True)   # warm-up call
+    times = []
+    t_start = time.perf_counter()
+    while time.perf_counter() - t_start < target_seconds or len(times) < 3:
+        t0 = time.perf_counter()
+        sc.step_q17(q, k, v, position, cos[position], sin[position], fp=True)
+        times.append(time.perf_counter() - t0)
+    per_call = float(np.median(times))
+    return {"us_per_sequence_layer": round(per_call * 1e6, 1), "gbps": round(step_bytes(position) / per_call / 1e9, 3),
+            "cores": 1, "kind": "oracle (FP32 formula, double accumulation)",
+            "sample": f"{len(times)} calls at position {position}, one sequence x 32 heads, median"}
+
+
+def cpu_reference_long_context(calls: int, position: int, batch: int, steps: int):
+    """The reference emulator's attention loop (oracle/_ref, one thread) at a
+    position beyond its own 4096-token limit, for the batch-16 32K decode run:
+    `calls` calls of one sequence at `position` (q/k rotated by the oracle's
+    extended table, cache rows random codes -- the loop's cost does not depend
+    on their values), scaled to batch x steps calls at the run's mean position."""
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import oracle as O
+    if not O.Reference.available(False):
+        return None
+    R = O.Reference(omp=False)
+    rng = np.random.default_rng(11)
+    sc = O.SequenceCache(32, position + 1)
+    sc.kc[:] = rng.integers(-127, 128, sc.kc.shape, dtype=np.int8)
+    sc.vc[:] = rng.integers(-127, 128, sc.vc.shape, dtype=np.int8)
+    sc.ks[:] = rng.integers(0, 8, sc.ks.shape, dtype=np.uint8)
+    sc.vs[:] = rng.integers(0, 8, sc.vs.shape, dtype=np.uint8)
+    rc = R.cache(position + 1)
+    rc.load_from(sc, position)
+    del sc
+    q, k, v = (rng.integers(-(1 << 18), 1 << 18, 4096, dtype=np.int32) for _ in range(3))
+    times = []
+    for _ in range(calls):
+        t0 = time.perf_counter()
+        rc.attention(q, k, v, position)
+        times.append(time.perf_counter() - t0)
+    per_call = float(np.median(times))
+    mean_pos = position + (steps - 1) / 2.0
+    total_s = per_call * (mean_pos + 1) / (position + 1) * batch * steps
+    return {"us_per_sequence_step": round(per_call * 1e6, 1), "extrapolated_total_s": round(total_s, 1),
+            "cores": 1, "kind": "reference",
+            "sample": (f"{calls} calls of the reference emulator's swiftkv_attention_4pe at position {position} "
+                       f"(one sequence, 32 heads), median; extrapolated to {batch} sequences x {steps} steps "
+                       f"at the mean position")}
 
 
 def main():
@@ -401,6 +477,14 @@ def main():
             if omp:
                 cpu["openmp"] = {"value": omp["value"], "cores": omp["cores"],
                                  "us_per_layer_batch1": omp["us_per_layer_batch1"]}
+        oracle_fp = cpu_fp32_oracle(max(2.0, args.cpu_seconds / 4), args.context - 1)
+        log(f"[bench] cpu FP32 oracle: {oracle_fp['us_per_sequence_layer']:.0f} us per sequence-layer")
+        if extra:
+            long_ref = cpu_reference_long_context(2, 32256, 16, 512)
+            if long_ref:
+                extra["batch16_positions32256to32767_1layer_t3"]["cpu_reference"] = long_ref
+                log(f"[bench] cpu reference at position 32256: {long_ref['us_per_sequence_step']:.0f} us per "
+                    f"sequence-step")
 
     att = main_res["kernel_avg_us"]["step"]
     traffic, traffic_src = profiled_traffic(args.batch, args.context)
@@ -434,6 +518,8 @@ def main():
                      "avg_launch_us": round(att, 2) if att else None},
         "cpu_baseline": cpu,
     }
+    if not args.no_cpu:
+        line["cpu_fp32_oracle"] = oracle_fp
     if main_res["exact"]:
         e = main_res["exact"]
         line["integer_exact_path"] = {"us_per_layer": round(e["us_per_layer"], 1), "gbps": round(e["gbps"], 1),

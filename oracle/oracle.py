@@ -312,6 +312,7 @@ class Reference:
         L.ref_cache_create.argtypes = [C.c_int]
         L.ref_cache_destroy.argtypes = [C.c_void_p]
         L.ref_cache_row.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, _i8p, _u8p, _i8p, _u8p]
+        L.ref_cache_rows.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, _i8p, _u8p, _i8p, _u8p]
         L.ref_attention.argtypes = [C.c_void_p, _i32p, _i32p, _i32p, C.c_int, _i16p, _f32p]
         L.ref_omp_threads.restype = C.c_int
         self.L = L
@@ -353,10 +354,9 @@ class _RefCache:
 
     def load_from(self, sc: SequenceCache, ntok: int):
         for h in range(sc.heads):
-            for t in range(ntok):
-                self.L.ref_cache_row(self.h, 0, h, t, np.ascontiguousarray(sc.kc[h, t]),
-                                     np.ascontiguousarray(sc.ks[h, t]), np.ascontiguousarray(sc.vc[h, t]),
-                                     np.ascontiguousarray(sc.vs[h, t]))
+            self.L.ref_cache_rows(self.h, h, 0, ntok, np.ascontiguousarray(sc.kc[h, :ntok]),
+                                  np.ascontiguousarray(sc.ks[h, :ntok]), np.ascontiguousarray(sc.vc[h, :ntok]),
+                                  np.ascontiguousarray(sc.vs[h, :ntok]))
 
     def row(self, head: int, token: int):
         kc = np.empty(HD, np.int8)
