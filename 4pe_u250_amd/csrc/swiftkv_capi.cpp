@@ -242,6 +242,10 @@ struct StepInput {
 };
 constexpr StepInput kF32Input{kInF32, 0}, kQ17Input{kInQ17, 0};
 
+// Largest distance between split-K partials (2^40 elements, 4 TiB): keeps
+// every extent computed from it far from overflow.
+constexpr int64_t kMaxPartStride = int64_t(1) << 40;
+
 int validate_step(swiftkv_context* ctx, const void* q, const void* k, const void* v,
                   const swiftkv_kv_cache* kv, const swiftkv_rope_lut* lut, const uint8_t* act_q,
                   const uint8_t* act_scale, int32_t layer, const int32_t* positions, int32_t batch,
@@ -771,6 +775,9 @@ int swiftkv_attention_partials(swiftkv_context* ctx, const float* q, const float
     if (!ctx) return fail(SWIFTKV_EINVAL, "null context");
     if (parts != 1 && parts != 2 && parts != 4) return fail(SWIFTKV_EINVAL, "parts = %d: must be 1, 2 or 4", parts);
     const int64_t rows_elems = static_cast<int64_t>(batch) * kModelDim;
+    if (parts > 1 && part_stride > kMaxPartStride)
+        return fail(SWIFTKV_EINVAL, "part_stride %lld exceeds %lld elements", static_cast<long long>(part_stride),
+                    static_cast<long long>(kMaxPartStride));
     if (parts > 1 && part_stride < rows_elems)
         return fail(SWIFTKV_EINVAL, "part_stride %lld is below batch * 4096 = %lld: partials would overlap",
                     static_cast<long long>(part_stride), static_cast<long long>(rows_elems));
@@ -938,6 +945,9 @@ int swiftkv_convert_partials_q17(swiftkv_context* ctx, const float* in, int32_t 
                                  int32_t* out, size_t n) {
     if (!ctx || (n && (!in || !out))) return fail(SWIFTKV_EINVAL, "null argument");
     if (parts != 1 && parts != 2 && parts != 4) return fail(SWIFTKV_EINVAL, "parts = %d: must be 1, 2 or 4", parts);
+    if (parts > 1 && part_stride > kMaxPartStride)
+        return fail(SWIFTKV_EINVAL, "part_stride %lld exceeds %lld elements", static_cast<long long>(part_stride),
+                    static_cast<long long>(kMaxPartStride));
     if (parts > 1 && (part_stride < 0 || static_cast<uint64_t>(part_stride) < n))
         return fail(SWIFTKV_EINVAL, "part_stride %lld is below n = %zu: partials would overlap",
                     static_cast<long long>(part_stride), n);

@@ -175,6 +175,8 @@ int swiftkv_attention_q17(swiftkv_context* ctx, const int32_t* q, const int32_t*
  * reduce/convert pass or intermediate buffer is needed.
  *   parts        1 (same as swiftkv_attention_f32), 2 or 4; other values
  *                SWIFTKV_EINVAL
+ *   part_stride  ignored for parts = 1; otherwise batch * 4096 <= part_stride
+ *                <= 2^40, else SWIFTKV_EINVAL
  * Other arguments as for swiftkv_attention_f32. */
 int swiftkv_attention_partials(swiftkv_context* ctx, const float* q, const float* k, const float* v,
                                int32_t parts, int64_t part_stride, swiftkv_kv_cache* kv_cache,
@@ -260,7 +262,7 @@ int swiftkv_convert_f32_q17(swiftkv_context* ctx, const float* in, int32_t* out,
 /* The Q/K/V linear stage's finalize on the device: out[i] = Q15.17 of the
  * `parts` FP32 partials in[i + p * part_stride] reduced in the reference's
  * order (see swiftkv_attention_partials; int4_linear_controller.cpp:1089-1118).
- * parts 1, 2 or 4; part_stride >= n for parts > 1; device pointers.  Feeds
+ * parts 1, 2 or 4; n <= part_stride <= 2^40 for parts > 1; device pointers.  Feeds
  * swiftkv_attention_exact (q17 = 1) with the inputs the reference's attention
  * stage receives. */
 int swiftkv_convert_partials_q17(swiftkv_context* ctx, const float* in, int32_t parts,

@@ -215,7 +215,7 @@ def test_partials_error_codes(skv, ctx, lut4096):
     kv = skv.KVCache(ctx, layers=1, max_batch=2, max_seq_len=64)
     buf = ctx.alloc(4 * 2 * 4096 * 4)
     out = ctx.alloc(2 * 4096 * 4)
-    for parts, stride in [(3, 8192), (0, 8192), (4, 8191), (2, -1)]:
+    for parts, stride in [(3, 8192), (0, 8192), (4, 8191), (2, -1), (4, (1 << 40) + 1)]:
         with pytest.raises(skv.SwiftKVError) as ei:
             skv.swiftkv_attention_partials(ctx, buf, buf, buf, parts, kv, lut4096, None, None, 0, [5, 6], out,
                                            part_stride=stride)
@@ -224,6 +224,8 @@ def test_partials_error_codes(skv, ctx, lut4096):
         ctx.convert_partials_q17(buf, out, 100, 3, 100)
     with pytest.raises(skv.SwiftKVError):
         ctx.convert_partials_q17(buf, out, 100, 2, 99)
+    with pytest.raises(skv.SwiftKVError):
+        ctx.convert_partials_q17(buf, out, 100, 4, (1 << 40) + 1)
     buf.free()
     out.free()
     kv.close()
