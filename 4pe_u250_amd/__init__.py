@@ -95,6 +95,8 @@ _SIGNATURES = {
     "swiftkv_memset_d": (C.c_int, [_vp, _vp, C.c_int, _sz]),
     "swiftkv_convert_f32_q17": (C.c_int, [_vp, _vp, _vp, _sz]),
     "swiftkv_convert_partials_q17": (C.c_int, [_vp, _vp, _i32, C.c_int64, _vp, _sz]),
+    "swiftkv_a14_unpack": (C.c_int, [_vp, _sz, _vp]),
+    "swiftkv_a14_decode": (C.c_int, [_vp, _vp, _sz, _vp]),
     "swiftkv_capture_begin": (C.c_int, [_vp]),
     "swiftkv_capture_end": (C.c_int, [_vp, C.POINTER(_vp)]),
     "swiftkv_graph_launch": (C.c_int, [_vp, _vp]),
@@ -495,6 +497,30 @@ def swiftkv_append_tokens(ctx: Context, k, v, kv_cache: KVCache, rope_lut: RopeL
     _check(lib().swiftkv_append_tokens(ctx.handle, _io_ptr(ctx, k, it), _io_ptr(ctx, v, it), 1 if q17 else 0,
                                        kv_cache.handle, rope_lut.handle, int(layer_index), int(seq), int(pos0),
                                        int(n)))
+
+
+def a14_unpack(words: np.ndarray) -> np.ndarray:
+    """Packed A14 words [..., 56] bytes -> int16 lanes [..., 32] through the C ABI."""
+    w = np.ascontiguousarray(words, dtype=np.uint8)
+    if w.shape[-1] != 56:
+        raise ValueError("A14 words are 56 bytes")
+    groups = w.size // 56
+    out = np.empty(w.shape[:-1] + (32,), np.int16)
+    _check(lib().swiftkv_a14_unpack(w.ctypes.data, groups, out.ctypes.data))
+    return out
+
+
+def a14_decode(words: np.ndarray, e8m0: np.ndarray) -> np.ndarray:
+    """Packed A14 words [..., 56] and their E8M0 bytes [...] -> the float values
+    lane * 2^(code - 140) [..., 32] the O projection multiplies (C ABI)."""
+    w = np.ascontiguousarray(words, dtype=np.uint8)
+    e = np.ascontiguousarray(e8m0, dtype=np.uint8)
+    if w.shape[-1] != 56 or e.shape != w.shape[:-1]:
+        raise ValueError("words must be [..., 56] bytes and e8m0 [...] bytes")
+    groups = w.size // 56
+    out = np.empty(w.shape[:-1] + (32,), np.float32)
+    _check(lib().swiftkv_a14_decode(w.ctypes.data, e.ctypes.data, groups, out.ctypes.data))
+    return out
 
 
 def unpack_a14(words: np.ndarray) -> np.ndarray:

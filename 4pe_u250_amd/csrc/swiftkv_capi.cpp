@@ -957,6 +957,36 @@ int swiftkv_convert_partials_q17(swiftkv_context* ctx, const float* in, int32_t 
     return ok();
 }
 
+// ---------------------------------------------------------------- A14 words (host)
+
+int swiftkv_a14_unpack(const uint8_t* words, size_t groups, int16_t* lanes) {
+    if (groups && (!words || !lanes)) return fail(SWIFTKV_EINVAL, "null argument");
+    for (size_t g = 0; g < groups; ++g) {
+        const uint8_t* w = words + g * SWIFTKV_A14_WORD_BYTES;
+        for (int i = 0; i < kGroup; ++i) {
+            const int bit = 14 * i;
+            // 14 bits starting at `bit` span at most three bytes of the word
+            uint32_t raw = 0;
+            for (int b = 0; b < 3 && (bit >> 3) + b < SWIFTKV_A14_WORD_BYTES; ++b)
+                raw |= static_cast<uint32_t>(w[(bit >> 3) + b]) << (8 * b);
+            const uint32_t v = (raw >> (bit & 7)) & 0x3fffu;
+            lanes[g * kGroup + i] = static_cast<int16_t>((v & 0x2000u) ? static_cast<int32_t>(v) - 0x4000 : v);
+        }
+    }
+    return ok();
+}
+
+int swiftkv_a14_decode(const uint8_t* words, const uint8_t* e8m0, size_t groups, float* values) {
+    if (groups && (!words || !e8m0 || !values)) return fail(SWIFTKV_EINVAL, "null argument");
+    int16_t lanes[kGroup];
+    for (size_t g = 0; g < groups; ++g) {
+        (void)swiftkv_a14_unpack(words + g * SWIFTKV_A14_WORD_BYTES, 1, lanes);
+        const int e = static_cast<int>(e8m0[g]) - 127 - 13;
+        for (int i = 0; i < kGroup; ++i) values[g * kGroup + i] = std::ldexp(static_cast<float>(lanes[i]), e);
+    }
+    return ok();
+}
+
 // ---------------------------------------------------------------- graphs
 
 int swiftkv_capture_begin(swiftkv_context* ctx) {

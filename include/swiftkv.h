@@ -268,6 +268,17 @@ int swiftkv_convert_f32_q17(swiftkv_context* ctx, const float* in, int32_t* out,
 int swiftkv_convert_partials_q17(swiftkv_context* ctx, const float* in, int32_t parts,
                                  int64_t part_stride, int32_t* out, size_t n);
 
+/* A14 activation words on the host (no device work).  A word is 56 bytes,
+ * the reference's ap_uint<448>: 32 signed 14-bit lanes, lane i at bits
+ * [14i, 14i+13] (swiftkv_attention.cpp:1761-1768).  _unpack writes the lanes
+ * as int16 [groups][32]; _decode writes what the O projection multiplies,
+ * lane * 2^(code - 140) as float [groups][32], with code the group's E8M0
+ * byte (the consumer takes code - 127 - 13 as the group exponent,
+ * int4_linear_controller.cpp:643-645).  Returns SWIFTKV_EINVAL on a null
+ * pointer with groups > 0. */
+int swiftkv_a14_unpack(const uint8_t* words, size_t groups, int16_t* lanes);
+int swiftkv_a14_decode(const uint8_t* words, const uint8_t* e8m0, size_t groups, float* values);
+
 /* --------------------------------------------------------------------------
  * HIP graphs: record a sequence of asynchronous calls (steps, appends,
  * synthetic fills) once and replay it with one launch, e.g. the 32 per-layer

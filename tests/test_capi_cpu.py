@@ -84,6 +84,32 @@ def test_unpack_a14_roundtrip(skv, oracle):
     assert (skv.unpack_a14(oracle.pack_a14(q)) == q).all()
 
 
+def test_a14_unpack_and_decode_through_the_abi(skv, oracle):
+    """The ABI's host unpacker against the oracle's packer (the reference's lane
+    layout) and the mirror's independent numpy unpacker; the decode against
+    lane * 2^(code - 140) in double precision, saturating to inf like the
+    float it returns."""
+    rng = np.random.default_rng(5)
+    q = rng.integers(-8192, 8192, (300, 32)).astype(np.int16)
+    q[0] = 0
+    q[1] = -8192
+    q[2] = 8191
+    q[3, ::2] = -1
+    words = oracle.pack_a14(q)
+    assert (skv.a14_unpack(words) == q).all()
+    assert (skv.unpack_a14(words) == q).all()
+    codes = rng.integers(0, 256, 300).astype(np.uint8)
+    codes[:4] = [0, 127, 140, 255]
+    got = skv.a14_decode(words, codes)
+    with np.errstate(over="ignore"):
+        want = np.ldexp(q.astype(np.float64), codes.astype(np.int64)[:, None] - 140).astype(np.float32)
+    assert (got.view(np.uint32) == want.view(np.uint32)).all()
+    L = skv.lib()
+    assert L.swiftkv_a14_unpack(None, 1, None) == skv.EINVAL
+    assert L.swiftkv_a14_decode(None, None, 1, None) == skv.EINVAL
+    assert L.swiftkv_a14_unpack(None, 0, None) == skv.OK
+
+
 def test_scale_bits(skv, oracle):
     s = np.arange(26, dtype=np.uint8)
     assert (skv.scale_bits(s) == oracle.shift_scale_bits(s)).all()
