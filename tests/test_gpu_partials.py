@@ -229,3 +229,43 @@ def test_partials_error_codes(skv, ctx, lut4096):
     buf.free()
     out.free()
     kv.close()
+
+
+def test_partials_graph_replay_matches_eager(skv, ctx, lut4096):
+    """The partial-input step recorded into a HIP graph (batch 1, eight splits
+    merged inside the launch) and replayed three times, with eager work and
+    synchronizations between the replays: every replay equals the eager call
+    bit for bit."""
+    _note("attention_partials: HIP graph replay vs eager")
+    positions = [2000]
+    kv = skv.KVCache(ctx, layers=1, max_batch=1, max_seq_len=2048)
+    kh, vh = history(960, 2000)
+    prefill(skv, ctx, kv, lut4096, 0, 0, kh, vh)
+    stride = 4096 + 32
+    d = [_upload_parts(ctx, cancelling_partials(970 + i, 4, (1, 4096)), stride) for i in range(3)]
+    out, aq, asc = ctx.alloc(4096 * 4), ctx.alloc(128 * 56), ctx.alloc(128)
+
+    def step():
+        skv.swiftkv_attention_partials(ctx, *d, 4, kv, lut4096, aq, asc, 0, positions, out, part_stride=stride)
+
+    def snapshot():
+        ctx.synchronize()
+        return (out.download(np.float32, (4096,)), aq.download(np.uint8, (128, 56)), asc.download(np.uint8, (128,)))
+
+    step()
+    eager = snapshot()
+    ctx.capture_begin()
+    step()
+    g = ctx.capture_end()
+    scratch = ctx.alloc(4096 * 4)
+    for rep in range(3):
+        out.zero()
+        g.launch()
+        ctx.convert_partials_q17(d[0], scratch, 4096, 4, stride)   # eager work between replays
+        got = snapshot()
+        assert (got[0].view(np.uint32) == eager[0].view(np.uint32)).all(), f"replay {rep}: output differs"
+        assert (got[1] == eager[1]).all() and (got[2] == eager[2]).all(), f"replay {rep}: A14/E8M0 differ"
+    g.close()
+    for x in d + [out, aq, asc, scratch]:
+        x.free()
+    kv.close()
