@@ -455,8 +455,9 @@ def main():
         if b1["partials"]:
             log(f"[bench] batch 1, {args.parts} split-K partials: {b1['partials']['us_per_layer']:.2f} us/layer")
     if not args.no_configs:
-        r = run_gpu(skv, ctx, [127], 1, 200, args.warmup, seed=2028)
-        extra["batch1_position127_1layer"] = summary(r)
+        # One launch per step: a graph of a single node would time hipGraphLaunch, not the kernel.
+        r = run_gpu(skv, ctx, [127], 1, 200, args.warmup, seed=2028, graph=False)
+        extra["batch1_position127_1layer"] = summary(r, graph=False)
         r = run_gpu(skv, ctx, [2047], 32, 20, args.warmup, seed=2029)
         extra["batch1_position2047_32layers"] = summary(r)
         rng = np.random.default_rng(4)
