@@ -148,6 +148,9 @@ class DeviceBuffer:
 
     def __init__(self, ctx: "Context", nbytes: int):
         self.ctx = ctx
+        # The C context outlives Context.close() while this buffer exists, so
+        # the buffer keeps the raw handle to free itself later.
+        self._ctx_handle = ctx.handle
         self.nbytes = int(nbytes)
         p = C.c_void_p()
         _check(lib().swiftkv_device_alloc(ctx.handle, self.nbytes, C.byref(p)))
@@ -178,13 +181,13 @@ class DeviceBuffer:
 
     def free(self) -> None:
         if self.ptr:
-            _check(lib().swiftkv_device_free(self.ctx.handle, C.c_void_p(self.ptr)))
-            self.ptr = None
+            ptr, self.ptr = self.ptr, None
+            _check(lib().swiftkv_device_free(self._ctx_handle, C.c_void_p(ptr)))
 
     def __del__(self):
         try:
-            if self.ptr and self.ctx.handle:
-                lib().swiftkv_device_free(self.ctx.handle, C.c_void_p(self.ptr))
+            if self.ptr:
+                lib().swiftkv_device_free(self._ctx_handle, C.c_void_p(self.ptr))
         except Exception:
             pass
 
@@ -285,8 +288,14 @@ class Graph:
 
     def close(self) -> None:
         if self.handle:
-            _check(lib().swiftkv_graph_destroy(self.handle))
-            self.handle = None
+            h, self.handle = self.handle, None
+            _check(lib().swiftkv_graph_destroy(h))
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 class RopeLut:
@@ -321,8 +330,14 @@ class RopeLut:
 
     def close(self) -> None:
         if self.handle:
-            _check(lib().swiftkv_rope_lut_destroy(self.handle))
-            self.handle = None
+            h, self.handle = self.handle, None
+            _check(lib().swiftkv_rope_lut_destroy(h))
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 class KVCache:
@@ -374,8 +389,14 @@ class KVCache:
 
     def close(self) -> None:
         if self.handle:
-            _check(lib().swiftkv_kv_cache_destroy(self.handle))
-            self.handle = None
+            h, self.handle = self.handle, None
+            _check(lib().swiftkv_kv_cache_destroy(h))
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 def _ptr(x) -> Optional[int]:

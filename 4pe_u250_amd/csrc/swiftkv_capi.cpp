@@ -18,6 +18,7 @@
 #include <cstring>
 #include <new>
 #include <string>
+#include <unordered_set>
 #include <vector>
 
 #include "swiftkv_common.hpp"
@@ -86,6 +87,12 @@ struct swiftkv_context {
     bool host_io = false;
     uint8_t* io_stage = nullptr;
     size_t io_bytes = 0;
+    // Objects created from the context (caches, tables, graphs, device
+    // buffers) may outlive swiftkv_context_destroy: the context is only
+    // marked released then, and freed when the last of them is destroyed.
+    int64_t children = 0;
+    bool released = false;
+    std::unordered_set<void*> buffers;   // swiftkv_device_alloc allocations not yet freed
 };
 
 struct swiftkv_graph {
@@ -114,8 +121,16 @@ struct swiftkv_kv_cache {
 namespace {
 
 int set_device(const swiftkv_context* ctx) {
+    if (ctx->released) return fail(SWIFTKV_ESTATE, "the context has been destroyed");
     SKV_HIP(hipSetDevice(ctx->device));
     return SWIFTKV_OK;
+}
+
+void free_context(swiftkv_context* ctx);
+
+// One object created from `ctx` has been destroyed.
+void release_child(swiftkv_context* ctx) {
+    if (--ctx->children == 0 && ctx->released) free_context(ctx);
 }
 
 // Entry points that synchronize, copy, allocate or memset cannot be recorded.
@@ -193,6 +208,7 @@ int upload_lut(swiftkv_context* ctx, std::vector<int2>&& host, int32_t positions
         delete lut;
         return fail(SWIFTKV_EHIP, "RoPE table upload: %s", hipGetErrorString(e));
     }
+    ++ctx->children;
     *out = lut;
     return ok();
 }
@@ -448,6 +464,23 @@ float shift_to_scale(uint32_t s) {
     return f;
 }
 
+// Releases everything the context owns (after its last object is gone).
+void free_context(swiftkv_context* ctx) {
+    (void)hipSetDevice(ctx->device);
+    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->partials) (void)hipFree(ctx->partials);
+    if (ctx->counters) (void)hipFree(ctx->counters);
+    if (ctx->io_stage) (void)hipFree(ctx->io_stage);
+    for (auto& t : ctx->timers)
+        if (t) (void)hipEventDestroy(t);
+    for (auto& p : ctx->profile_pool) {
+        (void)hipEventDestroy(p.begin);
+        (void)hipEventDestroy(p.end);
+    }
+    if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+}
+
 }  // namespace
 
 extern "C" {
@@ -481,24 +514,15 @@ int swiftkv_context_create(int device, swiftkv_context** out) {
 
 int swiftkv_context_destroy(swiftkv_context* ctx) {
     if (!ctx) return ok();
+    if (ctx->released) return fail(SWIFTKV_ESTATE, "the context has already been destroyed");
     if (ctx->capturing) {   // abandon the recording so the stream can be released
         hipGraph_t g = nullptr;
+        (void)hipSetDevice(ctx->device);
         if (hipStreamEndCapture(ctx->stream, &g) == hipSuccess && g) (void)hipGraphDestroy(g);
         ctx->capturing = false;
     }
-    (void)hipSetDevice(ctx->device);
-    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
-    if (ctx->partials) (void)hipFree(ctx->partials);
-    if (ctx->counters) (void)hipFree(ctx->counters);
-    if (ctx->io_stage) (void)hipFree(ctx->io_stage);
-    for (auto& t : ctx->timers)
-        if (t) (void)hipEventDestroy(t);
-    for (auto& p : ctx->profile_pool) {
-        (void)hipEventDestroy(p.begin);
-        (void)hipEventDestroy(p.end);
-    }
-    if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
-    delete ctx;
+    ctx->released = true;
+    if (ctx->children == 0) free_context(ctx);
     return ok();
 }
 
@@ -577,11 +601,13 @@ int swiftkv_rope_lut_generate(swiftkv_context* ctx, int32_t positions, double th
 
 int swiftkv_rope_lut_destroy(swiftkv_rope_lut* lut) {
     if (!lut) return ok();
-    if (int rc = not_capturing(lut->ctx, "swiftkv_rope_lut_destroy")) return rc;
-    (void)hipSetDevice(lut->ctx->device);
-    (void)hipStreamSynchronize(lut->ctx->stream);
+    swiftkv_context* ctx = lut->ctx;
+    if (int rc = not_capturing(ctx, "swiftkv_rope_lut_destroy")) return rc;
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
     if (lut->table) (void)hipFree(lut->table);
     delete lut;
+    release_child(ctx);
     return ok();
 }
 
@@ -638,17 +664,20 @@ int swiftkv_kv_cache_create(swiftkv_context* ctx, int32_t layers, int32_t max_ba
         delete kv;
         return fail(SWIFTKV_EHIP, "KV cache zero-fill: %s", hipGetErrorString(e));
     }
+    ++ctx->children;
     *out = kv;
     return ok();
 }
 
 int swiftkv_kv_cache_destroy(swiftkv_kv_cache* kv) {
     if (!kv) return ok();
-    if (int rc = not_capturing(kv->ctx, "swiftkv_kv_cache_destroy")) return rc;
-    (void)hipSetDevice(kv->ctx->device);
-    (void)hipStreamSynchronize(kv->ctx->stream);
+    swiftkv_context* ctx = kv->ctx;
+    if (int rc = not_capturing(ctx, "swiftkv_kv_cache_destroy")) return rc;
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
     if (kv->base) (void)hipFree(kv->base);
     delete kv;
+    release_child(ctx);
     return ok();
 }
 
@@ -886,18 +915,25 @@ int swiftkv_device_alloc(swiftkv_context* ctx, size_t bytes, void** out) {
     rc = set_device(ctx);
     if (rc) return rc;
     if (hipMalloc(out, bytes ? bytes : 1) != hipSuccess) return fail(SWIFTKV_ENOMEM, "hipMalloc of %zu bytes failed", bytes);
+    ctx->buffers.insert(*out);
+    ++ctx->children;
     return ok();
 }
 
+// Also accepted after swiftkv_context_destroy, like the other destroy calls.
 int swiftkv_device_free(swiftkv_context* ctx, void* ptr) {
     if (!ctx) return fail(SWIFTKV_EINVAL, "null context");
     if (!ptr) return ok();
     int rc = not_capturing(ctx, "swiftkv_device_free");
     if (rc) return rc;
-    rc = set_device(ctx);
-    if (rc) return rc;
-    SKV_HIP(hipStreamSynchronize(ctx->stream));
-    SKV_HIP(hipFree(ptr));
+    if (ctx->buffers.erase(ptr) == 0)
+        return fail(SWIFTKV_EINVAL, "%p was not allocated by swiftkv_device_alloc on this context, or was freed", ptr);
+    SKV_HIP(hipSetDevice(ctx->device));
+    const hipError_t sync = hipStreamSynchronize(ctx->stream);
+    const hipError_t fr = hipFree(ptr);
+    release_child(ctx);
+    if (sync != hipSuccess || fr != hipSuccess)
+        return fail(SWIFTKV_EHIP, "hipFree: %s", hipGetErrorString(sync != hipSuccess ? sync : fr));
     return ok();
 }
 
@@ -1024,6 +1060,7 @@ int swiftkv_capture_end(swiftkv_context* ctx, swiftkv_graph** out) {
     g->ctx = ctx;
     g->graph = graph;
     g->exec = exec;
+    ++ctx->children;
     *out = g;
     return ok();
 }
@@ -1040,12 +1077,14 @@ int swiftkv_graph_launch(swiftkv_context* ctx, const swiftkv_graph* graph) {
 
 int swiftkv_graph_destroy(swiftkv_graph* graph) {
     if (!graph) return ok();
-    if (int rc = not_capturing(graph->ctx, "swiftkv_graph_destroy")) return rc;
-    (void)hipSetDevice(graph->ctx->device);
-    (void)hipStreamSynchronize(graph->ctx->stream);
+    swiftkv_context* ctx = graph->ctx;
+    if (int rc = not_capturing(ctx, "swiftkv_graph_destroy")) return rc;
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
     if (graph->exec) (void)hipGraphExecDestroy(graph->exec);
     if (graph->graph) (void)hipGraphDestroy(graph->graph);
     delete graph;
+    release_child(ctx);
     return ok();
 }
 

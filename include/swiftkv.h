@@ -82,6 +82,10 @@ const char* swiftkv_version(void);
  * (host/decode_host.cpp:1256-1294, 1378-1404).
  * ------------------------------------------------------------------------ */
 int swiftkv_context_create(int device, swiftkv_context** out);
+/* Objects created from a context (KV caches, RoPE tables, graphs, device
+ * buffers) may be destroyed before or after it, in any order: the context
+ * then refuses new work (SWIFTKV_ESTATE) but stays valid for those destroy
+ * calls, and its resources are released with the last of them. */
 int swiftkv_context_destroy(swiftkv_context* ctx);
 int swiftkv_synchronize(swiftkv_context* ctx);
 /* Tokens per split-context work item; 0 selects the built-in heuristic.
@@ -248,6 +252,9 @@ int swiftkv_kv_cache_fill_synthetic(swiftkv_context* ctx, swiftkv_kv_cache* kv,
 
 /* --------------------------------------------------------------------------
  * Device-memory helpers for FFI callers without a GPU framework (ctypes).
+ * swiftkv_device_free takes only pointers from swiftkv_device_alloc on the
+ * same context (anything else, or a second free: SWIFTKV_EINVAL); it waits
+ * for the context stream before freeing.
  * ------------------------------------------------------------------------ */
 int swiftkv_device_alloc(swiftkv_context* ctx, size_t bytes, void** out);
 int swiftkv_device_free(swiftkv_context* ctx, void* ptr);

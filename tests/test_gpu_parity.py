@@ -360,3 +360,32 @@ def test_graph_replay_matches_eager(skv, ctx, lut4096, rope_tables):
     for b in qkv + outs + aqs + ass + [other]:
         b.free()
     kv.close()
+
+
+def test_objects_may_outlive_their_context(skv):
+    """Destroying a context first is allowed: it refuses new work, stays valid
+    for its objects' destroy calls, and is released with the last of them."""
+    _note("case: context destroyed before its cache, table and buffer")
+    L = skv.lib()
+    c = skv.Context(0)
+    handle = c.handle
+    kv = skv.KVCache(c, layers=1, max_batch=1, max_seq_len=64)
+    lut = skv.RopeLut.generate(c, 64)
+    buf = c.alloc(4096)
+    c.close()
+    assert L.swiftkv_synchronize(handle) == skv.ESTATE
+    assert L.swiftkv_context_destroy(handle) == skv.ESTATE
+    kv.close()
+    lut.close()
+    buf.free()          # the last object: the context is released here
+
+
+def test_device_free_rejects_foreign_and_double_frees(skv, ctx):
+    _note("case: device_free argument checks")
+    L = skv.lib()
+    buf = ctx.alloc(256)
+    p = buf.ptr
+    buf.free()
+    assert L.swiftkv_device_free(ctx.handle, p) == skv.EINVAL          # second free
+    assert L.swiftkv_device_free(ctx.handle, 0x1000) == skv.EINVAL     # never allocated here
+    assert L.swiftkv_device_free(ctx.handle, None) == skv.OK
