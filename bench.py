@@ -460,6 +460,10 @@ def main():
         extra["batch1_position127_1layer"] = summary(r, graph=False)
         r = run_gpu(skv, ctx, [2047], 32, 20, args.warmup, seed=2029)
         extra["batch1_position2047_32layers"] = summary(r)
+        # One layer repeated: its 37.8 MB stay resident in the 256 MB MALL, so
+        # this is the cache-resident figure, reported apart from the sweep.
+        r = run_gpu(skv, ctx, [4095], 1, 200, args.warmup, seed=2033, graph=False)
+        extra["batch1_position4095_1layer_repeated_mall_resident"] = summary(r, graph=False)
         rng = np.random.default_rng(4)
         lengths = rng.integers(256, 4097, 64)
         r = run_gpu(skv, ctx, lengths - 1, 32, args.steps, args.warmup, seed=2030)
