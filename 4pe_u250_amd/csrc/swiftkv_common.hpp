@@ -26,6 +26,10 @@ constexpr int kSeqAlign = 64;                    // capacity granularity (tokens
 // Split-context work: a workgroup of kAttendWaves wavefronts scans a range of
 // split_tokens tokens; each wave takes 64-token blocks round-robin.
 constexpr int kAttendWaves = 4;
+// Launches that fit one residency round of 8-wave workgroups (one per CU)
+// with splits of a multiple of 512 tokens use 8 waves: each wave then holds
+// fewer blocks and two waves share a SIMD to overlap the math.
+constexpr int kWideWaves = 8;
 constexpr int kBlockTokens = 64;
 constexpr int kSplitQuantum = kAttendWaves * kBlockTokens;   // 256
 constexpr int kPartialStride = 4 + kHeadDim;     // (m, l, pad, pad, acc[128]) floats
@@ -106,7 +110,9 @@ struct BulkArgs {
 };
 
 // Launchers (swiftkv_kernels.hip).
-hipError_t launch_step(const StepArgs& a, int grid_splits, InputFormat in, hipStream_t s);
+// waves: kAttendWaves, or kWideWaves when a.split_tokens is a multiple of
+// kWideWaves * kBlockTokens.
+hipError_t launch_step(const StepArgs& a, int grid_splits, int waves, InputFormat in, hipStream_t s);
 hipError_t launch_append_bulk(const BulkArgs& a, bool q17, hipStream_t s);
 // Integer-compatibility step (one workgroup per (sequence, head)); a.out is
 // int32 Q15.17; exp_lut holds the 33 Q30 exp2 entries.

@@ -286,8 +286,8 @@ __device__ __forceinline__ float merge_partials(const float* part, int n) {
 // ---------------------------------------------------------------- step
 
 // Grid (splits, 32 heads, batch), 256 threads; grid row z serves rows[z].
-template <int IN>
-__global__ __launch_bounds__(kAttendWaves * 64) void step_kernel(StepArgs a) {
+template <int IN, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void step_kernel(StepArgs a) {
     const uint32_t row = a.rows[blockIdx.z];
     const int split = blockIdx.x, h = blockIdx.y, b = static_cast<int>(row & 0xffu);
     const int pos = static_cast<int>(row >> 8);
@@ -307,8 +307,8 @@ __global__ __launch_bounds__(kAttendWaves * 64) void step_kernel(StepArgs a) {
     int8_t* page = page_ptr(a.kv, a.slot0 + b, a.layer, h);
     const int64_t cap = a.kv.seq_cap;
 
-    __shared__ float s_acc[kAttendWaves + 1][kHeadDim];
-    __shared__ float s_m[kAttendWaves + 1], s_l[kAttendWaves + 1];
+    __shared__ float s_acc[WAVES + 1][kHeadDim];
+    __shared__ float s_m[WAVES + 1], s_l[WAVES + 1];
 
     // Loads go out before any math, in the order they are needed: this
     // lane's channel pair (2*lane, 2*lane+1) of the new row's q, k, v and its
@@ -350,7 +350,7 @@ __global__ __launch_bounds__(kAttendWaves * 64) void step_kernel(StepArgs a) {
     rope_pair(ki.x, ki.y, row_cs, k0, k1);
 
     float m_run, l_run, acc[16];
-    scan_range(pr, bl, qf, t_first, t_stop, kAttendWaves * kBlockTokens, r, m_run, l_run, acc);
+    scan_range(pr, bl, qf, t_first, t_stop, WAVES * kBlockTokens, r, m_run, l_run, acc);
 
     // The new row: quantize, append; forward (k^ . q', v^) into the merge as
     // one more partial.
@@ -360,11 +360,11 @@ __global__ __launch_bounds__(kAttendWaves * 64) void step_kernel(StepArgs a) {
         float sp = qs0 * kh0 + qs1 * kh1;
 #pragma unroll
         for (int s = 1; s < 64; s <<= 1) sp += __shfl_xor(sp, s);
-        s_acc[kAttendWaves][2 * lane] = vh0;
-        s_acc[kAttendWaves][2 * lane + 1] = vh1;
+        s_acc[WAVES][2 * lane] = vh0;
+        s_acc[WAVES][2 * lane + 1] = vh1;
         if (lane == 0) {
-            s_m[kAttendWaves] = sp;
-            s_l[kAttendWaves] = 1.0f;
+            s_m[WAVES] = sp;
+            s_l[WAVES] = 1.0f;
         }
     }
     if (r == 0) {
@@ -377,7 +377,7 @@ __global__ __launch_bounds__(kAttendWaves * 64) void step_kernel(StepArgs a) {
     }
     __syncthreads();
 
-    const int nparts = owner ? kAttendWaves + 1 : kAttendWaves;
+    const int nparts = owner ? WAVES + 1 : WAVES;
     const int d = threadIdx.x;
     float o = 0.0f, l = 0.0f, mx = -INFINITY;
     if (d < kHeadDim) {
@@ -458,16 +458,25 @@ __global__ __launch_bounds__(256) void convert_kernel(const float* __restrict__ 
 
 // ---------------------------------------------------------------- launchers
 
-hipError_t launch_step(const StepArgs& a, int grid_splits, InputFormat in, hipStream_t s) {
-    const dim3 grid(grid_splits, kHeads, a.batch), block(kAttendWaves * 64);
+template <int WAVES>
+hipError_t launch_step_waves(const StepArgs& a, dim3 grid, InputFormat in, hipStream_t s) {
+    const dim3 block(WAVES * 64);
     switch (in) {
-    case kInF32: step_kernel<kInF32><<<grid, block, 0, s>>>(a); break;
-    case kInQ17: step_kernel<kInQ17><<<grid, block, 0, s>>>(a); break;
-    case kInParts2: step_kernel<kInParts2><<<grid, block, 0, s>>>(a); break;
-    case kInParts4: step_kernel<kInParts4><<<grid, block, 0, s>>>(a); break;
+    case kInF32: step_kernel<kInF32, WAVES><<<grid, block, 0, s>>>(a); break;
+    case kInQ17: step_kernel<kInQ17, WAVES><<<grid, block, 0, s>>>(a); break;
+    case kInParts2: step_kernel<kInParts2, WAVES><<<grid, block, 0, s>>>(a); break;
+    case kInParts4: step_kernel<kInParts4, WAVES><<<grid, block, 0, s>>>(a); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
+}
+
+hipError_t launch_step(const StepArgs& a, int grid_splits, int waves, InputFormat in, hipStream_t s) {
+    const dim3 grid(grid_splits, kHeads, a.batch);
+    if (waves == kAttendWaves) return launch_step_waves<kAttendWaves>(a, grid, in, s);
+    if (waves == kWideWaves && a.split_tokens % (kWideWaves * kBlockTokens) == 0)
+        return launch_step_waves<kWideWaves>(a, grid, in, s);
+    return hipErrorInvalidValue;
 }
 
 hipError_t launch_append_bulk(const BulkArgs& a, bool q17, hipStream_t s) {
