@@ -72,6 +72,7 @@ struct ProfilePair {
 struct swiftkv_context {
     int device = 0;
     int cus = 256;              // compute units of the device
+    int step_per_cu = 3;        // 4-wave step workgroups one CU holds at once
     hipStream_t stream = nullptr;
     int32_t split_tokens = 0;   // 0: heuristic
     // split-context workspace
@@ -214,23 +215,38 @@ int upload_lut(swiftkv_context* ctx, std::vector<int2>&& host, int32_t positions
     return ok();
 }
 
-// Tokens per split.  Aim for about 2048 workgroups (a few residency rounds on
-// 256 CUs): split a head only when batch x 32 heads is below that, and never
-// below one 256-token quantum.  A head held by one split skips the partial
-// exchange, which is worth more than the finer tail of smaller splits (batch
-// 64 at context 4096: one split per head ran 369 us/layer, 2048-token splits
-// 377 and 1024-token splits 395 us/layer).  At most kMaxSplitsPerHead splits:
-// at batch 1 the merge's latency grows with the split count faster than the
-// shorter scans save (context 4096: 8 splits 14.5 us, 16 splits 15.7 us).
+// Tokens per split.  A launch runs best when it fills one residency round:
+// one 8-wave workgroup per CU (step_waves picks 8 waves for such launches),
+// or step_per_cu 4-wave workgroups per CU.  So
+//   batch x 32 heads <= CUs:  splits = CUs / heads (at most 8);
+//   otherwise:                splits = step_per_cu x CUs / heads (at least 1),
+// rounded to whole 256-token quanta.  Measured at context 4096 on 256 CUs
+// (3 workgroups per CU), us/layer with this rule against other splits:
+//   batch 1: 8 splits (12.0); batch 2: 4 (18.1; 19.2 with 8);
+//   batch 3 and 4: 2 (23.3 and 29.0; 24.4 and 32.8 with 8);
+//   batch 5 to 8: none (35.2 to 52.0; 38.2 to 55.0 with more);
+//   batch 12: 2 (76.9; 81.2 with none); batch 16 and 32: none (98.4 and
+//   189.8; 101.2 and 192.1 with 4 and 2); batch 64: none (361; 377 with 2);
+//   batch 16 at context 32K: none (715.5; 722.9 with 4).
+// No split is longer than kMaxSplitTokensHeuristic: on long contexts a
+// split's exchange is small against its scan and finer work balances better
+// (batch 16 decoding from position 32256: 698 us/step with 8192-token splits
+// against 703-705 with none).  At most kMaxSplitsPerHead splits: at batch 1
+// the merge's latency grows with the split count faster than the shorter
+// scans save (16 splits: 15.7 us against 14.5 with 8, at 4 waves per
+// workgroup).
 constexpr int64_t kMaxSplitsPerHead = 8;
+constexpr int64_t kMaxSplitTokensHeuristic = 8192;
 
 int32_t choose_split(const swiftkv_context* ctx, const int32_t* positions, int32_t batch) {
     if (ctx->split_tokens > 0) return ctx->split_tokens;
     int32_t max_len = 1;
     for (int32_t b = 0; b < batch; ++b) max_len = std::max(max_len, positions[b] + 1);
     const int64_t heads = static_cast<int64_t>(batch) * kHeads;
+    const int64_t slots = heads <= ctx->cus ? ctx->cus : static_cast<int64_t>(ctx->cus) * ctx->step_per_cu;
+    const int64_t by_length = (max_len + kMaxSplitTokensHeuristic - 1) / kMaxSplitTokensHeuristic;
     const int64_t splits_per_head =
-        std::min<int64_t>(kMaxSplitsPerHead, std::max<int64_t>(1, (2048 + heads - 1) / heads));
+        std::min<int64_t>(kMaxSplitsPerHead, std::max<int64_t>({int64_t(1), slots / heads, by_length}));
     const int64_t tokens = (max_len + splits_per_head - 1) / splits_per_head;
     const int64_t quanta = std::max<int64_t>(1, (tokens + kSplitQuantum - 1) / kSplitQuantum);
     return static_cast<int32_t>(std::min<int64_t>(quanta * kSplitQuantum, kMaxSeq));
@@ -513,6 +529,7 @@ int swiftkv_context_create(int device, swiftkv_context** out) {
     if (!ctx) return fail(SWIFTKV_ENOMEM, "out of host memory");
     ctx->device = device;
     hipError_t e = hipDeviceGetAttribute(&ctx->cus, hipDeviceAttributeMultiprocessorCount, device);
+    if (e == hipSuccess) ctx->step_per_cu = std::max(1, step_workgroups_per_cu());
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
     for (int i = 0; e == hipSuccess && i < kTimerSlots; ++i) e = hipEventCreate(&ctx->timers[i]);
     const size_t counter_bytes = sizeof(uint32_t) * kMaxBatchPerLaunch * kHeads * kCounterStride;

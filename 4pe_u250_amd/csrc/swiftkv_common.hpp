@@ -113,6 +113,8 @@ struct BulkArgs {
 // waves: kAttendWaves, or kWideWaves when a.split_tokens is a multiple of
 // kWideWaves * kBlockTokens.
 hipError_t launch_step(const StepArgs& a, int grid_splits, int waves, InputFormat in, hipStream_t s);
+// Workgroups of the 4-wave step kernel one CU holds at once (0 on error).
+int step_workgroups_per_cu();
 hipError_t launch_append_bulk(const BulkArgs& a, bool q17, hipStream_t s);
 // Integer-compatibility step (one workgroup per (sequence, head)); a.out is
 // int32 Q15.17; exp_lut holds the 33 Q30 exp2 entries.

@@ -471,6 +471,14 @@ hipError_t launch_step_waves(const StepArgs& a, dim3 grid, InputFormat in, hipSt
     return hipGetLastError();
 }
 
+int step_workgroups_per_cu() {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, step_kernel<kInF32, kAttendWaves>, kAttendWaves * 64, 0) !=
+        hipSuccess)
+        return 0;
+    return n;
+}
+
 hipError_t launch_step(const StepArgs& a, int grid_splits, int waves, InputFormat in, hipStream_t s) {
     const dim3 grid(grid_splits, kHeads, a.batch);
     if (waves == kAttendWaves) return launch_step_waves<kAttendWaves>(a, grid, in, s);
