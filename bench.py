@@ -25,7 +25,8 @@ drawn from U{256..4096} (32 layers), batch 16 decoding 512 steps from
 position 32256 to 32767 on Student-t(3) data (one layer), and the batch-64
 call with host-memory inputs and outputs (PCIe included; never `value`).
 The batch-64 and batch-1 workloads are also timed through the entry that
-takes the Q/K/V projection's split-K FP32 partials (--parts, default 4).
+takes the Q/K/V projection's split-K FP32 partials (--parts, default 4), and
+the batch sizes between them (2 to 32) at position 4095 over 32 layers.
 On the host: the reference emulator's attention stage at position 4095 (one
 thread as shipped, and with its OpenMP pragmas), the FP32 tolerance oracle
 (reported apart from the reference), and the reference's attention loop at
@@ -469,12 +470,20 @@ def main():
         r = run_gpu(skv, ctx, lengths - 1, 32, args.steps, args.warmup, seed=2030)
         extra["batch64_ragged_32layers"] = dict(summary(r), length_seed=4, sum_attended=r["sum_attended"],
                                                 lengths="U{256..4096}")
+        sweep = {}
+        for b in (2, 4, 8, 16, 32):   # the batch sizes between the two headline ones, 32 layers at context 4096
+            r = run_gpu(skv, ctx, np.full(b, args.context - 1), 32, 5, 1, seed=2040 + b, graph=False)
+            sweep[str(b)] = {"us_per_layer": round(r["us_per_layer"], 2), "gbps": round(r["gbps"], 1),
+                             "pct_of_peak": round(r["pct_of_peak"], 2)}
+        extra["batch_sweep_position4095_32layers"] = sweep
+        log("[bench] batch sweep: " + ", ".join(f"{b}: {v['us_per_layer']:.1f} us" for b, v in sweep.items()))
         r = run_gpu(skv, ctx, np.full(16, 32256), 1, 512, 0, seed=2031, dist=skv.DIST_STUDENT_T3, graph=False,
                     advance=True)
         extra["batch16_positions32256to32767_1layer_t3"] = dict(summary(r, graph=False),
                                                                  steps=512, ms_total=round(r["ms_per_step"] * 512, 2))
         for k, v in extra.items():
-            log(f"[bench] {k}: {v['us_per_layer']:.2f} us/layer, {v['gbps']:.0f} GB/s")
+            if "us_per_layer" in v:
+                log(f"[bench] {k}: {v['us_per_layer']:.2f} us/layer, {v['gbps']:.0f} GB/s")
         extra["batch64_position4095_host_io"] = run_host_io(skv, ctx, args.batch, args.context, 20, seed=2032)
         log(f"[bench] host-memory I/O, batch {args.batch}: "
             f"{extra['batch64_position4095_host_io']['us_per_layer']:.1f} us/layer")
