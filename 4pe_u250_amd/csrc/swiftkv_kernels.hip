@@ -2,7 +2,8 @@
 // stage.
 //
 // step kernel (one launch per decode step and layer), grid (splits, 32 heads,
-// batch rows) of 256-thread workgroups; workgroup (j, h, z) owns tokens
+// batch rows) of 4-wave workgroups (8 waves when the launch has at most one
+// workgroup per CU and 512-token-multiple splits); workgroup (j, h, z) owns tokens
 // [j*C, min((j+1)*C, position+1)) of head h of the sequence that row z names
 // (rows come longest first, so a ragged batch does not end on long heads):
 //   1. every lane loads its channel pair of the new row's q/k/v (Q15.17,
@@ -14,7 +15,7 @@
 //      G32-quantizes the new K/V row, appends it to the cache, and forwards it
 //      into its own merge as one more partial -- the new token is written once
 //      and never read back (the reference does the same, hpp:37-41);
-//   3. four waves scan the cached tokens in 64-token blocks.  Lane = (chunk
+//   3. the waves scan the cached tokens in 64-token blocks.  Lane = (chunk
 //      c = lane&7, row r = lane>>3): one nontemporal dwordx4 per lane reads a
 //      16-channel chunk, so one wave instruction covers 8 full 128-B code
 //      rows.  Codes are dequantized in VGPRs, partial dots reduced over the 8
