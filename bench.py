@@ -229,6 +229,36 @@ def run_gpu(skv, ctx, positions, layers, steps, warmup, seed, outliers=False, di
     return res
 
 
+def run_prefill(skv, ctx, tokens, layers, reps, seed):
+    """swiftkv_append_tokens: the append rule (conversion, RoPE of k at its own
+    position, G32 quantization) over a `tokens`-long prompt of one sequence,
+    every layer; bytes = FP32 k and v read plus the 288-B rows written."""
+    lut = skv.RopeLut.generate(ctx, max(tokens, 4096))
+    kv = skv.KVCache(ctx, layers=layers, max_batch=1, max_seq_len=tokens)
+    n = tokens * 4096
+    k, v = ctx.alloc(n * 4), ctx.alloc(n * 4)
+    ctx.fill_synthetic(k, n, seed, 1)
+    ctx.fill_synthetic(v, n, seed, 2)
+    for layer in range(layers):           # warm-up pass
+        skv.swiftkv_append_tokens(ctx, k, v, kv, lut, layer, 0, 0, tokens)
+    ctx.synchronize()
+    ctx.timer_record(8)
+    for _ in range(reps):
+        for layer in range(layers):
+            skv.swiftkv_append_tokens(ctx, k, v, kv, lut, layer, 0, 0, tokens)
+    ctx.timer_record(9)
+    ms = ctx.timer_elapsed_ms(8, 9)
+    for b in (k, v):
+        b.free()
+    kv.close()
+    lut.close()
+    per_layer_s = ms / 1e3 / reps / layers
+    bytes_per_layer = tokens * 32 * (2 * 128 * 4 + TOKEN_HEAD_BYTES)
+    return {"us_per_layer": round(per_layer_s * 1e6, 2), "gbps": round(bytes_per_layer / per_layer_s / 1e9, 1),
+            "tokens_per_s": round(tokens / per_layer_s / layers, 1),
+            "sample": f"{reps} prompts of {tokens} tokens x {layers} layers, one sequence"}
+
+
 def run_host_io(skv, ctx, batch, context, reps, seed):
     """The per-layer call with host-memory q/k/v/out/A14 (pageable numpy
     arrays): copies in, step, copies out, wait -- the PCIe-inclusive rate."""
@@ -450,7 +480,7 @@ def main():
     if not args.no_batch1:
         # batch-1 headline: 1% of K channels x20
         b1 = run_gpu(skv, ctx, [args.context - 1], args.layers, max(args.steps, 20), args.warmup, seed=2027,
-                     outliers=True, parts=args.parts)
+                     outliers=True, parts=args.parts, exact_steps=min(args.exact_steps, 1) * 5)
         log(f"[bench] batch 1: {b1['us_per_layer']:.2f} us/layer, {b1['gbps']:.0f} GB/s "
             f"(graph replay {b1['graph']['us_per_layer']:.2f} us/layer)")
         if b1["partials"]:
@@ -485,6 +515,9 @@ def main():
             if "us_per_layer" in v:
                 log(f"[bench] {k}: {v['us_per_layer']:.2f} us/layer, {v['gbps']:.0f} GB/s")
         extra["batch64_position4095_host_io"] = run_host_io(skv, ctx, args.batch, args.context, 20, seed=2032)
+        extra["prefill_append_4096tokens_32layers"] = run_prefill(skv, ctx, 4096, 32, 5, seed=2034)
+        log(f"[bench] prefill append, 4096 tokens: {extra['prefill_append_4096tokens_32layers']['us_per_layer']:.1f} "
+            f"us/layer, {extra['prefill_append_4096tokens_32layers']['gbps']:.0f} GB/s")
         log(f"[bench] host-memory I/O, batch {args.batch}: "
             f"{extra['batch64_position4095_host_io']['us_per_layer']:.1f} us/layer")
     ctx.close()
@@ -555,6 +588,10 @@ def main():
             "note": "same workload through swiftkv_attention_partials; bytes count the parts x FP32 q/k/v rows"}
     if b1:
         line["batch1"] = dict(summary(b1), workload="32 layers x batch 1 x position 4095, 1% of K channels x20")
+        if b1["exact"]:
+            line["batch1"]["integer_exact_path"] = {"us_per_layer": round(b1["exact"]["us_per_layer"], 1),
+                                                    "max_abs_diff_vs_fp32_path":
+                                                        b1["exact"]["max_abs_diff_vs_fp32_path"]}
         if b1["partials"]:
             line["batch1"]["split_k_partials_input"] = {"parts": b1["partials"]["parts"],
                                                         "us_per_layer": round(b1["partials"]["us_per_layer"], 3),
