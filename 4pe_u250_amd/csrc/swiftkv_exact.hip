@@ -8,14 +8,18 @@
 // Grid (32 heads, batch rows), 256 threads per (sequence, head).  Wave 0
 // first appends the new row like the fast step; then tokens [0, position]
 // are processed in chunks of kChunk:
-//   - the 4 waves compute the chunk's integer scores (lane = 16-channel
-//     half-group c of token row r; the per-half shift and the 44-bit wraps are
-//     associative modulo 2^44, so the octet sum may run in any order) and
-//     stage its V codes in LDS;
+//   - the 4 waves issue all of the chunk's loads at once (K codes and scales
+//     into registers, V codes straight into LDS), then compute the integer
+//     scores (lane = 16-channel half-group c of token row r; the per-half
+//     shift and the 44-bit wraps are associative modulo 2^44, so the octet
+//     sum may run in any order), the exact 64-bit dot taken as signed-byte
+//     dot products over five limbs of the query;
 //   - one thread per token turns its score and the exclusive prefix maximum
-//     into a coefficient word (exp LUT, rescale flag);
-//   - threads 0..127 run Y, one channel each, and wave 2 runs Z, both in
-//     token order;
+//     into a coefficient word (exp LUT, rescale flag), and the same pass lays
+//     out prefix sums and ballots for Z and Y;
+//   - threads 0..127 run Y, one channel each, in token order, adding
+//     independently formed terms; wave 2 advances Z by prefix-sum
+//     differences and steps only at first and rescaling tokens;
 // then Y * 1/Z and the integer-path A14/E8M0 epilogue.
 #include "swiftkv_device.hpp"
 
@@ -27,6 +31,8 @@ using namespace dev;
 constexpr int kChunk = 256;                   // cached tokens per chunk (V codes staged in LDS)
 constexpr int kBatch = 8;                     // tokens whose LDS reads go out together in the Y and Z passes
 static_assert(kChunk % kBatch == 0, "batches tile a chunk");
+static_assert(kBatch == 8, "the Y pass reads a batch's coefficients as two 16-byte LDS loads");
+constexpr int kPasses = kChunk / 32;          // score passes per chunk: 4 waves x 8 token rows each
 constexpr int64_t kScoreScaleQ17 = 11585;     // RNE(2^17 / sqrt(128)) (swiftkv_attention.cpp:1101-1102)
 constexpr int64_t kLog2eQ21 = 3025551;        // RNE(log2(e) * 2^21) (cpp:207-208)
 
@@ -70,16 +76,50 @@ __device__ __forceinline__ uint32_t exp_neg_q17(int32_t x, const uint32_t* lut) 
     return static_cast<uint32_t>(out) & 0x3ffffu;
 }
 
+// The 16 rotated query channels of one half-group as five planes of signed
+// bytes, four channels per word: q = l0 + l1 2^8 + l2 2^16 + l3 2^24 + l4 2^32,
+// each limb the signed low byte of what the limbs below it leave, so every
+// limb lies in [-128, 127] and the top one in {-1, 0, 1} for any int32 q.
+struct QueryLimbs {
+    int32_t w[5][4];
+};
+
+__device__ __forceinline__ QueryLimbs split_query(const int32_t* q) {
+    QueryLimbs L;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        uint32_t packed[5] = {0u, 0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int byte = 0; byte < 4; ++byte) {
+            int64_t rest = q[4 * j + byte];
+#pragma unroll
+            for (int k = 0; k < 5; ++k) {
+                const int32_t limb = static_cast<int8_t>(static_cast<uint8_t>(rest));
+                packed[k] |= static_cast<uint32_t>(static_cast<uint8_t>(limb)) << (8 * byte);
+                rest = (rest - limb) >> 8;
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 5; ++k) L.w[k][j] = static_cast<int32_t>(packed[k]);
+    }
+    return L;
+}
+
 // 44-bit token dot contribution of one 16-channel half-group: the 16 int8
 // codes times the int32 rotated query, scaled by 2^(shift-10) (cpp:934-995).
-__device__ __forceinline__ int64_t half_dot(const int32_t* q, int4 w, uint32_t shift) {
+// The exact sum is taken limb by limb: four signed-byte dot products per limb
+// (each limb's sum stays within 16 * 128 * 128 = 2^18), then combined in 64
+// bits, so it equals the sum of the 16 full products.
+__device__ __forceinline__ int64_t half_dot(const QueryLimbs& L, int4 w, uint32_t shift) {
     const int32_t d[4] = {w.x, w.y, w.z, w.w};
     int64_t s = 0;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int k = 4; k >= 0; --k) {
+        int32_t acc = 0;
 #pragma unroll
-        for (int byte = 0; byte < 4; ++byte)
-            s += static_cast<int64_t>(q[4 * j + byte]) * static_cast<int8_t>(d[j] >> (8 * byte));
+        for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_sdot4(L.w[k][j], d[j], acc, false);
+        s = s * 256 + acc;
+    }
     const int64_t p = shift >= 10 ? static_cast<int64_t>(static_cast<uint64_t>(s) << (shift - 10))
                                   : (s >> (10 - shift));
     return wrap_bits(p, 44);
@@ -119,18 +159,38 @@ __device__ __forceinline__ uint32_t z_step(uint32_t z, uint32_t word) {
     return (z + coef) & kMask30;
 }
 
-// One token of Y for one channel: no rescale  Y = sat32(Y + wrap32(RNE(v c >> 17))),
-// rescale  Y = sat32(wrap32(RNE(Y c >> 17)) + v); one multiply either way.
-__device__ __forceinline__ int32_t value_step(int32_t y, uint32_t word, int32_t val) {
-    if (word & kInit) return val;
-    const bool rescale = (word & kRescale) != 0u;
-    const int32_t m = mulq17_wrap(rescale ? y : val, word & kCoefMask);
-    return __builtin_elementwise_add_sat(rescale ? val : y, m);
+// Y per token and channel (cpp:1463-1558):
+//   first token  Y = v
+//   no rescale   Y = sat32(Y + wrap32(RNE(v c >> 17)))
+//   rescale      Y = sat32(wrap32(RNE(Y c >> 17)) + v)
+// with v = code << shift as the reference's ap_int<32> (it wraps for code 64,
+// shift 25).  The no-rescale term does not depend on Y, so the terms of a
+// batch of tokens are formed independently and only the saturating adds run
+// in series.  The term in 32-bit operations, c < 2^18 and |code| <= 128:
+//   shift >= 17: v is a multiple of 2^17, so the quotient is exact and equals
+//                (v >> 17) c, with |v >> 17| <= 2^14 -- the low 32 bits of a
+//                24-bit product are the wrap;
+//   shift < 17:  v c = (code c) 2^shift exactly, |code c| < 2^25, so the term
+//                is RNE((code c) / 2^k) for k = 17 - shift in 1..17, in the
+//                floor((x + 2^(k-1) - 1 + bit k of x) >> k) form of rne_shift.
+__device__ __forceinline__ int32_t dequant_raw(int32_t code, uint32_t shift) {
+    return static_cast<int32_t>(static_cast<uint32_t>(code) << shift);
 }
 
-// code << shift as the reference's ap_int<32> (wraps for code 64, shift 25).
-__device__ __forceinline__ int32_t dequant_raw(uint32_t code_byte, uint32_t shift) {
-    return static_cast<int32_t>(static_cast<uint32_t>(static_cast<int32_t>(static_cast<int8_t>(code_byte))) << shift);
+__device__ __forceinline__ int32_t value_term(int32_t code, uint32_t shift, uint32_t coef) {
+    const int32_t c = static_cast<int32_t>(coef);
+    const int32_t exact = __mul24(dequant_raw(code, shift) >> 17, c);
+    const int32_t m = __mul24(code, c);
+    const uint32_t k = (17u - shift) & 31u;
+    const int32_t bit = static_cast<int32_t>(__builtin_amdgcn_ubfe(static_cast<uint32_t>(m), 17u - shift, 1u));
+    const int32_t rounded = (m + static_cast<int32_t>(0xffffu >> shift) + bit) >> k;
+    return shift >= 17u ? exact : rounded;
+}
+
+__device__ __forceinline__ int32_t value_step(int32_t y, uint32_t word, int32_t code, uint32_t shift, int32_t term) {
+    if (word & kInit) return dequant_raw(code, shift);
+    if (word & kRescale) return __builtin_elementwise_add_sat(mulq17_wrap(y, word & kCoefMask), dequant_raw(code, shift));
+    return __builtin_elementwise_add_sat(y, term);
 }
 
 struct ExactArgs {
@@ -155,9 +215,13 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
     __shared__ int32_t s_q[kHeadDim];
     __shared__ int32_t s_score[kChunk];
     __shared__ uint32_t s_word[kChunk];                  // coefficient words of the chunk
+    __shared__ __align__(16) uint32_t s_coef[kChunk];    // the coefficients alone, zero past n
+    __shared__ uint32_t s_psum[kChunk];                  // per-wave inclusive sums of ordinary coefficients
     __shared__ int8_t s_vc[kChunk][kHeadDim];            // V codes of the chunk
-    __shared__ uint8_t s_vs[kChunk][kGroupsPerHead];     // V shifts of the chunk
+    __shared__ __align__(16) uint8_t s_vs[kGroupsPerHead][kChunk];   // V shifts of the chunk, by group
     __shared__ int32_t s_wave_max[kChunk / 64];
+    __shared__ uint32_t s_wave_sum[kChunk / 64];
+    __shared__ uint64_t s_special[kChunk / 64];          // per-wave ballots of first and rescaling tokens
     __shared__ uint32_t s_lut[33];
     __shared__ uint32_t s_inv;
     __shared__ int16_t s_q14[kHeadDim];
@@ -180,9 +244,13 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
         s_q[2 * lane + 1] = q1;
     }
     __syncthreads();
-    int32_t qc[16];
+    QueryLimbs ql;
+    {
+        int32_t qc[16];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) qc[j] = s_q[16 * c + j];
+        for (int j = 0; j < 16; ++j) qc[j] = s_q[16 * c + j];
+        ql = split_query(qc);
+    }
 
     const int len = pos + 1;
     int32_t run_max = INT32_MIN;   // prefix maximum before the chunk (every thread)
@@ -190,29 +258,45 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
     int32_t y = 0;                 // Y of channel d (threads d < 128)
     for (int t0 = 0; t0 < len; t0 += kChunk) {
         const int n = min(kChunk, len - t0);
-        // Scores of tokens [t0, t0+n), 4 waves x 8 token rows per pass; the
-        // same passes stage the chunk's V codes and shifts in LDS.
-        for (int i = wave * 8 + r; i < kChunk; i += 32) {
-            const int64_t t = t0 + i;
-            int64_t p = 0;
-            if (i < n) {
-                const float2 sc = *reinterpret_cast<const float2*>(scales + t * 8 + (c >> 1) * 2);
-                p = half_dot(qc, *reinterpret_cast<const int4*>(page + t * kCodeBytes + c * 16), shift_of(sc.x));
-                reinterpret_cast<int4*>(&s_vc[i][0])[c] =
-                    *reinterpret_cast<const int4*>(page + cap * kCodeBytes + t * kCodeBytes + c * 16);
-                if ((c & 1) == 0) s_vs[i][c >> 1] = static_cast<uint8_t>(shift_of(sc.y));
-            }
+        // Scores of tokens [t0, t0+n), 4 waves x 8 token rows per pass.  All
+        // passes' loads go out first: per lane the K codes and scale pair
+        // into registers, and the V codes straight into LDS (lane l of a wave
+        // writes bytes [16 l, 16 l + 16) of its 8 rows, which is channel
+        // chunk c of row r).  Rows past n load the chunk's last token (inside
+        // the page) and are not used.
+        int4 kq[kPasses];
+        float2 scl[kPasses];
+#pragma unroll
+        for (int ps = 0; ps < kPasses; ++ps) {
+            const int64_t t = t0 + min(wave * 8 + r + 32 * ps, n - 1);
+            scl[ps] = *reinterpret_cast<const float2*>(scales + t * 8 + (c >> 1) * 2);
+            kq[ps] = *reinterpret_cast<const int4*>(page + t * kCodeBytes + c * 16);
+            __builtin_amdgcn_global_load_lds(page + (cap + t) * kCodeBytes + c * 16,
+                                             (__attribute__((address_space(3))) void*)&s_vc[wave * 8 + 32 * ps][0],
+                                             16, 0, 0);
+        }
+#pragma unroll
+        for (int ps = 0; ps < kPasses; ++ps) {
+            const int i = wave * 8 + r + 32 * ps;
+            int64_t p = half_dot(ql, kq[ps], shift_of(scl[ps].x));
+            // slots past n are read by the Y pass with a zero coefficient
+            if ((c & 1) == 0) s_vs[c >> 1][i] = i < n ? static_cast<uint8_t>(shift_of(scl[ps].y)) : 0;
             // sum of the token's 8 half-groups (lanes 8r .. 8r+7), modulo 2^44
             p += __shfl_xor(p, 1);
             p += __shfl_xor(p, 2);
             p += __shfl_xor(p, 4);
             if (c == 0 && i < n) s_score[i] = score_of(p);
         }
+        __builtin_amdgcn_s_waitcnt(0);   // the V codes are in LDS before the barrier
         __syncthreads();
 
         // Coefficient words, one token per thread: the exclusive prefix
         // maximum (wave scan, then the maxima of the waves before) gives each
-        // token's running maximum.
+        // token's running maximum.  The same pass lays out what Y and Z read:
+        // the coefficients alone, the per-wave inclusive sums of the
+        // coefficients of ordinary tokens (first and rescaling tokens count
+        // zero) with the wave totals, and per-wave ballots of the first and
+        // rescaling tokens.
         const int32_t sv = d < n ? s_score[d] : INT32_MIN;
         int32_t incl = sv;
 #pragma unroll
@@ -226,38 +310,86 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
         int32_t before = run_max;
         for (int w = 0; w < wave; ++w) before = max(before, s_wave_max[w]);
         excl = lane == 0 ? before : max(before, excl);
-        if (d < n) s_word[d] = (t0 == 0 && d == 0) ? kInit : coef_word(sv, excl, s_lut);
+        const uint32_t word = d >= n ? 0u : (t0 == 0 && d == 0) ? kInit : coef_word(sv, excl, s_lut);
+        const bool special = (word & (kInit | kRescale)) != 0u;
+        uint32_t psum = special ? 0u : (word & kCoefMask);
+#pragma unroll
+        for (int k = 1; k < 64; k <<= 1) {
+            const uint32_t o = __shfl_up(psum, k);
+            if (lane >= k) psum += o;
+        }
+        const uint64_t special_mask = __ballot(special);
+        s_word[d] = word;
+        s_coef[d] = word & kCoefMask;
+        s_psum[d] = psum;
+        if (lane == 63) s_wave_sum[wave] = psum;
+        if (lane == 0) s_special[wave] = special_mask;
 #pragma unroll
         for (int w = 0; w < kChunk / 64; ++w) run_max = max(run_max, s_wave_max[w]);
         __syncthreads();
 
-        // Y (threads 0..127, one channel each) and Z (wave 2), in token order.
-        // The LDS reads of kBatch tokens go out before their updates, so one
-        // read latency covers the batch (indices stay below kChunk: kChunk is
-        // a multiple of kBatch; entries past n are read and not used).
+        // Y (threads 0..127, one channel each) in token order, kBatch tokens
+        // at a time: their LDS reads go out together, and a batch with no
+        // first or rescaling token (the common case; the ballots say which)
+        // only adds its terms.  Slots past n have a zero coefficient, which
+        // makes a zero term.  Indices stay below kChunk (a multiple of kBatch).
         if (d < kHeadDim) {
             const int g = d >> 5;
-            for (int i0 = 0; i0 < n; i0 += kBatch) {
-                uint32_t w[kBatch];
-                int32_t v[kBatch];
+            for (int span = 0; span < n; span += 64) {
+                const uint64_t sp = s_special[span >> 6];
+                const uint64_t spans = (static_cast<uint64_t>(static_cast<uint32_t>(
+                                            __builtin_amdgcn_readfirstlane(static_cast<int>(sp >> 32)))) << 32) |
+                                       static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(sp)));
+                const int end = min(span + 64, n);
+                for (int i0 = span; i0 < end; i0 += kBatch) {
+                    const uint4 ca = *reinterpret_cast<const uint4*>(&s_coef[i0]);
+                    const uint4 cb = *reinterpret_cast<const uint4*>(&s_coef[i0 + 4]);
+                    const uint2 sw = *reinterpret_cast<const uint2*>(&s_vs[g][i0]);
+                    const uint32_t coef[kBatch] = {ca.x, ca.y, ca.z, ca.w, cb.x, cb.y, cb.z, cb.w};
+                    uint32_t sh[kBatch];
+                    int32_t code[kBatch], term[kBatch];
 #pragma unroll
-                for (int j = 0; j < kBatch; ++j) {
-                    w[j] = s_word[i0 + j];
-                    v[j] = dequant_raw(static_cast<uint8_t>(s_vc[i0 + j][d]), s_vs[i0 + j][g]);
+                    for (int j = 0; j < kBatch; ++j) {
+                        code[j] = s_vc[i0 + j][d];
+                        sh[j] = ((j < 4 ? sw.x : sw.y) >> (8 * (j & 3))) & 0xffu;
+                    }
+#pragma unroll
+                    for (int j = 0; j < kBatch; ++j) term[j] = value_term(code[j], sh[j], coef[j]);
+                    if (((spans >> (i0 - span)) & 0xffu) == 0u) {
+#pragma unroll
+                        for (int j = 0; j < kBatch; ++j) y = __builtin_elementwise_add_sat(y, term[j]);
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < kBatch; ++j) {
+                            const uint32_t w = static_cast<uint32_t>(
+                                __builtin_amdgcn_readfirstlane(static_cast<int>(s_word[i0 + j])));
+                            y = value_step(y, w, code[j], sh[j], term[j]);
+                        }
+                    }
                 }
-#pragma unroll
-                for (int j = 0; j < kBatch; ++j)
-                    if (i0 + j < n) y = value_step(y, w[j], v[j]);
             }
         } else if (wave == 2) {
-            for (int i0 = 0; i0 < n; i0 += kBatch) {
-                uint32_t w[kBatch];
+            // Z: ordinary tokens add their coefficients modulo 2^30, so
+            // between two first or rescaling tokens Z advances by a difference
+            // of prefix sums, and only those tokens step in order.
+            uint32_t done = 0u, offset = 0u;   // prefix sum already added; sum of the waves before
 #pragma unroll
-                for (int j = 0; j < kBatch; ++j) w[j] = s_word[i0 + j];
-#pragma unroll
-                for (int j = 0; j < kBatch; ++j)
-                    if (i0 + j < n) z = z_step(z, __builtin_amdgcn_readfirstlane(w[j]));
+            for (int w = 0; w < kChunk / 64; ++w) {
+                const uint64_t sp = s_special[w];
+                uint64_t m = (static_cast<uint64_t>(static_cast<uint32_t>(
+                                  __builtin_amdgcn_readfirstlane(static_cast<int>(sp >> 32)))) << 32) |
+                             static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(sp)));
+                while (m != 0u) {
+                    const int i = w * 64 + __builtin_ctzll(m);
+                    const uint32_t upto = offset + s_psum[i];   // sum of the ordinary tokens before i
+                    z = (z + (upto - done)) & kMask30;
+                    done = upto;
+                    z = z_step(z, static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(s_word[i]))));
+                    m &= m - 1u;
+                }
+                offset += s_wave_sum[w];
             }
+            z = (z + (offset - done)) & kMask30;
         }
         __syncthreads();
     }

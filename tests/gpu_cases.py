@@ -15,6 +15,20 @@ def student_t3(seed: int, shape) -> np.ndarray:
     return (n / np.sqrt(c / 3.0) / np.sqrt(3.0)).astype(np.float32)
 
 
+def wide_values(seed: int, shape) -> np.ndarray:
+    """N(0,1) rows, each scaled by 2^e with e uniform in [-8, 15], and 2% of the entries set to +-20000 (past
+    the Q15.17 range, so they saturate): G32 shifts from small to 25, including the code 64 at shift 25 whose
+    dequantized value wraps."""
+    x = f32_normal(seed, shape).astype(np.float64)
+    rows, total = shape[0], int(np.prod(shape))
+    z = splitmix64(seed + 3, rows + total)
+    e = (z[:rows] % np.uint64(24)).astype(np.int64) - 8
+    x *= np.ldexp(1.0, e).reshape((rows,) + (1,) * (len(shape) - 1))
+    zz = z[rows:].reshape(shape)
+    sign = np.where((zz >> np.uint64(32)) & np.uint64(1), 1.0, -1.0)
+    return np.where(zz % np.uint64(50) == 0, 20000.0 * sign, x).astype(np.float32)
+
+
 def outlier_channels(seed: int, count: int = 41) -> np.ndarray:
     z = splitmix64(seed, 4 * count)
     return np.unique((z % np.uint64(4096)).astype(np.int64))[:count]
@@ -23,6 +37,8 @@ def outlier_channels(seed: int, count: int = 41) -> np.ndarray:
 def history(seed: int, n: int, dist: str = "normal", outliers=None):
     if dist == "t3":
         k, v = student_t3(seed, (n, 4096)), student_t3(seed + 1, (n, 4096))
+    elif dist == "wide":
+        k, v = f32_normal(seed, (n, 4096)), wide_values(seed + 1, (n, 4096))
     else:
         k, v = f32_normal(seed, (n, 4096)), f32_normal(seed + 1, (n, 4096))
     if outliers is not None:

@@ -98,6 +98,7 @@ def test_exact_matches_reference_decode(skv, ctx, lut4096, golden, case):
     ([0, 1, 255, 256], "normal", False),
     ([257, 511, 512, 1030], "t3", False),
     ([1500, 77], "t3", True),
+    ([300, 700], "wide", False),
 ])
 def test_exact_matches_oracle_integer_recurrence(skv, ctx, lut4096, rope_tables, positions, dist, q17):
     _note(f"case: exact vs oracle, positions {positions}, {dist}, q17={q17}")
