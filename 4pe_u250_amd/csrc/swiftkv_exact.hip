@@ -193,6 +193,32 @@ __device__ __forceinline__ int32_t value_step(int32_t y, uint32_t word, int32_t 
     return __builtin_elementwise_add_sat(y, term);
 }
 
+// A wave-uniform 64-bit value read by every lane, moved to scalar registers.
+__device__ __forceinline__ uint64_t uniform64(uint64_t v) {
+    return (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(v >> 32))))
+            << 32) |
+           static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(v)));
+}
+
+// The codes, shifts and Y terms of tokens [i0, i0 + kBatch) for channel ch:
+// two 16-byte reads give the coefficients, one 8-byte read the shifts (stored
+// by group), and one byte read per token the code.
+__device__ __forceinline__ void batch_terms(const uint32_t* s_coef, const uint8_t* s_vs_g,
+                                            const int8_t (*s_vc)[kHeadDim], int i0, int ch, int32_t* code,
+                                            uint32_t* sh, int32_t* term) {
+    const uint4 ca = *reinterpret_cast<const uint4*>(&s_coef[i0]);
+    const uint4 cb = *reinterpret_cast<const uint4*>(&s_coef[i0 + 4]);
+    const uint2 sw = *reinterpret_cast<const uint2*>(&s_vs_g[i0]);
+    const uint32_t coef[kBatch] = {ca.x, ca.y, ca.z, ca.w, cb.x, cb.y, cb.z, cb.w};
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+        code[j] = s_vc[i0 + j][ch];
+        sh[j] = ((j < 4 ? sw.x : sw.y) >> (8 * (j & 3))) & 0xffu;
+    }
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) term[j] = value_term(code[j], sh[j], coef[j]);
+}
+
 struct ExactArgs {
     StepArgs step;
     uint32_t exp_lut[33];     // RNE(2^(30 + i/32)), i = 0..32 (cpp:185-195)
@@ -213,15 +239,19 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
     const float* scales = reinterpret_cast<const float*>(page + cap * (2 * kCodeBytes));
 
     __shared__ int32_t s_q[kHeadDim];
-    __shared__ int32_t s_score[kChunk];
+    // Per token of the chunk: the score, then (each thread rewrites its own
+    // token after reading it) the coefficient alone, zero past n.
+    __shared__ __align__(16) uint32_t s_tok[kChunk];
     __shared__ uint32_t s_word[kChunk];                  // coefficient words of the chunk
-    __shared__ __align__(16) uint32_t s_coef[kChunk];    // the coefficients alone, zero past n
     __shared__ uint32_t s_psum[kChunk];                  // per-wave inclusive sums of ordinary coefficients
     __shared__ int8_t s_vc[kChunk][kHeadDim];            // V codes of the chunk
     __shared__ __align__(16) uint8_t s_vs[kGroupsPerHead][kChunk];   // V shifts of the chunk, by group
     __shared__ int32_t s_wave_max[kChunk / 64];
     __shared__ uint32_t s_wave_sum[kChunk / 64];
     __shared__ uint64_t s_special[kChunk / 64];          // per-wave ballots of first and rescaling tokens
+    __shared__ int64_t s_map_sum[kHeadDim];              // the composed map of tokens [split, n), per channel
+    __shared__ int32_t s_map_lo[kHeadDim];
+    __shared__ int32_t s_map_hi[kHeadDim];
     __shared__ uint32_t s_lut[33];
     __shared__ uint32_t s_inv;
     __shared__ int16_t s_q14[kHeadDim];
@@ -285,7 +315,7 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
             p += __shfl_xor(p, 1);
             p += __shfl_xor(p, 2);
             p += __shfl_xor(p, 4);
-            if (c == 0 && i < n) s_score[i] = score_of(p);
+            if (c == 0 && i < n) s_tok[i] = static_cast<uint32_t>(score_of(p));
         }
         __builtin_amdgcn_s_waitcnt(0);   // the V codes are in LDS before the barrier
         __syncthreads();
@@ -297,7 +327,7 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
         // coefficients of ordinary tokens (first and rescaling tokens count
         // zero) with the wave totals, and per-wave ballots of the first and
         // rescaling tokens.
-        const int32_t sv = d < n ? s_score[d] : INT32_MIN;
+        const int32_t sv = d < n ? static_cast<int32_t>(s_tok[d]) : INT32_MIN;
         int32_t incl = sv;
 #pragma unroll
         for (int k = 1; k < 64; k <<= 1) {
@@ -320,7 +350,7 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
         }
         const uint64_t special_mask = __ballot(special);
         s_word[d] = word;
-        s_coef[d] = word & kCoefMask;
+        s_tok[d] = word & kCoefMask;
         s_psum[d] = psum;
         if (lane == 63) s_wave_sum[wave] = psum;
         if (lane == 0) s_special[wave] = special_mask;
@@ -328,33 +358,37 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
         for (int w = 0; w < kChunk / 64; ++w) run_max = max(run_max, s_wave_max[w]);
         __syncthreads();
 
-        // Y (threads 0..127, one channel each) in token order, kBatch tokens
-        // at a time: their LDS reads go out together, and a batch with no
-        // first or rescaling token (the common case; the ballots say which)
-        // only adds its terms.  Slots past n have a zero coefficient, which
-        // makes a zero term.  Indices stay below kChunk (a multiple of kBatch).
+        // Y in two parts at once.  Waves 0-1 (one channel per thread) run
+        // tokens [0, split) in order; waves 2-3 compose tokens [split, n)
+        // into one map Y -> clamp(Y + A, L, H) (every ordinary token is
+        // Y -> sat32(Y + t), and such maps compose: A adds t, L and H take
+        // sat32(. + t)), which waves 0-1 apply after the barrier.  split is
+        // about 9/16 of n (a composed token costs four more operations),
+        // past the chunk's last first or rescaling token, and a multiple of
+        // kBatch.  Slots past n have a zero coefficient, so a zero term.
+        const int split0 = min(n, ((n * 9) / 16 + kBatch - 1) & ~(kBatch - 1));
+        int last_special = -1;
+#pragma unroll
+        for (int w = 0; w < kChunk / 64; ++w) {
+            const int lo = split0 - 64 * w;
+            if (lo < 64) {
+                uint64_t m = uniform64(s_special[w]);
+                if (lo > 0) m &= ~0ull << lo;
+                if (m != 0u) last_special = 64 * w + 63 - __builtin_clzll(m);
+            }
+        }
+        const int split = last_special < 0 ? split0 : (last_special + kBatch) & ~(kBatch - 1);
+        const int ch = d & (kHeadDim - 1), g = ch >> 5;
         if (d < kHeadDim) {
-            const int g = d >> 5;
-            for (int span = 0; span < n; span += 64) {
-                const uint64_t sp = s_special[span >> 6];
-                const uint64_t spans = (static_cast<uint64_t>(static_cast<uint32_t>(
-                                            __builtin_amdgcn_readfirstlane(static_cast<int>(sp >> 32)))) << 32) |
-                                       static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(sp)));
-                const int end = min(span + 64, n);
+            // A batch with no first or rescaling token (the ballots say which)
+            // only adds its terms.
+            for (int span = 0; span < split; span += 64) {
+                const uint64_t spans = uniform64(s_special[span >> 6]);
+                const int end = min(span + 64, split);
                 for (int i0 = span; i0 < end; i0 += kBatch) {
-                    const uint4 ca = *reinterpret_cast<const uint4*>(&s_coef[i0]);
-                    const uint4 cb = *reinterpret_cast<const uint4*>(&s_coef[i0 + 4]);
-                    const uint2 sw = *reinterpret_cast<const uint2*>(&s_vs[g][i0]);
-                    const uint32_t coef[kBatch] = {ca.x, ca.y, ca.z, ca.w, cb.x, cb.y, cb.z, cb.w};
-                    uint32_t sh[kBatch];
                     int32_t code[kBatch], term[kBatch];
-#pragma unroll
-                    for (int j = 0; j < kBatch; ++j) {
-                        code[j] = s_vc[i0 + j][d];
-                        sh[j] = ((j < 4 ? sw.x : sw.y) >> (8 * (j & 3))) & 0xffu;
-                    }
-#pragma unroll
-                    for (int j = 0; j < kBatch; ++j) term[j] = value_term(code[j], sh[j], coef[j]);
+                    uint32_t sh[kBatch];
+                    batch_terms(s_tok, s_vs[g], s_vc, i0, ch, code, sh, term);
                     if (((spans >> (i0 - span)) & 0xffu) == 0u) {
 #pragma unroll
                         for (int j = 0; j < kBatch; ++j) y = __builtin_elementwise_add_sat(y, term[j]);
@@ -368,30 +402,50 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
                     }
                 }
             }
-        } else if (wave == 2) {
-            // Z: ordinary tokens add their coefficients modulo 2^30, so
-            // between two first or rescaling tokens Z advances by a difference
-            // of prefix sums, and only those tokens step in order.
-            uint32_t done = 0u, offset = 0u;   // prefix sum already added; sum of the waves before
+        } else {
+            if (wave == 2) {
+                // Z: ordinary tokens add their coefficients modulo 2^30, so
+                // between two first or rescaling tokens Z advances by a
+                // difference of prefix sums, and only those tokens step in order.
+                uint32_t done = 0u, offset = 0u;   // prefix sum already added; sum of the waves before
 #pragma unroll
-            for (int w = 0; w < kChunk / 64; ++w) {
-                const uint64_t sp = s_special[w];
-                uint64_t m = (static_cast<uint64_t>(static_cast<uint32_t>(
-                                  __builtin_amdgcn_readfirstlane(static_cast<int>(sp >> 32)))) << 32) |
-                             static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(sp)));
-                while (m != 0u) {
-                    const int i = w * 64 + __builtin_ctzll(m);
-                    const uint32_t upto = offset + s_psum[i];   // sum of the ordinary tokens before i
-                    z = (z + (upto - done)) & kMask30;
-                    done = upto;
-                    z = z_step(z, static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(s_word[i]))));
-                    m &= m - 1u;
+                for (int w = 0; w < kChunk / 64; ++w) {
+                    uint64_t m = uniform64(s_special[w]);
+                    while (m != 0u) {
+                        const int i = w * 64 + __builtin_ctzll(m);
+                        const uint32_t upto = offset + s_psum[i];   // sum of the ordinary tokens before i
+                        z = (z + (upto - done)) & kMask30;
+                        done = upto;
+                        z = z_step(z, static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(s_word[i]))));
+                        m &= m - 1u;
+                    }
+                    offset += s_wave_sum[w];
                 }
-                offset += s_wave_sum[w];
+                z = (z + (offset - done)) & kMask30;
             }
-            z = (z + (offset - done)) & kMask30;
+            if (split < n) {
+                int64_t sum = 0;
+                int32_t lo = INT32_MIN, hi = INT32_MAX;
+                for (int i0 = split; i0 < n; i0 += kBatch) {
+                    int32_t code[kBatch], term[kBatch];
+                    uint32_t sh[kBatch];
+                    batch_terms(s_tok, s_vs[g], s_vc, i0, ch, code, sh, term);
+#pragma unroll
+                    for (int j = 0; j < kBatch; ++j) {
+                        sum += term[j];
+                        lo = __builtin_elementwise_add_sat(lo, term[j]);
+                        hi = __builtin_elementwise_add_sat(hi, term[j]);
+                    }
+                }
+                s_map_sum[ch] = sum;
+                s_map_lo[ch] = lo;
+                s_map_hi[ch] = hi;
+            }
         }
         __syncthreads();
+        if (d < kHeadDim && split < n)
+            y = static_cast<int32_t>(min(max(static_cast<int64_t>(y) + s_map_sum[ch], static_cast<int64_t>(s_map_lo[ch])),
+                                         static_cast<int64_t>(s_map_hi[ch])));
     }
     // The normalizer 1/Z: the 18-bit quotient floor((2^34 + Z/2) / Z) (cpp:271-300).
     if (wave == 2 && lane == 0)
