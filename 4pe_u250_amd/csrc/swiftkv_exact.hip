@@ -17,8 +17,10 @@
 //   - one thread per token turns its score and the exclusive prefix maximum
 //     into a coefficient word (exp LUT, rescale flag), and the same pass lays
 //     out prefix sums and ballots for Z and Y;
-//   - threads 0..127 run Y, one channel each, in token order, adding
-//     independently formed terms; wave 2 advances Z by prefix-sum
+//   - Y, one channel per thread: waves 0-1 run the chunk's first part in
+//     token order, adding independently formed terms, while waves 2-3
+//     compose the rest (no first or rescaling token) into one clamp-add map
+//     applied after the barrier; wave 2 also advances Z by prefix-sum
 //     differences and steps only at first and rescaling tokens;
 // then Y * 1/Z and the integer-path A14/E8M0 epilogue.
 #include "swiftkv_device.hpp"
@@ -29,9 +31,9 @@ namespace {
 using namespace dev;
 
 constexpr int kChunk = 256;                   // cached tokens per chunk (V codes staged in LDS)
-constexpr int kBatch = 8;                     // tokens whose LDS reads go out together in the Y and Z passes
+constexpr int kBatch = 16;                    // tokens whose LDS reads go out together in the Y pass
 static_assert(kChunk % kBatch == 0, "batches tile a chunk");
-static_assert(kBatch == 8, "the Y pass reads a batch's coefficients as two 16-byte LDS loads");
+static_assert(kBatch % 8 == 0 && 64 % kBatch == 0, "a batch is whole 8-byte shift reads inside one 64-token ballot");
 constexpr int kPasses = kChunk / 32;          // score passes per chunk: 4 waves x 8 token rows each
 constexpr int64_t kScoreScaleQ17 = 11585;     // RNE(2^17 / sqrt(128)) (swiftkv_attention.cpp:1101-1102)
 constexpr int64_t kLog2eQ21 = 3025551;        // RNE(log2(e) * 2^21) (cpp:207-208)
@@ -136,8 +138,7 @@ __device__ __forceinline__ uint32_t shift_of(float scale) { return (__float_as_u
 // (the reference raises it only on a strictly larger score, and a maximum
 // does not depend on order), so every token's coefficient and rescale flag
 // follow from its score and that prefix maximum, for all tokens of a chunk at
-// once.  What stays sequential is Z (one wave, a few operations per token)
-// and Y (one lane per channel).
+// once.  What stays sequential is Z at first and rescaling tokens, and Y.
 constexpr uint32_t kInit = 1u << 31;      // first token of the sequence: Y = v, Z = 1
 constexpr uint32_t kRescale = 1u << 30;   // new maximum: Y = Y * coef + v, Z = Z * coef + 1
 constexpr uint32_t kCoefMask = (1u << 18) - 1u;
@@ -201,19 +202,30 @@ __device__ __forceinline__ uint64_t uniform64(uint64_t v) {
 }
 
 // The codes, shifts and Y terms of tokens [i0, i0 + kBatch) for channel ch:
-// two 16-byte reads give the coefficients, one 8-byte read the shifts (stored
-// by group), and one byte read per token the code.
+// 16-byte reads give the coefficients, 8-byte reads the shifts (stored by
+// group), and one byte read per token the code.
 __device__ __forceinline__ void batch_terms(const uint32_t* s_coef, const uint8_t* s_vs_g,
                                             const int8_t (*s_vc)[kHeadDim], int i0, int ch, int32_t* code,
                                             uint32_t* sh, int32_t* term) {
-    const uint4 ca = *reinterpret_cast<const uint4*>(&s_coef[i0]);
-    const uint4 cb = *reinterpret_cast<const uint4*>(&s_coef[i0 + 4]);
-    const uint2 sw = *reinterpret_cast<const uint2*>(&s_vs_g[i0]);
-    const uint32_t coef[kBatch] = {ca.x, ca.y, ca.z, ca.w, cb.x, cb.y, cb.z, cb.w};
+    uint32_t coef[kBatch], shw[kBatch / 4];
+#pragma unroll
+    for (int q = 0; q < kBatch / 4; ++q) {
+        const uint4 cq = *reinterpret_cast<const uint4*>(&s_coef[i0 + 4 * q]);
+        coef[4 * q] = cq.x;
+        coef[4 * q + 1] = cq.y;
+        coef[4 * q + 2] = cq.z;
+        coef[4 * q + 3] = cq.w;
+    }
+#pragma unroll
+    for (int q = 0; q < kBatch / 8; ++q) {
+        const uint2 sw = *reinterpret_cast<const uint2*>(&s_vs_g[i0 + 8 * q]);
+        shw[2 * q] = sw.x;
+        shw[2 * q + 1] = sw.y;
+    }
 #pragma unroll
     for (int j = 0; j < kBatch; ++j) {
         code[j] = s_vc[i0 + j][ch];
-        sh[j] = ((j < 4 ? sw.x : sw.y) >> (8 * (j & 3))) & 0xffu;
+        sh[j] = (shw[j >> 2] >> (8 * (j & 3))) & 0xffu;
     }
 #pragma unroll
     for (int j = 0; j < kBatch; ++j) term[j] = value_term(code[j], sh[j], coef[j]);
@@ -389,7 +401,7 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
                     int32_t code[kBatch], term[kBatch];
                     uint32_t sh[kBatch];
                     batch_terms(s_tok, s_vs[g], s_vc, i0, ch, code, sh, term);
-                    if (((spans >> (i0 - span)) & 0xffu) == 0u) {
+                    if (((spans >> (i0 - span)) & ((1ull << kBatch) - 1u)) == 0u) {
 #pragma unroll
                         for (int j = 0; j < kBatch; ++j) y = __builtin_elementwise_add_sat(y, term[j]);
                     } else {
