@@ -422,20 +422,35 @@ __global__ __launch_bounds__(WAVES * 64) void step_kernel(StepArgs a) {
 
 // ---------------------------------------------------------------- utilities
 
-// Grid (n, 8): token t = blockIdx.x, wave = head.
+constexpr int kAppendTokens = 2;   // prefill rows per wave (their loads in flight together)
+
+// Grid (ceil(n / kAppendTokens), 8): wave = head (4 per workgroup), each
+// wave kAppendTokens consecutive tokens.  All of the wave's loads (k, v and
+// the RoPE pair of every token) go out before any row is quantized, so a
+// wave keeps kAppendTokens rows in flight; tokens past n load the last token
+// and store nothing.
 template <bool Q17>
 __global__ __launch_bounds__(256) void append_bulk_kernel(BulkArgs a) {
-    const int t = blockIdx.x;
     const int h = blockIdx.y * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    const int pos = a.pos0 + t;
-    const size_t elem = static_cast<size_t>(t) * kModelDim + h * kHeadDim + 2 * lane;
-    const int2 cs = a.lut[static_cast<size_t>(pos) * kRopePairs + lane];
-    const int2 ki = load_pair<Q17>(a.k, elem);
-    const int2 vi = load_pair<Q17>(a.v, elem);
-    int32_t k0, k1;
-    rope_pair(ki.x, ki.y, cs, k0, k1);
-    append_row(page_ptr(a.kv, a.slot, a.layer, h), a.kv.seq_cap, pos, lane, k0, k1, vi.x, vi.y);
+    const int t0 = blockIdx.x * kAppendTokens;
+    int2 cs[kAppendTokens], ki[kAppendTokens], vi[kAppendTokens];
+#pragma unroll
+    for (int j = 0; j < kAppendTokens; ++j) {
+        const int t = min(t0 + j, a.n - 1);
+        const size_t elem = static_cast<size_t>(t) * kModelDim + h * kHeadDim + 2 * lane;
+        cs[j] = a.lut[static_cast<size_t>(a.pos0 + t) * kRopePairs + lane];
+        ki[j] = load_pair<Q17>(a.k, elem);
+        vi[j] = load_pair<Q17>(a.v, elem);
+    }
+    int8_t* page = page_ptr(a.kv, a.slot, a.layer, h);
+#pragma unroll
+    for (int j = 0; j < kAppendTokens; ++j) {
+        if (t0 + j >= a.n) break;
+        int32_t k0, k1;
+        rope_pair(ki[j].x, ki[j].y, cs[j], k0, k1);
+        append_row(page, a.kv.seq_cap, a.pos0 + t0 + j, lane, k0, k1, vi[j].x, vi[j].y);
+    }
 }
 
 // out[i] = Q15.17 of in[i] (NP = 1) or of the NP reduced split-K partials.
@@ -489,7 +504,7 @@ hipError_t launch_step(const StepArgs& a, int grid_splits, int waves, InputForma
 }
 
 hipError_t launch_append_bulk(const BulkArgs& a, bool q17, hipStream_t s) {
-    const dim3 grid(a.n, kHeads / 4);
+    const dim3 grid((a.n + kAppendTokens - 1) / kAppendTokens, kHeads / 4);
     if (q17) append_bulk_kernel<true><<<grid, 256, 0, s>>>(a);
     else append_bulk_kernel<false><<<grid, 256, 0, s>>>(a);
     return hipGetLastError();
