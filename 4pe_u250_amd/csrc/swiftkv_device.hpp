@@ -77,6 +77,20 @@ __device__ __forceinline__ float dpp_f(float x) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), Ctrl, 0xF, 0xF, true));
 }
 
+template <int Ctrl>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t x) {
+    return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), Ctrl, 0xF, 0xF, true));
+}
+
+// Max over the 16 lanes of an aligned DPP row (one G32 group of a row when
+// lane l holds channels 2l and 2l+1); every lane gets it.
+__device__ __forceinline__ uint32_t row16_max(uint32_t x) {
+    x = max(x, dpp_u<kDppQuadXor1>(x));
+    x = max(x, dpp_u<kDppQuadXor2>(x));
+    x = max(x, dpp_u<kDppHalfMirror>(x));
+    return max(x, dpp_u<kDppRowRor8>(x));
+}
+
 // Sum over the 8 lanes of an aligned octet; every lane gets the same bits
 // (each step adds a value and its partner in commutative order).
 __device__ __forceinline__ float octet_sum(float x) {
@@ -181,13 +195,8 @@ struct RowCodes {
 
 __device__ __forceinline__ RowCodes append_row_codes(int8_t* page, int seq_cap, int pos, int lane, int32_t k0,
                                                      int32_t k1, int32_t v0, int32_t v1) {
-    uint32_t mk = max(magnitude(k0), magnitude(k1));
-    uint32_t mv = max(magnitude(v0), magnitude(v1));
-#pragma unroll
-    for (int d = 1; d < 16; d <<= 1) {
-        mk = max(mk, static_cast<uint32_t>(__shfl_xor(static_cast<int>(mk), d)));
-        mv = max(mv, static_cast<uint32_t>(__shfl_xor(static_cast<int>(mv), d)));
-    }
+    const uint32_t mk = row16_max(max(magnitude(k0), magnitude(k1)));
+    const uint32_t mv = row16_max(max(magnitude(v0), magnitude(v1)));
     RowCodes rc;
     rc.sk = g32_shift(mk);
     rc.sv = g32_shift(mv);
