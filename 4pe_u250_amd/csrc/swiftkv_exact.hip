@@ -5,9 +5,10 @@
 // (max, Z, Y) recurrence is sequential per head -- and meant for bit-level
 // comparison with the FPGA / C model; the sequential chains bound it, not HBM.
 //
-// Grid (32 heads, batch rows), 256 threads per (sequence, head).  Wave 0
-// first appends the new row like the fast step; then tokens [0, position]
-// are processed in chunks of kChunk:
+// Grid (32 heads x SLICES, batch rows), 256 threads per (sequence, head,
+// slice of 128 / SLICES channels); SLICES is 4 for the smallest batches and
+// 1 otherwise.  Wave 0 first appends the new row like the fast step; then
+// tokens [0, position] are processed in chunks of kChunk:
 //   - the 4 waves issue all of the chunk's loads at once (K codes and scales
 //     into registers, V codes straight into LDS), then compute the integer
 //     scores (lane = 16-channel half-group c of token row r; the per-half
@@ -17,11 +18,12 @@
 //   - one thread per token turns its score and the exclusive prefix maximum
 //     into a coefficient word (exp LUT, rescale flag), and the same pass lays
 //     out prefix sums and ballots for Z and Y;
-//   - Y, one channel per thread: waves 0-1 run the chunk's first part in
-//     token order, adding independently formed terms, while waves 2-3
-//     compose the rest (no first or rescaling token) into one clamp-add map
-//     applied after the barrier; wave 2 also advances Z by prefix-sum
-//     differences and steps only at first and rescaling tokens;
+//   - Y, one channel per thread: the first kCh threads run the chunk's
+//     first part in token order, adding independently formed terms, while
+//     the rest of the threads compose the remaining tokens (no first or
+//     rescaling token among them) into clamp-add maps applied after the
+//     barrier; wave 3 also advances Z by prefix-sum differences and steps
+//     only at first and rescaling tokens;
 // then Y * 1/Z and the integer-path A14/E8M0 epilogue.
 #include "swiftkv_device.hpp"
 
@@ -35,6 +37,11 @@ constexpr int kBatch = 16;                    // tokens whose LDS reads go out t
 static_assert(kChunk % kBatch == 0, "batches tile a chunk");
 static_assert(kBatch % 8 == 0 && 64 % kBatch == 0, "a batch is whole 8-byte shift reads inside one 64-token ballot");
 constexpr int kPasses = kChunk / 32;          // score passes per chunk: 4 waves x 8 token rows each
+// Largest batch whose launch splits each head's Y over 4 workgroups (32
+// channels each): at context 4096 this took batch 1 and 2 from 175 to 147-150
+// us, was even at batch 4 and slower from batch 8 on, where one workgroup per
+// head already fills the machine and the 4x score work shows.
+constexpr int kExactSlicedMaxBatch = 2;
 constexpr int64_t kScoreScaleQ17 = 11585;     // RNE(2^17 / sqrt(128)) (swiftkv_attention.cpp:1101-1102)
 constexpr int64_t kLog2eQ21 = 3025551;        // RNE(log2(e) * 2^21) (cpp:207-208)
 
@@ -236,11 +243,26 @@ struct ExactArgs {
     uint32_t exp_lut[33];     // RNE(2^(30 + i/32)), i = 0..32 (cpp:185-195)
 };
 
-template <bool Q17>
+// SLICES workgroups share a (sequence, head): each runs the whole token loop
+// (scores, coefficients, Z) but Y for kHeadDim / SLICES channels only, so a
+// small batch spreads over more CUs.  All of them append the new row; they
+// write the same bytes.
+template <bool Q17, int SLICES>
 __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
+    static_assert(SLICES == 1 || SLICES == 4, "128 or 32 channels per workgroup");
+    // Y roles: threads [0, kCh) run the ordered part (one channel each),
+    // threads [kSeqLanes, 256) compose kCompParts parts of kCh channels,
+    // threads in between (wave 0's upper half when kCh = 32) idle.
+    constexpr int kCh = kHeadDim / SLICES;
+    constexpr int kSeqLanes = kCh < 64 ? 64 : kCh;
+    constexpr int kCompParts = (256 - kSeqLanes) / kCh;
+    // The ordered part's share of a chunk: a composed token costs about 15
+    // operations against 12, so about 9/16 with one composed part and 3/16
+    // with six.
+    constexpr int kSeqShare16 = kCompParts == 1 ? 9 : 3;
     const StepArgs& a = ea.step;
     const uint32_t row = a.rows[blockIdx.y];
-    const int h = blockIdx.x, b = static_cast<int>(row & 0xffu);
+    const int h = blockIdx.x / SLICES, slice = blockIdx.x % SLICES, b = static_cast<int>(row & 0xffu);
     const int pos = static_cast<int>(row >> 8);
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int lane = threadIdx.x & 63;
@@ -261,12 +283,12 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
     __shared__ int32_t s_wave_max[kChunk / 64];
     __shared__ uint32_t s_wave_sum[kChunk / 64];
     __shared__ uint64_t s_special[kChunk / 64];          // per-wave ballots of first and rescaling tokens
-    __shared__ int64_t s_map_sum[kHeadDim];              // the composed map of tokens [split, n), per channel
-    __shared__ int32_t s_map_lo[kHeadDim];
-    __shared__ int32_t s_map_hi[kHeadDim];
+    __shared__ int64_t s_map_sum[kCompParts * kCh];      // the composed maps of the parts after split
+    __shared__ int32_t s_map_lo[kCompParts * kCh];
+    __shared__ int32_t s_map_hi[kCompParts * kCh];
     __shared__ uint32_t s_lut[33];
     __shared__ uint32_t s_inv;
-    __shared__ int16_t s_q14[kHeadDim];
+    __shared__ int16_t s_q14[kCh];
     if (threadIdx.x < 33) s_lut[threadIdx.x] = ea.exp_lut[threadIdx.x];
 
     // Wave 0 rotates the query into LDS and appends the new row; the barrier
@@ -296,8 +318,8 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
 
     const int len = pos + 1;
     int32_t run_max = INT32_MIN;   // prefix maximum before the chunk (every thread)
-    uint32_t z = 0;                // Z (wave 2, uniform)
-    int32_t y = 0;                 // Y of channel d (threads d < 128)
+    uint32_t z = 0;                // Z (wave 3, uniform)
+    int32_t y = 0;                 // Y of channel slice * kCh + d (threads d < kCh)
     for (int t0 = 0; t0 < len; t0 += kChunk) {
         const int n = min(kChunk, len - t0);
         // Scores of tokens [t0, t0+n), 4 waves x 8 token rows per pass.  All
@@ -370,15 +392,16 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
         for (int w = 0; w < kChunk / 64; ++w) run_max = max(run_max, s_wave_max[w]);
         __syncthreads();
 
-        // Y in two parts at once.  Waves 0-1 (one channel per thread) run
-        // tokens [0, split) in order; waves 2-3 compose tokens [split, n)
-        // into one map Y -> clamp(Y + A, L, H) (every ordinary token is
-        // Y -> sat32(Y + t), and such maps compose: A adds t, L and H take
-        // sat32(. + t)), which waves 0-1 apply after the barrier.  split is
-        // about 9/16 of n (a composed token costs four more operations),
-        // past the chunk's last first or rescaling token, and a multiple of
-        // kBatch.  Slots past n have a zero coefficient, so a zero term.
-        const int split0 = min(n, ((n * 9) / 16 + kBatch - 1) & ~(kBatch - 1));
+        // Y in parts at once.  Threads [0, kCh) (one channel each) run
+        // tokens [0, split) in order; the composing threads split [split, n)
+        // into kCompParts runs of q tokens and compose each run into one map
+        // Y -> clamp(Y + A, L, H) (every ordinary token is Y -> sat32(Y + t),
+        // and such maps compose: A adds t, L and H take sat32(. + t)), which
+        // the ordered threads apply in order after the barrier.  split is
+        // about kSeqShare16/16 of n, past the chunk's last first or rescaling
+        // token, and a multiple of kBatch, and so is q.  Slots past n have a
+        // zero coefficient, so a zero term.
+        const int split0 = min(n, ((n * kSeqShare16) / 16 + kBatch - 1) & ~(kBatch - 1));
         int last_special = -1;
 #pragma unroll
         for (int w = 0; w < kChunk / 64; ++w) {
@@ -390,8 +413,12 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
             }
         }
         const int split = last_special < 0 ? split0 : (last_special + kBatch) & ~(kBatch - 1);
-        const int ch = d & (kHeadDim - 1), g = ch >> 5;
-        if (d < kHeadDim) {
+        const int rest = n - split;
+        const int q = rest > 0 ? ((rest + kCompParts - 1) / kCompParts + kBatch - 1) & ~(kBatch - 1) : 0;
+        const int cp = d < kSeqLanes ? 0 : (d - kSeqLanes) / kCh;   // composed part of a composing thread
+        const int cl = d < kSeqLanes ? d % kCh : (d - kSeqLanes) % kCh;
+        const int ch = slice * kCh + cl, g = ch >> 5;
+        if (d < kCh) {
             // A batch with no first or rescaling token (the ballots say which)
             // only adds its terms.
             for (int span = 0; span < split; span += 64) {
@@ -414,8 +441,8 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
                     }
                 }
             }
-        } else {
-            if (wave == 2) {
+        } else if (d >= kSeqLanes) {
+            if (wave == 3) {
                 // Z: ordinary tokens add their coefficients modulo 2^30, so
                 // between two first or rescaling tokens Z advances by a
                 // difference of prefix sums, and only those tokens step in order.
@@ -435,10 +462,11 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
                 }
                 z = (z + (offset - done)) & kMask30;
             }
-            if (split < n) {
+            const int begin = split + cp * q, end = min(n, begin + q);
+            if (begin < n) {
                 int64_t sum = 0;
                 int32_t lo = INT32_MIN, hi = INT32_MAX;
-                for (int i0 = split; i0 < n; i0 += kBatch) {
+                for (int i0 = begin; i0 < end; i0 += kBatch) {
                     int32_t code[kBatch], term[kBatch];
                     uint32_t sh[kBatch];
                     batch_terms(s_tok, s_vs[g], s_vc, i0, ch, code, sh, term);
@@ -449,18 +477,24 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
                         hi = __builtin_elementwise_add_sat(hi, term[j]);
                     }
                 }
-                s_map_sum[ch] = sum;
-                s_map_lo[ch] = lo;
-                s_map_hi[ch] = hi;
+                s_map_sum[cp * kCh + cl] = sum;
+                s_map_lo[cp * kCh + cl] = lo;
+                s_map_hi[cp * kCh + cl] = hi;
             }
         }
         __syncthreads();
-        if (d < kHeadDim && split < n)
-            y = static_cast<int32_t>(min(max(static_cast<int64_t>(y) + s_map_sum[ch], static_cast<int64_t>(s_map_lo[ch])),
-                                         static_cast<int64_t>(s_map_hi[ch])));
+        if (d < kCh) {
+#pragma unroll
+            for (int p = 0; p < kCompParts; ++p) {
+                if (split + p * q >= n) break;
+                const int k = p * kCh + cl;
+                y = static_cast<int32_t>(min(max(static_cast<int64_t>(y) + s_map_sum[k], static_cast<int64_t>(s_map_lo[k])),
+                                             static_cast<int64_t>(s_map_hi[k])));
+            }
+        }
     }
     // The normalizer 1/Z: the 18-bit quotient floor((2^34 + Z/2) / Z) (cpp:271-300).
-    if (wave == 2 && lane == 0)
+    if (wave == 3 && lane == 0)
         s_inv = z ? static_cast<uint32_t>(((1ull << 34) + (z >> 1)) / z) & 0x3ffffu : 0x3ffffu;
     __syncthreads();
 
@@ -468,12 +502,13 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
     // and the integer-path A14/E8M0 (cpp:1694-1771, 2656-2682): group max of
     // |raw| (INT32_MIN counts as INT32_MAX), one float conversion, frexp
     // exponent e, q = trunc(clamp(raw*2^-17 * 2^(13-e) +- 0.5, +-8191)),
-    // code = e + 127.  Threads d < 128 own channel d; a group is 32 lanes of
-    // one wave.
-    const size_t grp0 = static_cast<size_t>(b) * (kHeads * kGroupsPerHead) + h * kGroupsPerHead;
-    if (d < kHeadDim) {
+    // code = e + 127.  Threads d < kCh own channel slice * kCh + d; a group
+    // is 32 lanes of one wave.
+    constexpr int kGroups = kCh / 32;   // G32 groups of this workgroup
+    const size_t grp0 = static_cast<size_t>(b) * (kHeads * kGroupsPerHead) + h * kGroupsPerHead + slice * kGroups;
+    if (d < kCh) {
         const int32_t o = mulq17_wrap(y, s_inv);
-        reinterpret_cast<int32_t*>(a.out)[static_cast<size_t>(b) * kModelDim + h * kHeadDim + d] = o;
+        reinterpret_cast<int32_t*>(a.out)[static_cast<size_t>(b) * kModelDim + h * kHeadDim + slice * kCh + d] = o;
         int32_t m = o == INT32_MIN ? INT32_MAX : (o < 0 ? -o : o);
 #pragma unroll
         for (int s = 1; s < 32; s <<= 1) m = max(m, __shfl_xor(m, s));
@@ -493,7 +528,7 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
         if (a.act_scale != nullptr && (d & 31) == 0) a.act_scale[grp0 + (d >> 5)] = code;
     }
     __syncthreads();
-    if (a.act_q != nullptr && d < kGroupsPerHead * 14) {
+    if (a.act_q != nullptr && d < kGroups * 14) {
         const int gi = d / 14, w = d % 14;
         uint32_t word = 0;
         const int bit0 = 32 * w;
@@ -512,9 +547,15 @@ hipError_t launch_exact(const StepArgs& a, const uint32_t* exp_lut, bool q17, hi
     ExactArgs ea;
     ea.step = a;
     for (int i = 0; i < 33; ++i) ea.exp_lut[i] = exp_lut[i];
-    const dim3 grid(kHeads, a.batch);
-    if (q17) exact_kernel<true><<<grid, 256, 0, s>>>(ea);
-    else exact_kernel<false><<<grid, 256, 0, s>>>(ea);
+    if (a.batch <= kExactSlicedMaxBatch) {
+        const dim3 grid(kHeads * 4, a.batch);
+        if (q17) exact_kernel<true, 4><<<grid, 256, 0, s>>>(ea);
+        else exact_kernel<false, 4><<<grid, 256, 0, s>>>(ea);
+    } else {
+        const dim3 grid(kHeads, a.batch);
+        if (q17) exact_kernel<true, 1><<<grid, 256, 0, s>>>(ea);
+        else exact_kernel<false, 1><<<grid, 256, 0, s>>>(ea);
+    }
     return hipGetLastError();
 }
 

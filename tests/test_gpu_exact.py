@@ -99,6 +99,7 @@ def test_exact_matches_reference_decode(skv, ctx, lut4096, golden, case):
     ([257, 511, 512, 1030], "t3", False),
     ([1500, 77], "t3", True),
     ([300, 700], "wide", False),
+    ([300, 700, 5, 257, 256, 511, 1, 0, 64], "wide", False),
 ])
 def test_exact_matches_oracle_integer_recurrence(skv, ctx, lut4096, rope_tables, positions, dist, q17):
     _note(f"case: exact vs oracle, positions {positions}, {dist}, q17={q17}")
