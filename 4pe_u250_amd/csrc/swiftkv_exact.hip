@@ -9,8 +9,9 @@
 // slice of 128 / SLICES channels); SLICES is 4 for the smallest batches and
 // 1 otherwise.  Wave 0 first appends the new row like the fast step; then
 // tokens [0, position] are processed in chunks of kChunk:
-//   - the 4 waves issue all of the chunk's loads at once (K codes and scales
-//     into registers, V codes straight into LDS), then compute the integer
+//   - the 4 waves issue all of the chunk's loads at once through one buffer
+//     resource (K codes and scales into registers, V codes straight into
+//     LDS), then compute the integer
 //     scores (lane = 16-channel half-group c of token row r; the per-half
 //     shift and the 44-bit wraps are associative modulo 2^44, so the octet
 //     sum may run in any order), the exact 64-bit dot taken as signed-byte
@@ -201,6 +202,24 @@ __device__ __forceinline__ int32_t value_step(int32_t y, uint32_t word, int32_t 
     return __builtin_elementwise_add_sat(y, term);
 }
 
+typedef int32_t ExV4i __attribute__((ext_vector_type(4)));
+typedef uint32_t ExV2u __attribute__((ext_vector_type(2)));
+constexpr int32_t kExBufferWord3 = 0x00020000;   // raw buffer, gfx9 data format
+
+// Sum over the 8 lanes of an aligned octet of a 64-bit integer (DPP moves of
+// both halves, integer adds, so exact in any order); every lane gets it.
+template <int Ctrl>
+__device__ __forceinline__ int64_t dpp64(int64_t x) {
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), Ctrl, 0xF, 0xF, true));
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x >> 32), Ctrl, 0xF, 0xF, true));
+    return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+__device__ __forceinline__ int64_t octet_sum64(int64_t x) {
+    x += dpp64<kDppQuadXor1>(x);
+    x += dpp64<kDppQuadXor2>(x);
+    return x + dpp64<kDppHalfMirror>(x);
+}
+
 // A wave-uniform 64-bit value read by every lane, moved to scalar registers.
 __device__ __forceinline__ uint64_t uniform64(uint64_t v) {
     return (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(v >> 32))))
@@ -270,7 +289,8 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
     const int d = threadIdx.x;                  // token of the chunk (coefficients), channel (Y, d < 128)
     int8_t* page = page_ptr(a.kv, a.slot0 + b, a.layer, h);
     const int64_t cap = a.kv.seq_cap;
-    const float* scales = reinterpret_cast<const float*>(page + cap * (2 * kCodeBytes));
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        page, static_cast<short>(0), static_cast<int32_t>(cap * kTokenBytes), kExBufferWord3);
 
     __shared__ int32_t s_q[kHeadDim];
     // Per token of the chunk: the score, then (each thread rewrites its own
@@ -328,27 +348,29 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
         // writes bytes [16 l, 16 l + 16) of its 8 rows, which is channel
         // chunk c of row r).  Rows past n load the chunk's last token (inside
         // the page) and are not used.
-        int4 kq[kPasses];
-        float2 scl[kPasses];
+        // The page is read through one buffer resource: per-lane 32-bit
+        // offsets within the chunk, the chunk's own offset in an SGPR.
+        ExV4i kq[kPasses];
+        ExV2u scl[kPasses];
+        const int32_t k_chunk = t0 * kCodeBytes, v_chunk = static_cast<int32_t>(cap + t0) * kCodeBytes;
+        const int32_t s_chunk = static_cast<int32_t>(cap * 2 * kCodeBytes) + t0 * kScaleBytes;
 #pragma unroll
         for (int ps = 0; ps < kPasses; ++ps) {
-            const int64_t t = t0 + min(wave * 8 + r + 32 * ps, n - 1);
-            scl[ps] = *reinterpret_cast<const float2*>(scales + t * 8 + (c >> 1) * 2);
-            kq[ps] = *reinterpret_cast<const int4*>(page + t * kCodeBytes + c * 16);
-            __builtin_amdgcn_global_load_lds(page + (cap + t) * kCodeBytes + c * 16,
-                                             (__attribute__((address_space(3))) void*)&s_vc[wave * 8 + 32 * ps][0],
-                                             16, 0, 0);
+            const int32_t tr = min(wave * 8 + r + 32 * ps, n - 1);
+            scl[ps] = __builtin_amdgcn_raw_buffer_load_b64(rsrc, tr * kScaleBytes + (c >> 1) * 8, s_chunk, 0);
+            kq[ps] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, tr * kCodeBytes + c * 16, k_chunk, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rsrc, (__attribute__((address_space(3))) void*)&s_vc[wave * 8 + 32 * ps][0], 16,
+                tr * kCodeBytes + c * 16, v_chunk, 0, 0);
         }
 #pragma unroll
         for (int ps = 0; ps < kPasses; ++ps) {
             const int i = wave * 8 + r + 32 * ps;
-            int64_t p = half_dot(ql, kq[ps], shift_of(scl[ps].x));
+            const int4 kw = make_int4(kq[ps].x, kq[ps].y, kq[ps].z, kq[ps].w);
+            // the token's sum of its 8 half-groups (lanes 8r .. 8r+7), exact
+            const int64_t p = octet_sum64(half_dot(ql, kw, shift_of(__uint_as_float(scl[ps].x))));
             // slots past n are read by the Y pass with a zero coefficient
-            if ((c & 1) == 0) s_vs[c >> 1][i] = i < n ? static_cast<uint8_t>(shift_of(scl[ps].y)) : 0;
-            // sum of the token's 8 half-groups (lanes 8r .. 8r+7), modulo 2^44
-            p += __shfl_xor(p, 1);
-            p += __shfl_xor(p, 2);
-            p += __shfl_xor(p, 4);
+            if ((c & 1) == 0) s_vs[c >> 1][i] = i < n ? static_cast<uint8_t>(shift_of(__uint_as_float(scl[ps].y))) : 0;
             if (c == 0 && i < n) s_tok[i] = static_cast<uint32_t>(score_of(p));
         }
         __builtin_amdgcn_s_waitcnt(0);   // the V codes are in LDS before the barrier
