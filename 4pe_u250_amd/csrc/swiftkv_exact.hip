@@ -220,6 +220,37 @@ __device__ __forceinline__ int64_t octet_sum64(int64_t x) {
     return x + dpp64<kDppHalfMirror>(x);
 }
 
+// Inclusive wave scans with DPP (GFX9): row shifts by 1, 2, 4, 8 scan each
+// 16-lane row, then row 0's last lane is broadcast into row 1 and row 2's
+// into row 3, then lane 31 into rows 2 and 3.  Lanes a move cannot reach, and
+// rows outside its row mask, take the identity.
+constexpr int kDppRowShr1 = 0x111, kDppRowShr2 = 0x112, kDppRowShr4 = 0x114, kDppRowShr8 = 0x118;
+constexpr int kDppRowBcast15 = 0x142, kDppRowBcast31 = 0x143, kDppWaveShr1 = 0x138;
+
+template <int Ctrl, int RowMask>
+__device__ __forceinline__ int32_t dpp_shifted(int32_t identity, int32_t x) {
+    return __builtin_amdgcn_update_dpp(identity, x, Ctrl, RowMask, 0xF, false);
+}
+
+__device__ __forceinline__ int32_t wave_scan_max(int32_t x) {
+    x = max(x, dpp_shifted<kDppRowShr1, 0xF>(INT32_MIN, x));
+    x = max(x, dpp_shifted<kDppRowShr2, 0xF>(INT32_MIN, x));
+    x = max(x, dpp_shifted<kDppRowShr4, 0xF>(INT32_MIN, x));
+    x = max(x, dpp_shifted<kDppRowShr8, 0xF>(INT32_MIN, x));
+    x = max(x, dpp_shifted<kDppRowBcast15, 0xA>(INT32_MIN, x));
+    return max(x, dpp_shifted<kDppRowBcast31, 0xC>(INT32_MIN, x));
+}
+
+__device__ __forceinline__ uint32_t wave_scan_add(uint32_t v) {
+    int32_t x = static_cast<int32_t>(v);
+    x += dpp_shifted<kDppRowShr1, 0xF>(0, x);
+    x += dpp_shifted<kDppRowShr2, 0xF>(0, x);
+    x += dpp_shifted<kDppRowShr4, 0xF>(0, x);
+    x += dpp_shifted<kDppRowShr8, 0xF>(0, x);
+    x += dpp_shifted<kDppRowBcast15, 0xA>(0, x);
+    return static_cast<uint32_t>(x + dpp_shifted<kDppRowBcast31, 0xC>(0, x));
+}
+
 // A wave-uniform 64-bit value read by every lane, moved to scalar registers.
 __device__ __forceinline__ uint64_t uniform64(uint64_t v) {
     return (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(v >> 32))))
@@ -384,26 +415,16 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
         // zero) with the wave totals, and per-wave ballots of the first and
         // rescaling tokens.
         const int32_t sv = d < n ? static_cast<int32_t>(s_tok[d]) : INT32_MIN;
-        int32_t incl = sv;
-#pragma unroll
-        for (int k = 1; k < 64; k <<= 1) {
-            const int32_t o = __shfl_up(incl, k);
-            if (lane >= k) incl = max(incl, o);
-        }
+        const int32_t incl = wave_scan_max(sv);
         if (lane == 63) s_wave_max[wave] = incl;
-        int32_t excl = __shfl_up(incl, 1);
+        int32_t excl = dpp_shifted<kDppWaveShr1, 0xF>(INT32_MIN, incl);
         __syncthreads();
         int32_t before = run_max;
         for (int w = 0; w < wave; ++w) before = max(before, s_wave_max[w]);
         excl = lane == 0 ? before : max(before, excl);
         const uint32_t word = d >= n ? 0u : (t0 == 0 && d == 0) ? kInit : coef_word(sv, excl, s_lut);
         const bool special = (word & (kInit | kRescale)) != 0u;
-        uint32_t psum = special ? 0u : (word & kCoefMask);
-#pragma unroll
-        for (int k = 1; k < 64; k <<= 1) {
-            const uint32_t o = __shfl_up(psum, k);
-            if (lane >= k) psum += o;
-        }
+        const uint32_t psum = wave_scan_add(special ? 0u : (word & kCoefMask));
         const uint64_t special_mask = __ballot(special);
         s_word[d] = word;
         s_tok[d] = word & kCoefMask;
