@@ -371,29 +371,43 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
     int32_t run_max = INT32_MIN;   // prefix maximum before the chunk (every thread)
     uint32_t z = 0;                // Z (wave 3, uniform)
     int32_t y = 0;                 // Y of channel slice * kCh + d (threads d < kCh)
-    for (int t0 = 0; t0 < len; t0 += kChunk) {
-        const int n = min(kChunk, len - t0);
-        // Scores of tokens [t0, t0+n), 4 waves x 8 token rows per pass.  All
-        // passes' loads go out first: per lane the K codes and scale pair
-        // into registers, and the V codes straight into LDS (lane l of a wave
-        // writes bytes [16 l, 16 l + 16) of its 8 rows, which is channel
-        // chunk c of row r).  Rows past n load the chunk's last token (inside
-        // the page) and are not used.
-        // The page is read through one buffer resource: per-lane 32-bit
-        // offsets within the chunk, the chunk's own offset in an SGPR.
-        ExV4i kq[kPasses];
-        ExV2u scl[kPasses];
-        const int32_t k_chunk = t0 * kCodeBytes, v_chunk = static_cast<int32_t>(cap + t0) * kCodeBytes;
-        const int32_t s_chunk = static_cast<int32_t>(cap * 2 * kCodeBytes) + t0 * kScaleBytes;
+    // A chunk's loads, 4 waves x 8 token rows per pass: per lane the K codes
+    // and scale pair into registers, and the V codes straight into LDS (lane
+    // l of a wave writes bytes [16 l, 16 l + 16) of its 8 rows, which is
+    // channel chunk c of row r), all passes at once.  Rows past the chunk's
+    // end load its last token (inside the page) and are not used.  The page
+    // is read through one buffer resource: per-lane 32-bit offsets within the
+    // chunk, the chunk's own offset in an SGPR.
+    ExV4i kq[kPasses];
+    ExV2u scl[kPasses];
+    auto issue = [&](int tc, bool with_k, bool with_v) {   // flags are compile-time at every call
+        const int nc = min(kChunk, len - tc);
+        const int32_t k_chunk = tc * kCodeBytes, v_chunk = static_cast<int32_t>(cap + tc) * kCodeBytes;
+        const int32_t s_chunk = static_cast<int32_t>(cap * 2 * kCodeBytes) + tc * kScaleBytes;
 #pragma unroll
         for (int ps = 0; ps < kPasses; ++ps) {
-            const int32_t tr = min(wave * 8 + r + 32 * ps, n - 1);
-            scl[ps] = __builtin_amdgcn_raw_buffer_load_b64(rsrc, tr * kScaleBytes + (c >> 1) * 8, s_chunk, 0);
-            kq[ps] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, tr * kCodeBytes + c * 16, k_chunk, 0);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rsrc, (__attribute__((address_space(3))) void*)&s_vc[wave * 8 + 32 * ps][0], 16,
-                tr * kCodeBytes + c * 16, v_chunk, 0, 0);
+            const int32_t tr = min(wave * 8 + r + 32 * ps, nc - 1);
+            if (with_k) {
+                scl[ps] = __builtin_amdgcn_raw_buffer_load_b64(rsrc, tr * kScaleBytes + (c >> 1) * 8, s_chunk, 0);
+                kq[ps] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, tr * kCodeBytes + c * 16, k_chunk, 0);
+            }
+            if (with_v)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    rsrc, (__attribute__((address_space(3))) void*)&s_vc[wave * 8 + 32 * ps][0], 16,
+                    tr * kCodeBytes + c * 16, v_chunk, 0, 0);
         }
+    };
+    // With SLICES = 4 (the smallest batches, where each chunk's load latency
+    // is exposed) the next chunk's K codes and scales are loaded while this
+    // chunk's coefficient and Y passes run; its V codes, which go to LDS,
+    // follow at the top of its own iteration (the barrier after the scores
+    // waits for every write into LDS, so they cannot be outstanding there).
+    constexpr bool kPrefetch = SLICES == 4;
+    if constexpr (kPrefetch) issue(0, true, false);
+    for (int t0 = 0; t0 < len; t0 += kChunk) {
+        const int n = min(kChunk, len - t0);
+        issue(t0, !kPrefetch, true);
+        // Scores of tokens [t0, t0+n).
 #pragma unroll
         for (int ps = 0; ps < kPasses; ++ps) {
             const int i = wave * 8 + r + 32 * ps;
@@ -405,6 +419,8 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
             if (c == 0 && i < n) s_tok[i] = static_cast<uint32_t>(score_of(p));
         }
         __builtin_amdgcn_s_waitcnt(0);   // the V codes are in LDS before the barrier
+        if constexpr (kPrefetch)
+            if (t0 + kChunk < len) issue(t0 + kChunk, true, false);
         __syncthreads();
 
         // Coefficient words, one token per thread: the exclusive prefix
