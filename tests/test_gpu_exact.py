@@ -135,6 +135,43 @@ def test_exact_matches_oracle_integer_recurrence(skv, ctx, lut4096, rope_tables,
     kv.close()
 
 
+@pytest.mark.parametrize("batch", [1, 3])   # four workgroups per head, and one
+def test_exact_every_token_a_new_maximum(skv, ctx, lut4096, rope_tables, batch):
+    """Keys that grow along the query's direction make most tokens a new
+    running maximum (578 of 700: INT8 quantization makes some neighbours tie,
+    and a tie is no new maximum), so each chunk's ordered part holds almost
+    all of it and takes the rescale branch token after token.  Query and keys
+    live on the slowest-rotating channel pairs (j = 60..63), so the rotation
+    cannot undo the growth."""
+    _note(f"case: exact, rising keys, batch {batch}, position 700")
+    cos, sin = rope_tables
+    p = 700
+    chans = np.array([h * 128 + c for h in range(H) for c in range(120, 128)])
+    kv = skv.KVCache(ctx, layers=1, max_batch=batch, max_seq_len=p + 1)
+    scs = []
+    for b in range(batch):
+        kh = np.zeros((p, 4096), np.float32)
+        kh[:, chans] = (0.25 * (1.0 + np.arange(p, dtype=np.float64) / 64.0))[:, None].astype(np.float32)
+        vh = f32_normal(8100 + b, (p, 4096))
+        prefill(skv, ctx, kv, lut4096, 0, b, kh, vh)
+        scs.append(oracle_sequence(cos, sin, kh, vh, p + 1))
+    q = np.zeros((batch, 4096), np.float32)
+    q[:, chans] = 1.0
+    k = np.zeros((batch, 4096), np.float32)
+    k[:, chans] = np.float32(0.25 * (1.0 + p / 64.0))
+    v = f32_normal(8200, (batch, 4096))
+    qq, kq, vq = O.f2q17(q), O.f2q17(k), O.f2q17(v)
+    out, aq, asc = exact_step(skv, ctx, kv, lut4096, 0, [p] * batch, qq, kq, vq, q17=True)
+    for b in range(batch):
+        res = scs[b].step_q17(qq[b], kq[b], vq[b], p, cos[p], sin[p], fp=False, integer=True)
+        ref = res["int"].reshape(4096)
+        diff = np.flatnonzero(out[b] != ref)
+        assert diff.size == 0, f"seq {b}: {diff.size} Q15.17 values differ (first {diff[:4]})"
+        q14, e8 = O.a14_q17(ref.reshape(128, 32))
+        assert (asc[b] == e8).all() and (aq[b] == O.pack_a14(q14)).all(), f"seq {b}: A14"
+    kv.close()
+
+
 def test_exact_batch_over_one_launch(skv, ctx, lut4096, rope_tables):
     """The exact entry over 260 sequences (two launches), against the oracle's
     integer recurrence on a sample of sequences from both launches."""
