@@ -29,6 +29,25 @@ def wide_values(seed: int, shape) -> np.ndarray:
     return np.where(zz % np.uint64(50) == 0, 20000.0 * sign, x).astype(np.float32)
 
 
+RISING_CHANNELS = np.array([h * 128 + c for h in range(H) for c in range(120, 128)])
+
+
+def rising_keys(tokens) -> np.ndarray:
+    """Keys on the slowest-rotating channel pairs (j = 60..63) of every head,
+    growing with the token index: against a query on the same channels
+    (rising_query) the scores rise, so most tokens set a new running maximum."""
+    t = np.asarray(tokens, dtype=np.float64)
+    k = np.zeros((t.size, 4096), np.float32)
+    k[:, RISING_CHANNELS] = (0.25 * (1.0 + t / 64.0))[:, None].astype(np.float32)
+    return k
+
+
+def rising_query(batch: int) -> np.ndarray:
+    q = np.zeros((batch, 4096), np.float32)
+    q[:, RISING_CHANNELS] = 1.0
+    return q
+
+
 def outlier_channels(seed: int, count: int = 41) -> np.ndarray:
     z = splitmix64(seed, 4 * count)
     return np.unique((z % np.uint64(4096)).astype(np.int64))[:count]
@@ -39,6 +58,8 @@ def history(seed: int, n: int, dist: str = "normal", outliers=None):
         k, v = student_t3(seed, (n, 4096)), student_t3(seed + 1, (n, 4096))
     elif dist == "wide":
         k, v = f32_normal(seed, (n, 4096)), wide_values(seed + 1, (n, 4096))
+    elif dist == "rising":
+        k, v = rising_keys(np.arange(n)), f32_normal(seed + 1, (n, 4096))
     else:
         k, v = f32_normal(seed, (n, 4096)), f32_normal(seed + 1, (n, 4096))
     if outliers is not None:

@@ -13,7 +13,8 @@ import numpy as np
 import pytest
 
 import oracle as O
-from gpu_cases import H, assert_rows_equal, history, oracle_sequence, outlier_channels, prefill
+from gpu_cases import (H, assert_rows_equal, history, oracle_sequence, outlier_channels, prefill, rising_keys,
+                       rising_query)
 from helpers import f32_normal, kat_vector
 
 pytestmark = pytest.mark.gpu
@@ -146,19 +147,13 @@ def test_exact_every_token_a_new_maximum(skv, ctx, lut4096, rope_tables, batch):
     _note(f"case: exact, rising keys, batch {batch}, position 700")
     cos, sin = rope_tables
     p = 700
-    chans = np.array([h * 128 + c for h in range(H) for c in range(120, 128)])
     kv = skv.KVCache(ctx, layers=1, max_batch=batch, max_seq_len=p + 1)
     scs = []
     for b in range(batch):
-        kh = np.zeros((p, 4096), np.float32)
-        kh[:, chans] = (0.25 * (1.0 + np.arange(p, dtype=np.float64) / 64.0))[:, None].astype(np.float32)
-        vh = f32_normal(8100 + b, (p, 4096))
+        kh, vh = history(8100 + 10 * b, p, "rising")
         prefill(skv, ctx, kv, lut4096, 0, b, kh, vh)
         scs.append(oracle_sequence(cos, sin, kh, vh, p + 1))
-    q = np.zeros((batch, 4096), np.float32)
-    q[:, chans] = 1.0
-    k = np.zeros((batch, 4096), np.float32)
-    k[:, chans] = np.float32(0.25 * (1.0 + p / 64.0))
+    q, k = rising_query(batch), rising_keys([p] * batch)
     v = f32_normal(8200, (batch, 4096))
     qq, kq, vq = O.f2q17(q), O.f2q17(k), O.f2q17(v)
     out, aq, asc = exact_step(skv, ctx, kv, lut4096, 0, [p] * batch, qq, kq, vq, q17=True)

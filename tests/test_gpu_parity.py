@@ -9,7 +9,7 @@ import pytest
 
 import oracle as O
 from gpu_cases import (H, assert_close, assert_rows_equal, history, oracle_sequence, outlier_channels,
-                       prefill, run_step)
+                       prefill, rising_keys, rising_query, run_step)
 from helpers import f32_normal, kat_vector
 
 pytestmark = pytest.mark.gpu
@@ -43,6 +43,8 @@ def _scenario(skv, ctx, lut, rope_tables, positions, seed, layers=1, layer=0, ca
     q = f32_normal(seed + 1000, (B, 4096))
     k = f32_normal(seed + 1001, (B, 4096))
     v = f32_normal(seed + 1002, (B, 4096))
+    if dist == "rising":
+        q, k = rising_query(B), rising_keys(positions)
     if outliers is not None:
         k[:, outliers] *= np.float32(20.0)
     if q17:
@@ -111,6 +113,14 @@ def test_randomized_configurations(skv, ctx, lut4096, rope_tables, case):
           f"outliers {outl is not None}, q17 {q17}")
     _scenario(skv, ctx, lut4096, rope_tables, positions, seed=9300 + 100 * case, layers=3, layer=layer,
               dist=dist, outliers=outl, split=split, q17=q17)
+
+
+@pytest.mark.parametrize("split", [0, 256])
+def test_rising_scores(skv, ctx, lut4096, rope_tables, split):
+    """Keys growing along the query: the running maximum moves at most
+    tokens, so the online softmax rescales in nearly every block and split."""
+    _note(f"case: rising scores, batch 2, positions 700/1300, split_tokens {split}")
+    _scenario(skv, ctx, lut4096, rope_tables, [700, 1300], seed=8300, dist="rising", split=split)
 
 
 def test_q17_entry(skv, ctx, lut4096, rope_tables):
