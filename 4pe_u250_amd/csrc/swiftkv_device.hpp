@@ -20,13 +20,13 @@ namespace dev {
 // half-even to an integer exactly, and v_cvt_i32_f32 clamps out-of-range
 // values to INT32_MIN/INT32_MAX.  Every |x| < 2^-18 rounds to 0 and every
 // |x| >= 2^14 clamps, so only NaN (which the conversion maps to 0) needs
-// its sign-saturated value put back.
+// its sign-saturated value: a NaN is replaced by the infinity of its sign
+// before the conversion.
 __device__ __forceinline__ int32_t f32_to_q17(float x) {
-    const float r = __builtin_rintf(x * 131072.0f);
+    const float inf = __uint_as_float((__float_as_uint(x) & 0x80000000u) | 0x7f800000u);
+    const float r = __builtin_isnan(x) ? inf : __builtin_rintf(x * 131072.0f);
     int32_t v;
     asm("v_cvt_i32_f32 %0, %1" : "=v"(v) : "v"(r));
-    const uint32_t b = __float_as_uint(x);
-    if ((b & 0x7fffffffu) > 0x7f800000u) v = (b >> 31) ? INT32_MIN : INT32_MAX;
     return v;
 }
 
