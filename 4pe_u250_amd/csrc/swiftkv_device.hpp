@@ -193,8 +193,7 @@ struct RowCodes {
     uint32_t sk, sv;           // G32 shifts of the lane's group
 };
 
-__device__ __forceinline__ RowCodes append_row_codes(int8_t* page, int seq_cap, int pos, int lane, int32_t k0,
-                                                     int32_t k1, int32_t v0, int32_t v1) {
+__device__ __forceinline__ RowCodes row_codes(int32_t k0, int32_t k1, int32_t v0, int32_t v1) {
     const uint32_t mk = row16_max(max(magnitude(k0), magnitude(k1)));
     const uint32_t mv = row16_max(max(magnitude(v0), magnitude(v1)));
     RowCodes rc;
@@ -204,6 +203,29 @@ __device__ __forceinline__ RowCodes append_row_codes(int8_t* page, int seq_cap, 
     rc.k1 = g32_code_byte(k1, rc.sk);
     rc.v0 = g32_code_byte(v0, rc.sv);
     rc.v1 = g32_code_byte(v1, rc.sv);
+    return rc;
+}
+
+// The row's stores through a buffer resource over the page: 32-bit lane
+// offsets, the row's offset in an SGPR.
+__device__ __forceinline__ void store_row(__amdgpu_buffer_rsrc_t page, int seq_cap, int pos, int lane,
+                                          const RowCodes& rc) {
+    __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(rc.k0 | (rc.k1 << 8)), page, lane * 2,
+                                          pos * kCodeBytes, 0);
+    __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(rc.v0 | (rc.v1 << 8)), page, lane * 2,
+                                          (seq_cap + pos) * kCodeBytes, 0);
+    if ((lane & 15) == 0) {
+        typedef float v2f_t __attribute__((ext_vector_type(2)));
+        const v2f_t sc = {shift_scale(rc.sk), shift_scale(rc.sv)};
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(__attribute__((ext_vector_type(2))) uint32_t, sc),
+                                              page, (lane >> 4) * 8, seq_cap * (2 * kCodeBytes) + pos * kScaleBytes,
+                                              0);
+    }
+}
+
+__device__ __forceinline__ RowCodes append_row_codes(int8_t* page, int seq_cap, int pos, int lane, int32_t k0,
+                                                     int32_t k1, int32_t v0, int32_t v1) {
+    const RowCodes rc = row_codes(k0, k1, v0, v1);
     const int64_t row = static_cast<int64_t>(pos) * kCodeBytes;
     reinterpret_cast<uint16_t*>(page + row)[lane] = static_cast<uint16_t>(rc.k0 | (rc.k1 << 8));
     reinterpret_cast<uint16_t*>(page + static_cast<int64_t>(seq_cap) * kCodeBytes + row)[lane] =

@@ -431,7 +431,8 @@ constexpr int kAppendTokens = 2;   // prefill rows per wave (their loads in flig
 // and store nothing.
 template <bool Q17>
 __global__ __launch_bounds__(256) void append_bulk_kernel(BulkArgs a) {
-    const int h = blockIdx.y * 4 + (threadIdx.x >> 6);
+    // wave-uniform through readfirstlane, so the page's buffer resource stays in SGPRs
+    const int h = blockIdx.y * 4 + __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int lane = threadIdx.x & 63;
     const int t0 = blockIdx.x * kAppendTokens;
     int2 cs[kAppendTokens], ki[kAppendTokens], vi[kAppendTokens];
@@ -443,13 +444,14 @@ __global__ __launch_bounds__(256) void append_bulk_kernel(BulkArgs a) {
         ki[j] = load_pair<Q17>(a.k, elem);
         vi[j] = load_pair<Q17>(a.v, elem);
     }
-    int8_t* page = page_ptr(a.kv, a.slot, a.layer, h);
+    const __amdgpu_buffer_rsrc_t page = __builtin_amdgcn_make_buffer_rsrc(
+        page_ptr(a.kv, a.slot, a.layer, h), static_cast<short>(0), static_cast<int32_t>(a.kv.page_bytes), kBufferWord3);
 #pragma unroll
     for (int j = 0; j < kAppendTokens; ++j) {
         if (t0 + j >= a.n) break;
         int32_t k0, k1;
         rope_pair(ki[j].x, ki[j].y, cs[j], k0, k1);
-        append_row(page, a.kv.seq_cap, a.pos0 + t0 + j, lane, k0, k1, vi[j].x, vi[j].y);
+        store_row(page, a.kv.seq_cap, a.pos0 + t0 + j, lane, row_codes(k0, k1, vi[j].x, vi[j].y));
     }
 }
 
