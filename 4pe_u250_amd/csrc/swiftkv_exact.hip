@@ -307,9 +307,9 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
     constexpr int kSeqLanes = kCh < 64 ? 64 : kCh;
     constexpr int kCompParts = (256 - kSeqLanes) / kCh;
     // The ordered part's share of a chunk: a composed token costs about 15
-    // operations against 12, so about 9/16 with one composed part and 3/16
-    // with six.
-    constexpr int kSeqShare16 = kCompParts == 1 ? 9 : 3;
+    // operations against 12, so about 9/16 with one composed part; with six,
+    // 2/16 measured best (the composed runs round up to whole batches).
+    constexpr int kSeqShare16 = kCompParts == 1 ? 9 : 2;
     const StepArgs& a = ea.step;
     const uint32_t row = a.rows[blockIdx.y];
     const int h = blockIdx.x / SLICES, slice = blockIdx.x % SLICES, b = static_cast<int>(row & 0xffu);
