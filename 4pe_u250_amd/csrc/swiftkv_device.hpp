@@ -9,6 +9,14 @@
 namespace swiftkv {
 namespace dev {
 
+// Vector register types of the buffer-load and -store builtins.
+typedef int32_t v4i __attribute__((ext_vector_type(4)));
+typedef int32_t v2i __attribute__((ext_vector_type(2)));
+typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+typedef float v2f __attribute__((ext_vector_type(2)));
+
+constexpr int32_t kBufferWord3 = 0x00020000;   // raw buffer resource, gfx9 data format
+
 // ---------------------------------------------------------------- numerics
 
 // FP32 -> Q15.17 with round-half-even and saturation.  The reference states
@@ -215,11 +223,9 @@ __device__ __forceinline__ void store_row(__amdgpu_buffer_rsrc_t page, int seq_c
     __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(rc.v0 | (rc.v1 << 8)), page, lane * 2,
                                           (seq_cap + pos) * kCodeBytes, 0);
     if ((lane & 15) == 0) {
-        typedef float v2f_t __attribute__((ext_vector_type(2)));
-        const v2f_t sc = {shift_scale(rc.sk), shift_scale(rc.sv)};
-        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(__attribute__((ext_vector_type(2))) uint32_t, sc),
-                                              page, (lane >> 4) * 8, seq_cap * (2 * kCodeBytes) + pos * kScaleBytes,
-                                              0);
+        const v2f sc = {shift_scale(rc.sk), shift_scale(rc.sv)};
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u, sc), page, (lane >> 4) * 8,
+                                              seq_cap * (2 * kCodeBytes) + pos * kScaleBytes, 0);
     }
 }
 

@@ -202,9 +202,6 @@ __device__ __forceinline__ int32_t value_step(int32_t y, uint32_t word, int32_t 
     return __builtin_elementwise_add_sat(y, term);
 }
 
-typedef int32_t ExV4i __attribute__((ext_vector_type(4)));
-typedef uint32_t ExV2u __attribute__((ext_vector_type(2)));
-constexpr int32_t kExBufferWord3 = 0x00020000;   // raw buffer, gfx9 data format
 
 // Sum over the 8 lanes of an aligned octet of a 64-bit integer (DPP moves of
 // both halves, integer adds, so exact in any order); every lane gets it.
@@ -321,7 +318,7 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
     int8_t* page = page_ptr(a.kv, a.slot0 + b, a.layer, h);
     const int64_t cap = a.kv.seq_cap;
     const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        page, static_cast<short>(0), static_cast<int32_t>(cap * kTokenBytes), kExBufferWord3);
+        page, static_cast<short>(0), static_cast<int32_t>(cap * kTokenBytes), kBufferWord3);
 
     __shared__ int32_t s_q[kHeadDim];
     // Per token of the chunk: the score, then (each thread rewrites its own
@@ -378,8 +375,8 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
     // end load its last token (inside the page) and are not used.  The page
     // is read through one buffer resource: per-lane 32-bit offsets within the
     // chunk, the chunk's own offset in an SGPR.
-    ExV4i kq[kPasses];
-    ExV2u scl[kPasses];
+    v4i kq[kPasses];
+    v2u scl[kPasses];
     auto issue = [&](int tc, bool with_k, bool with_v) {   // flags are compile-time at every call
         const int nc = min(kChunk, len - tc);
         const int32_t k_chunk = tc * kCodeBytes, v_chunk = static_cast<int32_t>(cap + tc) * kCodeBytes;

@@ -40,11 +40,6 @@ static_assert(kMaxSplits <= kHeadDim, "one merge thread per split statistic");
 // 1/sqrt(128) * log2(e) so the softmax uses v_exp_f32 (2^x) directly.
 constexpr float kScoreScale = (1.0f / 11.313708498984761f) * 1.4426950408889634f;
 
-// Native vector types: the nontemporal load builtin takes ext_vector pointers.
-typedef int32_t v4i __attribute__((ext_vector_type(4)));
-typedef float v2f __attribute__((ext_vector_type(2)));
-typedef int32_t v2i __attribute__((ext_vector_type(2)));
-
 // The cache is streamed exactly once per step, so every cache load is
 // nontemporal: it keeps the stream from displacing reusable lines in L2/MALL
 // (streaming reads reach ~88% of HBM peak this way versus ~78% with
@@ -90,7 +85,6 @@ struct PageReader {
     int32_t s_lane;       // lane's (K, V) scale pair of group c/2 in the scale plane
 };
 
-constexpr int32_t kBufferWord3 = 0x00020000;   // raw buffer, gfx9 data format
 constexpr int kNontemporal = 2;                // cache policy: nt
 
 __device__ __forceinline__ PageReader make_reader(const int8_t* page, int64_t cap, int c, int r) {
