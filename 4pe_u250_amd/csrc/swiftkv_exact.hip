@@ -186,14 +186,15 @@ __device__ __forceinline__ int32_t dequant_raw(int32_t code, uint32_t shift) {
     return static_cast<int32_t>(static_cast<uint32_t>(code) << shift);
 }
 
+// Both cases in one form: x = v >> min(shift, 17) is the code itself below
+// 17 and v >> 17 above, m = x c, and the rounding shift k = 17 - shift
+// clamps to 0 above 17, where the rounding terms (2^(16-shift) - 1 and a
+// zero-width bit field) vanish and the term is m.
 __device__ __forceinline__ int32_t value_term(int32_t code, uint32_t shift, uint32_t coef) {
-    const int32_t c = static_cast<int32_t>(coef);
-    const int32_t exact = __mul24(dequant_raw(code, shift) >> 17, c);
-    const int32_t m = __mul24(code, c);
-    const uint32_t k = (17u - shift) & 31u;
-    const int32_t bit = static_cast<int32_t>(__builtin_amdgcn_ubfe(static_cast<uint32_t>(m), 17u - shift, 1u));
-    const int32_t rounded = (m + static_cast<int32_t>(0xffffu >> shift) + bit) >> k;
-    return shift >= 17u ? exact : rounded;
+    const int32_t m = __mul24(dequant_raw(code, shift) >> min(shift, 17u), static_cast<int32_t>(coef));
+    const uint32_t k = __builtin_elementwise_sub_sat(17u, shift);
+    const int32_t bit = static_cast<int32_t>(__builtin_amdgcn_ubfe(static_cast<uint32_t>(m), k, min(k, 1u)));
+    return (m + static_cast<int32_t>(0xffffu >> shift) + bit) >> k;
 }
 
 __device__ __forceinline__ int32_t value_step(int32_t y, uint32_t word, int32_t code, uint32_t shift, int32_t term) {
