@@ -213,13 +213,16 @@ def test_exact_and_fast_path_agree(skv, ctx, lut4096, rope_tables):
     assert err.max() < 2e-3 * max(1.0, np.abs(out_f).max()), err.max()
 
 
-def test_host_io_mode_matches_device_mode(skv, ctx, lut4096):
+@pytest.mark.parametrize("positions", [
+    [5, 300, 64],
+    [int(p) for p in np.random.default_rng(37).integers(0, 301, 37)],
+])
+def test_host_io_mode_matches_device_mode(skv, ctx, lut4096, positions):
     """Host-memory I/O stages through the device and returns the same bits as
     the device-pointer call, for the FP32, Q15.17 and exact entries and the
     bulk append."""
-    _note("case: host-memory I/O vs device pointers, batch 3")
-    positions = [5, 300, 64]
     B = len(positions)
+    _note(f"case: host-memory I/O vs device pointers, batch {B}")
     kv = skv.KVCache(ctx, layers=1, max_batch=B, max_seq_len=301)
     kvh = skv.KVCache(ctx, layers=1, max_batch=B, max_seq_len=301)
     for b, p in enumerate(positions):
