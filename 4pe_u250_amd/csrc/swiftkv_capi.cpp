@@ -78,6 +78,11 @@ struct swiftkv_context {
     // split-context workspace
     float* partials = nullptr;
     size_t partial_elems = 0;
+    // Graphs record the workspace pointer in their kernel nodes, so a buffer
+    // the workspace outgrows while a graph of this context exists is kept
+    // here, and released when the last graph is destroyed.
+    int64_t graphs = 0;
+    std::vector<void*> retired;
     uint32_t* counters = nullptr;   // [kMaxBatchPerLaunch][32] split arrivals (kCounterStride apart), zero between launches
     // timing
     hipEvent_t timers[kTimerSlots] = {};
@@ -141,17 +146,32 @@ int not_capturing(const swiftkv_context* ctx, const char* what) {
     return SWIFTKV_OK;
 }
 
+// Releases the buffers retired while graphs existed (none may be left).
+int free_retired(swiftkv_context* ctx) {
+    if (ctx->retired.empty()) return SWIFTKV_OK;
+    SKV_HIP(hipStreamSynchronize(ctx->stream));
+    for (void* p : ctx->retired) SKV_HIP(hipFree(p));
+    ctx->retired.clear();
+    return SWIFTKV_OK;
+}
+
 // Device buffer growth.  The old buffer may still be read by queued kernels,
-// so the stream is drained before it is released.
+// so the stream is drained before it is released.  A buffer that recorded
+// graphs may reference (graph_visible) is retired instead while any graph of
+// the context exists: a replay after the growth still finds it allocated.
 template <typename T>
-int ensure(swiftkv_context* ctx, T*& ptr, size_t& have, size_t need) {
+int ensure(swiftkv_context* ctx, T*& ptr, size_t& have, size_t need, bool graph_visible) {
     if (need <= have) return SWIFTKV_OK;
     if (ctx->capturing)
         return fail(SWIFTKV_ESTATE, "split workspace too small during graph capture (%zu < %zu bytes): run the "
                     "call once before capturing", have * sizeof(T), need * sizeof(T));
     if (ptr) {
-        SKV_HIP(hipStreamSynchronize(ctx->stream));
-        SKV_HIP(hipFree(ptr));
+        if (graph_visible && ctx->graphs > 0) {
+            ctx->retired.push_back(ptr);
+        } else {
+            SKV_HIP(hipStreamSynchronize(ctx->stream));
+            SKV_HIP(hipFree(ptr));
+        }
         ptr = nullptr;
         have = 0;
     }
@@ -355,7 +375,7 @@ int run_step(swiftkv_context* ctx, const void* q, const void* k, const void* v, 
         const int32_t grid_splits = (max_pos + 1 + a.split_tokens - 1) / a.split_tokens;
         a.max_splits = grid_splits;
         if ((rc = ensure(ctx, ctx->partials, ctx->partial_elems,
-                         static_cast<size_t>(nb) * kHeads * grid_splits * kPartialStride)))
+                         static_cast<size_t>(nb) * kHeads * grid_splits * kPartialStride, true)))
             return rc;
         a.partials = ctx->partials;
         a.counters = ctx->counters;
@@ -443,7 +463,7 @@ int dispatch_step(swiftkv_context* ctx, bool exact, const void* q, const void* k
     const size_t off_k = align(in_bytes), off_v = 2 * align(in_bytes), off_out = 3 * align(in_bytes);
     const size_t off_aq = off_out + align(row_bytes);
     const size_t off_as = off_aq + align(aq_bytes), total = off_as + align(as_bytes);
-    if ((rc = ensure(ctx, ctx->io_stage, ctx->io_bytes, total))) return rc;
+    if ((rc = ensure(ctx, ctx->io_stage, ctx->io_bytes, total, false))) return rc;
     uint8_t* st = ctx->io_stage;
     SKV_HIP(hipMemcpyAsync(st, q, in_bytes, hipMemcpyHostToDevice, ctx->stream));
     SKV_HIP(hipMemcpyAsync(st + off_k, k, in_bytes, hipMemcpyHostToDevice, ctx->stream));
@@ -498,6 +518,7 @@ void free_context(swiftkv_context* ctx) {
     (void)hipSetDevice(ctx->device);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     if (ctx->partials) (void)hipFree(ctx->partials);
+    for (void* p : ctx->retired) (void)hipFree(p);
     if (ctx->counters) (void)hipFree(ctx->counters);
     if (ctx->io_stage) (void)hipFree(ctx->io_stage);
     for (auto& t : ctx->timers)
@@ -870,7 +891,7 @@ int swiftkv_append_tokens(swiftkv_context* ctx, const void* k, const void* v, in
     const size_t rows_bytes = static_cast<size_t>(n) * kModelDim * 4;
     if (ctx->host_io) {   // stage the host rows (see dispatch_step)
         const size_t half = (rows_bytes + 255) & ~static_cast<size_t>(255);
-        if ((rc = ensure(ctx, ctx->io_stage, ctx->io_bytes, 2 * half))) return rc;
+        if ((rc = ensure(ctx, ctx->io_stage, ctx->io_bytes, 2 * half, false))) return rc;
         SKV_HIP(hipMemcpyAsync(ctx->io_stage, k, rows_bytes, hipMemcpyHostToDevice, ctx->stream));
         SKV_HIP(hipMemcpyAsync(ctx->io_stage + half, v, rows_bytes, hipMemcpyHostToDevice, ctx->stream));
         k = ctx->io_stage;
@@ -1092,6 +1113,7 @@ int swiftkv_capture_end(swiftkv_context* ctx, swiftkv_graph** out) {
     g->graph = graph;
     g->exec = exec;
     ++ctx->children;
+    ++ctx->graphs;
     *out = g;
     return ok();
 }
@@ -1115,8 +1137,10 @@ int swiftkv_graph_destroy(swiftkv_graph* graph) {
     if (graph->exec) (void)hipGraphExecDestroy(graph->exec);
     if (graph->graph) (void)hipGraphDestroy(graph->graph);
     delete graph;
+    int rc = SWIFTKV_OK;
+    if (--ctx->graphs == 0) rc = free_retired(ctx);
     release_child(ctx);
-    return ok();
+    return rc ? rc : ok();
 }
 
 // ---------------------------------------------------------------- timing

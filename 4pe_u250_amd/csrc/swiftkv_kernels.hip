@@ -183,8 +183,8 @@ __device__ __forceinline__ void scan_range(const PageReader& pr, BlockLoads& bl,
 
 // Per-(sequence, head) output: FP32 row and, when requested, A14/G32 + E8M0
 // (swiftkv_attention.cpp:1715-1771, 2656-2682): per 32 outputs, e = frexp
-// exponent of max|o|, q = trunc(clamp(o*2^(13-e) +- 0.5, +-8191)), code =
-// e + 127 (0 for an all-zero group).  Called by every thread of the block;
+// exponent of max|o| clamped at -127, q = trunc(clamp(o*2^(13-e) +- 0.5,
+// +-8191)), code = e + 127 (0 for an all-zero group).  Called by every thread of the block;
 // threads d < 128 supply output channel d.
 __device__ __forceinline__ void finalize_head(const StepArgs& a, int b, int h, float o) {
     const int d = threadIdx.x;
@@ -197,10 +197,14 @@ __device__ __forceinline__ void finalize_head(const StepArgs& a, int b, int h, f
     int16_t q14 = 0;
     uint8_t code = 0;
     if (mx_abs != 0.0f) {
+        // The reference clamps the group exponent at -127 (swiftkv_attention.cpp:1722-1724).
+        // o * 2^(13-e) is formed with ldexpf: it equals the product with the
+        // power of two wherever that power is a finite float, and stays finite
+        // for a group max below 2^-115, where 2^(13-e) would overflow to inf.
         int e = 0;
         (void)frexpf(mx_abs, &e);
-        const float inv = ldexpf(1.0f, 13 - e);
-        const float sc = __fmul_rn(o, inv);
+        e = max(e, -127);
+        const float sc = ldexpf(o, 13 - e);
         float rr = sc >= 0.0f ? __fadd_rn(sc, 0.5f) : __fsub_rn(sc, 0.5f);
         rr = fminf(fmaxf(rr, -8191.0f), 8191.0f);
         q14 = static_cast<int16_t>(static_cast<int>(rr));

@@ -292,8 +292,10 @@ int swiftkv_a14_decode(const uint8_t* words, const uint8_t* e8m0, size_t groups,
  * calls of a decode step.  The recording keeps every argument, including the
  * positions, so a replay repeats exactly the recorded work.  Run each
  * recorded call once outside capture first: the split workspace must already
- * be large enough.  While capturing, calls that synchronize, copy, allocate
- * or memset return SWIFTKV_ESTATE.
+ * be large enough.  Eager calls after a capture may still grow the workspace:
+ * the buffer a graph was recorded with stays allocated until the last graph
+ * of the context is destroyed, so replays remain valid.  While capturing,
+ * calls that synchronize, copy, allocate or memset return SWIFTKV_ESTATE.
  * ------------------------------------------------------------------------ */
 int swiftkv_capture_begin(swiftkv_context* ctx);
 int swiftkv_capture_end(swiftkv_context* ctx, swiftkv_graph** out);

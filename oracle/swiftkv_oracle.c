@@ -407,7 +407,8 @@ void oracle_attend_head_int(const int32_t* q, const int8_t* kc, const uint8_t* k
 /* ------------------------------------------------------------------------ */
 /* A14 / E8M0 epilogue (cpp:1715-1771, 2656-2682; emulator:690-711).          */
 /* Values are float; int path passes raw*2^-17.  Per 32 values:               */
-/* e = frexp exponent of max|x|; q = trunc(clamp(x*2^(13-e) +- 0.5, +-8191)); */
+/* e = frexp exponent of max|x|, at least -127;                               */
+/* q = trunc(clamp(x*2^(13-e) +- 0.5, +-8191));                               */
 /* code = e + 127, or 0 when the group is all zero.                           */
 /* ------------------------------------------------------------------------ */
 void oracle_a14_group(const float* x, int16_t* q14, uint8_t* code) {
@@ -423,10 +424,12 @@ void oracle_a14_group(const float* x, int16_t* q14, uint8_t* code) {
     }
     int e;
     frexpf(mx, &e);
-    if (e < -127) e = -127;
-    float inv = ldexpf(1.0f, 13 - e);
+    if (e < -127) e = -127; /* cpp:1722-1724 */
     for (int i = 0; i < G32; ++i) {
-        volatile float r = x[i] * inv;
+        /* x * 2^(13-e) as ldexpf: the same value as the product with the
+         * power of two wherever that power is finite, and finite for a group
+         * max below 2^-115, where 2^(13-e) itself overflows. */
+        volatile float r = ldexpf(x[i], 13 - e);
         volatile float rr = r >= 0.0f ? r + 0.5f : r - 0.5f;
         float c = rr;
         if (c > 8191.0f) c = 8191.0f;

@@ -69,13 +69,25 @@ def test_null_and_range_checks_without_device(skv):
     assert L.swiftkv_rope_lut_destroy(None) == skv.OK
 
 
-def test_no_device_is_a_hip_error(skv):
-    import torch  # noqa: F401  (only to know whether a device is visible)
-    if torch.cuda.is_available():
-        pytest.skip("a device is visible")
-    with pytest.raises(skv.SwiftKVError) as ei:
-        skv.Context(0)
-    assert ei.value.code == skv.EHIP
+def test_context_create_reports_the_device_state(skv):
+    """The library itself says whether a device is there: with none visible,
+    swiftkv_context_create fails with SWIFTKV_EHIP and a HIP message; with one,
+    it succeeds for device 0 and refuses an index past the last device with
+    SWIFTKV_ERANGE.  Either way no handle is returned on failure."""
+    L = skv.lib()
+    h = C.c_void_p(1)
+    rc = L.swiftkv_context_create(0, C.byref(h))
+    if rc == skv.OK:
+        assert h.value
+        assert L.swiftkv_context_destroy(h) == skv.OK
+        h2 = C.c_void_p(1)
+        assert L.swiftkv_context_create(4096, C.byref(h2)) == skv.ERANGE
+        assert h2.value is None
+        assert b"device 4096" in L.swiftkv_last_error()
+    else:
+        assert rc == skv.EHIP
+        assert h.value is None
+        assert b"hip" in L.swiftkv_last_error().lower()
 
 
 def test_unpack_a14_roundtrip(skv, oracle):

@@ -147,6 +147,42 @@ def test_student_t_beyond_reference_limit(skv, ctx, rope_tables):
     lut.close()
 
 
+def test_a14_epilogue_small_group_maximum(skv, ctx, lut4096, rope_tables):
+    """A group whose largest output is near 2^-120: 2^(13-e) is not a finite
+    float there, so the epilogue must scale the output itself.  Token 0's key
+    dominates the query by about 120 in log2 units and carries zero V in
+    channels 0-31; the new token carries V = 1 there, so those outputs are
+    its tiny weight.  A14/E8M0 bit-exact against the oracle's rule on the
+    GPU's output, and the decoded group within half a step of it."""
+    _note("case: A14 group maximum near 2^-120 (batch 1, position 1)")
+    cos, sin = rope_tables
+    a = np.float32(21.69)
+    k0, v0 = np.zeros((1, 4096), np.float32), np.zeros((1, 4096), np.float32)
+    q, k1, v1 = (np.zeros((1, 4096), np.float32) for _ in range(3))
+    for h in range(H):
+        k0[0, h * 128 + 126:h * 128 + 128] = a
+        v0[0, h * 128 + 32:h * 128 + 128] = 1.0
+        q[0, h * 128 + 126:h * 128 + 128] = a
+        v1[0, h * 128:h * 128 + 32] = 1.0
+        v1[0, h * 128 + 32:h * 128 + 128] = 0.5
+    kv = skv.KVCache(ctx, layers=1, max_batch=1, max_seq_len=64)
+    prefill(skv, ctx, kv, lut4096, 0, 0, k0, v0)
+    sc = oracle_sequence(cos, sin, k0, v0, 2)
+    out, aq, asc = run_step(skv, ctx, kv, lut4096, 0, [1], q, k1, v1)
+    res = sc.step_q17(O.f2q17(q[0]), O.f2q17(k1[0]), O.f2q17(v1[0]), 1, cos[1], sin[1], fp=True)
+    assert_rows_equal(kv, sc, 0, 0, 0, 2)
+    assert_close(out[0].reshape(H, 128), res["fp"], "small group")
+    o = out[0].reshape(128, 32)
+    tiny = o[0::4]                                   # group 0 of every head
+    assert (tiny > 0).all() and (np.abs(tiny).max(axis=1) < 2.0 ** -115).all(), "the case must reach 2^-115"
+    q14, e8 = O.a14(o)
+    assert (asc[0] == e8).all() and (aq[0] == O.pack_a14(q14)).all()
+    assert (e8[0::4] < 127 - 114).all()
+    step = np.ldexp(1.0, e8[0::4].astype(np.int64) - 140)[:, None]
+    assert (np.abs(q14[0::4] * step - tiny) <= 0.51 * step).all()
+    kv.close()
+
+
 def test_kat_inputs_through_q17_entry(skv, ctx, lut4096, rope_tables):
     """The reference KAT sequence (positions 0 then 1 on one cache, PE0 heads
     0..7 from tb_attention_pe0_kv_rtl.cpp:79-101) through the GPU path."""
@@ -370,6 +406,57 @@ def test_graph_replay_matches_eager(skv, ctx, lut4096, rope_tables):
     for b in qkv + outs + aqs + ass + [other]:
         b.free()
     kv.close()
+
+
+def test_graph_replay_after_the_workspace_grows(skv, ctx, lut4096):
+    """A graph records the split workspace's address.  An eager call that
+    needs a larger workspace after the capture must leave the recorded buffer
+    allocated: replays before and after the growth equal the eager result bit
+    for bit, and destroying the graph afterwards releases the old buffer."""
+    _note("case: graph of a batch-1 8-split step, then an eager 16 x 4-split step grows the workspace")
+    fresh = skv.Context(0)
+    lut = skv.RopeLut.generate(fresh, 4096)
+    kv = skv.KVCache(fresh, layers=1, max_batch=16, max_seq_len=4096)
+    kv.fill_synthetic(lut, ntok=4095, seed=77)
+    qkv = [fresh.alloc(16 * 4096 * 4) for _ in range(3)]
+    for i, b in enumerate(qkv):
+        fresh.fill_synthetic(b, 16 * 4096, 78, 10 + i)
+    out, big_out = fresh.alloc(4096 * 4), fresh.alloc(16 * 4096 * 4)
+    aq, asc = fresh.alloc(128 * 56), fresh.alloc(128)
+
+    def small_step():
+        skv.swiftkv_attention(fresh, qkv[0], qkv[1], qkv[2], kv, lut, aq, asc, 0, [4095], out)
+
+    def snapshot():
+        fresh.synchronize()
+        return [out.download(np.float32, (4096,)), aq.download(np.uint8, (128, 56)), asc.download(np.uint8, (128,))]
+
+    small_step()                       # sizes the workspace for 32 heads x 8 splits
+    eager = snapshot()
+    fresh.capture_begin()
+    small_step()
+    g = fresh.capture_end()
+    g.launch()
+    assert all(np.array_equal(x, y) for x, y in zip(eager, snapshot())), "replay before the growth"
+    # 16 sequences x 32 heads x 4 splits: 8x the recorded workspace
+    fresh.set_split_tokens(1024)
+    skv.swiftkv_attention(fresh, qkv[0], qkv[1], qkv[2], kv, lut, None, None, 0, np.full(16, 4095, np.int32),
+                          big_out)
+    fresh.set_split_tokens(0)
+    fresh.synchronize()
+    for rep in range(3):
+        out.zero()
+        g.launch()
+        got = snapshot()
+        assert all(np.array_equal(x, y) for x, y in zip(eager, got)), f"replay {rep} after the growth"
+    g.close()
+    small_step()                       # the grown workspace serves the eager call
+    assert all(np.array_equal(x, y) for x, y in zip(eager, snapshot()))
+    for b in qkv + [out, big_out, aq, asc]:
+        b.free()
+    kv.close()
+    lut.close()
+    fresh.close()
 
 
 def test_objects_may_outlive_their_context(skv):

@@ -373,21 +373,55 @@ def test_fp_and_integer_paths_agree(oracle, rope_tables):
 
 
 # ----------------------------------------------------------------- A14 epilogue
-def test_a14_group_rule_and_packing(oracle, skv):
+def test_a14_float_rule_equals_the_integer_rule_on_q17_values(oracle):
+    """The float A14 rule (applied to the FP32 path's output) and the integer
+    path's rule (pinned by the reference KAT hashes, the emulator decode
+    goldens and the reference build) must agree on every value the integer
+    path can produce, raw * 2^-17: same lanes, same E8M0 code.  Spans from
+    2^1 to 2^31 raw cover group exponents -15 to 15."""
     rng = np.random.default_rng(8)
-    x = (rng.standard_normal((16, 32)) * np.logspace(-3, 2, 16)[:, None]).astype(np.float32)
-    x[3] = 0.0
-    q, e = oracle.a14(x)
-    assert e[3] == 0 and (q[3] == 0).all()
-    for r in range(16):
-        if r == 3:
-            continue
-        ex = np.frexp(np.abs(x[r]).max())[1]
-        assert e[r] == ex + 127
-        expect = np.trunc(np.clip(x[r].astype(np.float32) * np.float32(2.0 ** (13 - ex)) +
-                                  np.where(x[r] >= 0, 0.5, -0.5).astype(np.float32), -8191, 8191))
-        assert (q[r] == expect.astype(np.int16)).all()
-        assert np.abs(q[r]).max() >= 4096    # max element lands in the top octave
+    for span in range(1, 32):
+        raw = rng.integers(-(1 << span) + 1, 1 << span, (64, 32), dtype=np.int64).astype(np.int32)
+        raw[0] = 0
+        raw[1, 5] = (1 << span) - 1
+        raw[2, :] = np.where(np.arange(32) % 2, 1, -1) << (span - 1)   # ties at the top octave
+        x = (raw.astype(np.float32) * np.float32(2.0 ** -17))
+        qf, ef = oracle.a14(x)
+        qi, ei = oracle.a14_q17(raw)
+        assert (qf == qi).all() and (ef == ei).all(), f"span 2^{span}"
+        assert ef[0] == 0 and (qf[0] == 0).all()
+
+
+def test_a14_scale_invariance_down_to_the_exponent_floor(oracle):
+    """Scaling a group by 2^-k leaves its lanes unchanged and lowers its code
+    by k while the group exponent stays >= -127 (the reference's floor,
+    swiftkv_attention.cpp:1722-1724).  Below the floor the code stays 0 and
+    the lanes still decode, lane * 2^-140, to within half a step of the
+    value: the scaling must stay finite where 2^(13-e) overflows (e < -114)."""
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((8, 32)).astype(np.float32)
+    x[1, 3] = 0.0
+    q0, e0 = oracle.a14(x)
+    top = np.frexp(np.abs(x).max(axis=1))[1]
+    assert (e0 == top + 127).all()
+    assert (np.abs(q0).max(axis=1) >= 4096).all()     # the largest lane lands in the top octave
+    for k in range(1, 150):
+        xs = np.ldexp(x, -k).astype(np.float32)
+        q, e = oracle.a14(xs)
+        for r in range(8):
+            if top[r] - k >= -100:           # every lane still a normal float: exact invariance
+                assert e[r] == e0[r] - k and (q[r] == q0[r]).all(), (k, r)
+            elif top[r] - k >= -127:         # small lanes become subnormal and lose low bits
+                assert e[r] == e0[r] - k and (np.abs(q[r].astype(int) - q0[r]) <= 1).all(), (k, r)
+            else:
+                assert e[r] == 0
+                step = 2.0 ** -140
+                assert (np.abs(q[r] * step - xs[r].astype(np.float64)) <= 0.5 * step + 2.0 ** -151).all(), (k, r)
+
+
+def test_a14_packing(oracle, skv):
+    rng = np.random.default_rng(10)
+    q = rng.integers(-8191, 8192, (16, 32)).astype(np.int16)
     words = oracle.pack_a14(q)
     assert (skv.unpack_a14(words) == q).all()
 
