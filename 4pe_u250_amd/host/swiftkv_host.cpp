@@ -20,6 +20,7 @@
 //   swiftkv_host --decode --batch 16 --context 32257 --steps 512 --layers 1 --t3
 //   swiftkv_host --exact --batch 4 --context 1024 --rope-lut rope_lut.bin
 //   swiftkv_host --batch 64 --parts 4
+//   swiftkv_host --batch 3 --layers 2 --context 700 --steps 2 --dump /tmp/run
 #include "swiftkv.h"
 
 #include <algorithm>
@@ -92,6 +93,14 @@ std::vector<std::uint8_t> read_file_checked(const std::string& path, std::size_t
     return data;
 }
 
+// Writes `bytes` bytes to `path`, replacing the file.
+void write_file(const std::string& path, const void* data, std::size_t bytes) {
+    std::ofstream out(path, std::ios::binary | std::ios::trunc);
+    if (!out) throw std::runtime_error("cannot create " + path);
+    out.write(static_cast<const char*>(data), static_cast<std::streamsize>(bytes));
+    if (!out) throw std::runtime_error("short write to " + path);
+}
+
 // Algorithmic HBM bytes of one (sequence, layer) step at `position`: every
 // cached token-head read once, the new row written, FP32 q/k/v in (each as
 // `parts` partial rows) and the output out.
@@ -120,6 +129,7 @@ struct Config {
     bool host_io = false;     // host-memory q/k/v and outputs
     bool t3 = false;          // Student-t(3) data instead of N(0,1)
     bool outliers = false;    // 1% of K channels x20
+    std::string dump;         // directory for the last call's outputs and the appended rows
 };
 
 void print_usage(const char* program) {
@@ -144,6 +154,9 @@ void print_usage(const char* program) {
         << "  --host-io        inputs and outputs in host memory (PCIe included)\n"
         << "  --t3             Student-t(3) data, unit variance\n"
         << "  --outliers       1% of K channels scaled x20\n"
+        << "  --dump DIR       write the last layer's outputs of the last step (output.bin, activation_q.bin,\n"
+        << "                   activation_scale.bin), the rows appended by that step for every sequence,\n"
+        << "                   layer and head as reference records (appended.bin) and meta.json into DIR\n"
         << "  --help           this text\n";
 }
 
@@ -211,6 +224,10 @@ Config parse_args(int argc, char** argv, bool* help) {
             c.t3 = true;
         } else if (a == "--outliers") {
             c.outliers = true;
+        } else if (a == "--dump") {
+            const char* v = value();
+            if (v == nullptr || *v == '\0') throw std::runtime_error("--dump needs a directory");
+            c.dump = v;
         } else {
             throw std::runtime_error("unknown option " + a + " (try --help)");
         }
@@ -436,6 +453,51 @@ int run(const Config& cfg) {
         max_abs = std::max(max_abs, std::fabs(x));
     }
     if (max_abs == 0.0) throw std::runtime_error("attention output is all zero");
+
+    if (!cfg.dump.empty()) {
+        // The outputs of the last call (the last layer of the last step) and
+        // the row that step appended for every (sequence, layer, head), in the
+        // reference's 320-byte record format, for an offline comparison with
+        // an independent model of the stage.
+        const int p_last = cfg.decode ? p0 + cfg.steps - 1 : p0;
+        std::vector<std::uint8_t> aq_bytes(static_cast<std::size_t>(cfg.batch) * kGroupsPerSequence *
+                                           SWIFTKV_A14_WORD_BYTES),
+            as_bytes(static_cast<std::size_t>(cfg.batch) * kGroupsPerSequence);
+        if (cfg.host_io) {
+            aq_bytes = host_aq;
+            as_bytes = host_as;
+        } else {
+            check(swiftkv_memcpy_d2h(ctx.p, aq_bytes.data(), act_q.p, aq_bytes.size()), "swiftkv_memcpy_d2h");
+            check(swiftkv_memcpy_d2h(ctx.p, as_bytes.data(), act_scale.p, as_bytes.size()), "swiftkv_memcpy_d2h");
+        }
+        std::vector<std::uint8_t> records(static_cast<std::size_t>(cfg.batch) * cfg.layers * SWIFTKV_HEADS *
+                                          SWIFTKV_RECORD_BYTES);
+        for (int b = 0; b < cfg.batch; ++b)
+            for (int layer = 0; layer < cfg.layers; ++layer)
+                for (int h = 0; h < SWIFTKV_HEADS; ++h) {
+                    const std::size_t idx = (static_cast<std::size_t>(b) * cfg.layers + layer) * SWIFTKV_HEADS + h;
+                    check(swiftkv_kv_cache_export_records(ctx.p, kv.p, b, layer, h, p_last, 1,
+                                                          records.data() + idx * SWIFTKV_RECORD_BYTES),
+                          "swiftkv_kv_cache_export_records");
+                }
+        write_file(cfg.dump + "/output.bin", last.data(), last.size());
+        write_file(cfg.dump + "/activation_q.bin", aq_bytes.data(), aq_bytes.size());
+        write_file(cfg.dump + "/activation_scale.bin", as_bytes.data(), as_bytes.size());
+        write_file(cfg.dump + "/appended.bin", records.data(), records.size());
+        std::ostringstream meta;
+        meta << "{\"batch\": " << cfg.batch << ", \"layers\": " << cfg.layers << ", \"layer\": " << cfg.layers - 1
+             << ", \"first_position\": " << p0 << ", \"position\": " << p_last << ", \"steps\": " << cfg.steps
+             << ", \"decode\": " << (cfg.decode ? "true" : "false") << ", \"seed\": " << cfg.seed
+             << ", \"input_seed\": " << cfg.seed + 1 << ", \"input_streams\": [1000, 1001, 1002]"
+             << ", \"distribution\": " << dist << ", \"outliers\": " << (cfg.outliers ? "true" : "false")
+             << ", \"parts\": " << cfg.parts << ", \"q17\": " << (cfg.q17 ? "true" : "false")
+             << ", \"exact\": " << (cfg.exact ? "true" : "false")
+             << ", \"input_layout\": \"[part][layer][batch][4096] FP32\""
+             << ", \"output\": \"" << (cfg.exact ? "int32 Q15.17" : "float32") << " [batch][4096]\""
+             << ", \"appended\": \"records [batch][layer][head][320] of token position\"}\n";
+        const std::string text = meta.str();
+        write_file(cfg.dump + "/meta.json", text.data(), text.size());
+    }
 
     // With host I/O the calls are synchronous, so the wall clock is the time.
     const double ms = cfg.host_io ? wall_ms : static_cast<double>(device_ms);

@@ -44,6 +44,10 @@ REPO = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, REPO)
 
 HBM_PEAK_GBPS = 8000.0
+# Timer slots of the per-step event pairs (the library holds 64 slots; bench
+# uses 0..9 for its regions).
+STEP_SLOT0, STEP_SLOTS = 16, 48
+MIN_STEP_SAMPLES = 20
 METRIC = "decode-attn µs/layer + achieved HBM GB/s (% of peak), ctx 4096, batch 1/64"
 TOKEN_HEAD_BYTES = 288
 
@@ -58,17 +62,38 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def profiled_traffic(batch: int, context: int):
-    """HBM bytes per step-kernel launch measured by rocprofv3 FETCH_SIZE and
-    WRITE_SIZE (each scaled by the copy-kernel calibration) for this workload,
-    from the committed summary; None when no summary covers it."""
+PROFILE_KEYS = ("traffic_bytes_per_launch", "algorithmic_bytes_per_launch", "trace_avg_us", "fetch_ratio",
+                "lds_bank_conflict_cycles_per_launch", "lds_instructions_per_launch", "achieved_waves_per_simd",
+                "achieved_occupancy_frac", "vgprs", "bench_ms_per_step", "commit")
+
+
+def profile_summary(batch: int, context: int):
+    """The committed rocprofv3 summary of the step kernel on this workload:
+    HBM bytes per launch (FETCH_SIZE and WRITE_SIZE, each scaled by the
+    copy-kernel calibration), their ratio to the algorithmic bytes, LDS bank
+    conflicts, achieved occupancy, and the commit and bench ms/step of the run
+    it came from.  ({}, None) when no summary covers the workload."""
     path = os.path.join(REPO, "profiles", f"step_kernel_batch{batch}_ctx{context}.md")
     if not os.path.exists(path):
-        return None, None
+        return {}, None
+    vals = {}
     for line in open(path):
-        if line.startswith("traffic_bytes_per_launch:"):
-            return int(float(line.split(":", 1)[1])), os.path.relpath(path, REPO)
-    return None, None
+        key, sep, rest = line.partition(":")
+        if sep and key.strip() in PROFILE_KEYS:
+            text = rest.strip()
+            try:
+                vals[key.strip()] = float(text) if "." in text or "e" in text else int(text)
+            except ValueError:
+                vals[key.strip()] = text
+    return vals, os.path.relpath(path, REPO)
+
+
+def profile_counters(vals):
+    """The counter evidence carried in a bench line's roofline."""
+    keys = ("fetch_ratio", "lds_bank_conflict_cycles_per_launch", "lds_instructions_per_launch",
+            "achieved_waves_per_simd", "achieved_occupancy_frac", "vgprs", "trace_avg_us", "commit",
+            "bench_ms_per_step")
+    return {k: vals[k] for k in keys if k in vals} or None
 
 
 def run_gpu(skv, ctx, positions, layers, steps, warmup, seed, outliers=False, dist=0, exact_steps=0,
@@ -114,6 +139,16 @@ def run_gpu(skv, ctx, positions, layers, steps, warmup, seed, outliers=False, di
         one_step(positions + s if advance else positions)
     ctx.timer_record(1)
     ms = ctx.timer_elapsed_ms(0, 1)
+    # The same steps again, each one bracketed by events (slot i before step
+    # i, all on the stream, no host wait between steps): the median step.
+    samples = []
+    if not advance:
+        n_each = max(MIN_STEP_SAMPLES, min(steps, STEP_SLOTS - 1))
+        for s in range(n_each):
+            ctx.timer_record(STEP_SLOT0 + s)
+            one_step(positions)
+        ctx.timer_record(STEP_SLOT0 + n_each)
+        samples = [ctx.timer_elapsed_ms(STEP_SLOT0 + s, STEP_SLOT0 + s + 1) for s in range(n_each)]
     # The same steps again with an event pair around every launch, for the
     # step kernel's average duration (the roofline).  The event records add
     # small gaps on the stream, so `value` comes from the pass above.
@@ -199,6 +234,8 @@ def run_gpu(skv, ctx, positions, layers, steps, warmup, seed, outliers=False, di
     ms_step = ms / steps
     res = {
         "ms_per_step": ms_step,
+        "ms_per_step_median": float(np.median(samples)) if samples else None,
+        "step_samples": len(samples),
         "us_per_layer": 1000.0 * ms_step / layers,
         "gbps": total_bytes / (ms / 1e3) / 1e9,
         "tokens_per_s": batch * steps / (ms / 1e3),
@@ -297,6 +334,9 @@ def summary(res, graph=True):
          "pct_of_peak": round(res["pct_of_peak"], 2), "tokens_per_s": round(res["tokens_per_s"], 1),
          "step_kernel_avg_us": round(res["step_avg_us"], 2),
          "step_kernel_gbps": round(res["step_kernel_gbps"], 1)}
+    if res.get("ms_per_step_median"):
+        layers = res["ms_per_step"] / res["us_per_layer"] * 1000.0
+        d["us_per_layer_median_step"] = round(1000.0 * res["ms_per_step_median"] / layers, 3)
     if graph and "graph" in res:
         d["graph_replay"] = {k: round(v, 3) for k, v in res["graph"].items()}
     return d
@@ -541,7 +581,8 @@ def main():
                     f"sequence-step")
 
     att = main_res["step_avg_us"]
-    traffic, traffic_src = profiled_traffic(args.batch, args.context)
+    prof, traffic_src = profile_summary(args.batch, args.context)
+    traffic = prof.get("traffic_bytes_per_launch")
     line = {
         "metric": METRIC,
         "value": round(main_res["gbps"], 1),
@@ -550,6 +591,10 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(main_res["ms_per_step"], 4),
+        "ms_per_step_median": round(main_res["ms_per_step_median"], 4),
+        "step_timing": (f"ms_per_step: hipEvents around the {args.steps} timed steps / {args.steps}; "
+                        f"ms_per_step_median: median of {main_res['step_samples']} further steps, each between "
+                        "its own pair of events on the stream"),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -560,6 +605,7 @@ def main():
                    "batch": args.batch, "context": args.context, "layers": args.layers, "heads": 32,
                    "head_dim": 128, "kv_dtype": "int8+fp32 G32 scales"},
         "us_per_layer": round(main_res["us_per_layer"], 2),
+        "us_per_layer_median_step": round(1000.0 * main_res["ms_per_step_median"] / args.layers, 2),
         "tokens_per_s": round(main_res["tokens_per_s"], 1),
         "pct_of_peak": round(main_res["pct_of_peak"], 2),
         "kernel_avg_us_event_pairs": {k: (round(v, 2) if v else v) for k, v in main_res["kernel_avg_us"].items()},
@@ -572,7 +618,8 @@ def main():
                      "avg_launch_us": round(att, 2),
                      "launches": main_res["step_launches"],
                      "timing": "hipEvents around the timed region on the context stream / step-kernel launches in "
-                               "it (the only kernel there)"},
+                               "it (the only kernel there)",
+                     "profile_counters": profile_counters(prof)},
         "cpu_baseline": cpu,
     }
     if not args.no_cpu:
@@ -596,13 +643,15 @@ def main():
             line["batch1"]["split_k_partials_input"] = {"parts": b1["partials"]["parts"],
                                                         "us_per_layer": round(b1["partials"]["us_per_layer"], 3),
                                                         "gbps": round(b1["partials"]["gbps"], 1)}
-        t1, t1_src = profiled_traffic(1, args.context)
+        prof1, t1_src = profile_summary(1, args.context)
+        line["batch1"]["us_per_layer_median_step"] = round(1000.0 * b1["ms_per_step_median"] / args.layers, 3)
         line["batch1"]["roofline"] = {"bound": "hbm (latency-bound at this size)",
                                       "achieved": round(b1["step_kernel_gbps"], 1), "peak": HBM_PEAK_GBPS,
                                       "unit": "GB/s", "frac": round(b1["step_kernel_gbps"] / HBM_PEAK_GBPS, 4),
-                                      "traffic": t1, "traffic_source": t1_src,
+                                      "traffic": prof1.get("traffic_bytes_per_launch"), "traffic_source": t1_src,
                                       "bytes_per_launch": b1["dominant_bytes_per_launch"],
-                                      "avg_launch_us": round(b1["step_avg_us"], 2)}
+                                      "avg_launch_us": round(b1["step_avg_us"], 2),
+                                      "profile_counters": profile_counters(prof1)}
     if extra:
         line["configs"] = extra
     print(json.dumps(line), flush=True)

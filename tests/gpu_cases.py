@@ -123,3 +123,27 @@ def assert_close(got, ref, what=""):
     assert not bad.any(), (f"{what}: {int(bad.sum())} values outside atol {ATOL} + rtol {RTOL}; "
                            f"max abs err {err.max():.3g}")
     return float(err.max())
+
+
+def synthetic_rows(ctx, seed, slot, layer, t0, n, dist=0, k_outliers=False):
+    """FP32 K/V rows [t0, t0+n) that the device cache filler used for (slot,
+    layer): streams 2*(64*slot + layer) (K) and that + 1 (V)."""
+    sid = 2 * (slot * 64 + layer)
+    buf = ctx.alloc(n * 4096 * 4)
+    ctx.fill_synthetic(buf, n * 4096, seed, sid, dist, k_outliers, first=t0 * 4096)
+    k = buf.download(np.float32, (n, 4096))
+    ctx.fill_synthetic(buf, n * 4096, seed, sid + 1, dist, False, first=t0 * 4096)
+    v = buf.download(np.float32, (n, 4096))
+    buf.free()
+    return k, v
+
+
+def oracle_cache_synthetic(skv, ctx, cos, sin, seed, slot, layer, ntok, cap, dist=0, k_outliers=False, chunk=4096):
+    """The oracle's cache of (slot, layer) rebuilt from the filler's FP32 rows
+    [0, ntok) through the append rule."""
+    sc = O.SequenceCache(H, cap)
+    for t0 in range(0, ntok, chunk):
+        n = min(chunk, ntok - t0)
+        k, v = synthetic_rows(ctx, seed, slot, layer, t0, n, dist, k_outliers)
+        sc.fill_q17(O.f2q17(k), O.f2q17(v), t0, cos, sin)
+    return sc

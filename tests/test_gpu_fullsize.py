@@ -1,7 +1,8 @@
 """GPU parity at the workload's full sizes.
 
-Caches of these sizes (2.4 GB to 4.8 GB) are filled on the device from
-synthetic streams through the append rule; the tests regenerate the FP32
+Caches of these sizes (0.6 GB for 32 layers at batch 1 up to the 77.3 GB
+arena of 64 sequences x 32 layers x 4096 tokens) are filled on the device
+from synthetic streams through the append rule; the tests regenerate the FP32
 source rows of sampled sequences, rebuild them with the oracle and compare:
   - every cached and appended row of the sampled sequences, bit-exact;
   - the appended row of every sequence, bit-exact;
@@ -13,7 +14,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from gpu_cases import H, assert_close, assert_rows_equal
+from gpu_cases import H, assert_close, assert_rows_equal, oracle_cache_synthetic as _oracle_cache
 
 pytestmark = pytest.mark.gpu
 
@@ -21,27 +22,6 @@ pytestmark = pytest.mark.gpu
 def _note(msg):
     print(msg, flush=True)
     sys.stdout.flush()
-
-
-def _source_rows(skv, ctx, seed, slot, layer, t0, n, dist=0, k_outliers=False):
-    """FP32 K/V rows [t0, t0+n) that the synthetic filler used for (slot, layer)."""
-    sid = 2 * (slot * 64 + layer)
-    buf = ctx.alloc(n * 4096 * 4)
-    ctx.fill_synthetic(buf, n * 4096, seed, sid, dist, k_outliers, first=t0 * 4096)
-    k = buf.download(np.float32, (n, 4096))
-    ctx.fill_synthetic(buf, n * 4096, seed, sid + 1, dist, False, first=t0 * 4096)
-    v = buf.download(np.float32, (n, 4096))
-    buf.free()
-    return k, v
-
-
-def _oracle_cache(skv, ctx, cos, sin, seed, slot, layer, ntok, cap, dist=0, k_outliers=False, chunk=4096):
-    sc = O.SequenceCache(H, cap)
-    for t0 in range(0, ntok, chunk):
-        n = min(chunk, ntok - t0)
-        k, v = _source_rows(skv, ctx, seed, slot, layer, t0, n, dist, k_outliers)
-        sc.fill_q17(O.f2q17(k), O.f2q17(v), t0, cos, sin)
-    return sc
 
 
 def _appended_rows_match(kv, slot, layer, pos, k_f32, v_f32, cos, sin):
@@ -103,6 +83,116 @@ def test_batch64_context4096(skv, ctx, rope_tables, ragged):
         q14, e8 = O.a14(o[b].reshape(128, 32))
         assert (codes[b] == e8).all() and (words[b] == O.pack_a14(q14)).all()
     for x in bufs + [out, aq, asc]:
+        x.free()
+    kv.close()
+    lut.close()
+
+
+def _layer_inputs(skv, ctx, seed, layers, batch, k_outliers=False):
+    """q/k/v of a whole decode step, [layer][batch][4096] each, on the device
+    and on the host."""
+    n = layers * batch * 4096
+    bufs, host = [], []
+    for i in range(3):
+        b = ctx.alloc(n * 4)
+        ctx.fill_synthetic(b, n, seed, 9100 + i, 0, k_outliers and i == 1)
+        bufs.append(b)
+        host.append(b.download(np.float32, (layers, batch, 4096)))
+    return bufs, host
+
+
+def _check_sequence_layer(skv, ctx, kv, cos, sin, seed, slot, layer, pos, q, k, v, out_row, aq_row, asc_row,
+                          k_outliers=False):
+    """Every cached row of (slot, layer) and the appended one bit-exact, the
+    output within tolerance, A14/E8M0 bit-exact against the rule."""
+    sc = _oracle_cache(skv, ctx, cos, sin, seed, slot, layer, pos, pos + 1, k_outliers=k_outliers)
+    res = sc.step_q17(O.f2q17(q), O.f2q17(k), O.f2q17(v), pos, cos[pos], sin[pos], fp=True)
+    assert_rows_equal(kv, sc, slot, layer, 0, pos + 1)
+    err = assert_close(out_row.reshape(H, 128), res["fp"], f"slot {slot} layer {layer} position {pos}")
+    q14, e8 = O.a14(out_row.reshape(128, 32))
+    assert (asc_row == e8).all() and (aq_row == O.pack_a14(q14)).all(), f"slot {slot} layer {layer}: A14"
+    return err
+
+
+@pytest.mark.parametrize("position,outliers", [(2047, False), (4095, True)],
+                         ids=["position2047", "position4095_outliers"])
+def test_batch1_32layer_step(skv, ctx, rope_tables, position, outliers):
+    """One full decode step of a 32-layer cache at batch 1: position 2047
+    (the 512 MiB cache of 32 x 2048 tokens) and position 4095 with 1% of K
+    channels x20.  The 32 per-layer calls run back to back, then layers 0,
+    16 and 31 are checked in full against the oracle and every layer's
+    appended row bit for bit."""
+    cos, sin = rope_tables
+    layers, seed = 32, 3100 + position
+    _note(f"case: batch 1, 32 layers, position {position}, outliers={outliers}")
+    lut = skv.RopeLut.generate(ctx, 4096)
+    kv = skv.KVCache(ctx, layers=layers, max_batch=1, max_seq_len=position + 1)
+    kv.fill_synthetic(lut, ntok=position, seed=seed, k_outliers=outliers)
+    bufs, (q, k, v) = _layer_inputs(skv, ctx, seed + 1, layers, 1, k_outliers=outliers)
+    outs = ctx.alloc(layers * 4096 * 4)
+    aqs, ass = ctx.alloc(layers * 128 * 56), ctx.alloc(layers * 128)
+    for layer in range(layers):
+        off = layer * 4096 * 4
+        skv.swiftkv_attention(ctx, bufs[0].ptr + off, bufs[1].ptr + off, bufs[2].ptr + off, kv, lut,
+                              aqs.ptr + layer * 128 * 56, ass.ptr + layer * 128, layer, [position], outs.ptr + off)
+    ctx.synchronize()
+    o = outs.download(np.float32, (layers, 4096))
+    words = aqs.download(np.uint8, (layers, 128, 56))
+    codes = ass.download(np.uint8, (layers, 128))
+    assert np.isfinite(o).all()
+    for layer in range(layers):
+        _appended_rows_match(kv, 0, layer, position, k[layer, 0], v[layer, 0], cos, sin)
+    for layer in (0, 16, 31):
+        _note(f"  oracle check of layer {layer}")
+        _check_sequence_layer(skv, ctx, kv, cos, sin, seed, 0, layer, position, q[layer, 0], k[layer, 0],
+                              v[layer, 0], o[layer], words[layer], codes[layer], k_outliers=outliers)
+    for x in bufs + [outs, aqs, ass]:
+        x.free()
+    kv.close()
+    lut.close()
+
+
+@pytest.mark.parametrize("ragged", [False, True], ids=["position4095", "ragged256to4096"])
+def test_batch64_32layer_arena(skv, ctx, rope_tables, ragged):
+    """The benchmark's arena: 64 sequences x 32 layers x 4096 tokens (77.3 GB),
+    filled on the device, one decode step of 32 per-layer calls.  Checked
+    against the oracle: (slot 63, layer 31) and (slot 0, layer 0) in full --
+    the last and the first page of the arena -- plus the longest and the
+    shortest sequence on layer 17, and every slot's appended row on layers 0
+    and 31.  The ragged case draws attended lengths from U{256..4096}."""
+    cos, sin = rope_tables
+    layers, batch, seed = 32, 64, 6400 + int(ragged)
+    rng = np.random.default_rng(seed)
+    positions = (rng.integers(256, 4097, batch) - 1 if ragged else np.full(batch, 4095)).astype(np.int32)
+    _note(f"case: batch 64 x 32 layers x capacity 4096 arena, {'ragged' if ragged else 'uniform'} positions")
+    lut = skv.RopeLut.generate(ctx, 4096)
+    kv = skv.KVCache(ctx, layers=layers, max_batch=batch, max_seq_len=4096)
+    assert kv.nbytes == 64 * 32 * 32 * 4096 * 288
+    kv.fill_synthetic(lut, ntok=4095, seed=seed)
+    bufs, (q, k, v) = _layer_inputs(skv, ctx, seed + 1, layers, batch)
+    outs = ctx.alloc(layers * batch * 4096 * 4)
+    aqs, ass = ctx.alloc(layers * batch * 128 * 56), ctx.alloc(layers * batch * 128)
+    stride = batch * 4096 * 4
+    for layer in range(layers):
+        skv.swiftkv_attention(ctx, bufs[0].ptr + layer * stride, bufs[1].ptr + layer * stride,
+                              bufs[2].ptr + layer * stride, kv, lut, aqs.ptr + layer * batch * 128 * 56,
+                              ass.ptr + layer * batch * 128, layer, positions, outs.ptr + layer * stride)
+    ctx.synchronize()
+    _note("  step done")
+    o = outs.download(np.float32, (layers, batch, 4096))
+    assert np.isfinite(o).all()
+    for layer in (0, 31):
+        for b in range(batch):
+            _appended_rows_match(kv, b, layer, int(positions[b]), k[layer, b], v[layer, b], cos, sin)
+    checks = [(63, 31), (0, 0), (int(np.argmax(positions)), 17), (int(np.argmin(positions)), 17)]
+    for slot, layer in checks:
+        p = int(positions[slot])
+        _note(f"  oracle check of slot {slot}, layer {layer}, position {p}")
+        words = aqs.download(np.uint8, (128, 56), offset=(layer * batch + slot) * 128 * 56)
+        codes = ass.download(np.uint8, (128,), offset=(layer * batch + slot) * 128)
+        _check_sequence_layer(skv, ctx, kv, cos, sin, seed, slot, layer, p, q[layer, slot], k[layer, slot],
+                              v[layer, slot], o[layer, slot], words, codes)
+    for x in bufs + [outs, aqs, ass]:
         x.free()
     kv.close()
     lut.close()

@@ -1,0 +1,64 @@
+"""Repeatability of the split merge.
+
+A head split across workgroups is finished by whichever split arrives last;
+the partials are exchanged through device memory inside one launch.  The
+merge reads the partials in split order, so for fixed inputs every launch
+must give the same bits whatever the arrival order was.  Each case runs the
+same step 2,000 times (the append rewrites the same row with the same bits),
+writing every launch's outputs to its own slice, and compares every launch
+with the first, in chunks, stopping at the first chunk that differs.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+LAUNCHES = 2000
+CHUNK = 250
+
+
+def _note(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.mark.parametrize("batch,position,split", [(1, 4095, 0), (4, 4095, 256)],
+                         ids=["batch1_8splits", "batch4_16splits_of_256"])
+def test_split_merge_is_bitwise_repeatable(skv, ctx, batch, position, split):
+    _note(f"case: {LAUNCHES} launches, batch {batch}, position {position}, split_tokens {split or 'heuristic'}")
+    lut = skv.RopeLut.generate(ctx, 4096)
+    kv = skv.KVCache(ctx, layers=1, max_batch=batch, max_seq_len=position + 1)
+    kv.fill_synthetic(lut, ntok=position, seed=1234 + batch)
+    qkv = [ctx.alloc(batch * 4096 * 4) for _ in range(3)]
+    for i, b in enumerate(qkv):
+        ctx.fill_synthetic(b, batch * 4096, 1240 + batch, 20 + i)
+    row, aq_row, as_row = batch * 4096 * 4, batch * 128 * 56, batch * 128
+    outs, aqs, ass = ctx.alloc(CHUNK * row), ctx.alloc(CHUNK * aq_row), ctx.alloc(CHUNK * as_row)
+    positions = np.full(batch, position, np.int32)
+    ctx.set_split_tokens(split)
+    first = None
+    try:
+        for c0 in range(0, LAUNCHES, CHUNK):
+            for i in range(CHUNK):
+                skv.swiftkv_attention(ctx, qkv[0], qkv[1], qkv[2], kv, lut, aqs.ptr + i * aq_row,
+                                      ass.ptr + i * as_row, 0, positions, outs.ptr + i * row)
+            ctx.synchronize()
+            o = outs.download(np.uint32, (CHUNK, batch * 4096))
+            w = aqs.download(np.uint8, (CHUNK, aq_row))
+            e = ass.download(np.uint8, (CHUNK, as_row))
+            if first is None:
+                first = (o[0].copy(), w[0].copy(), e[0].copy())
+                assert np.isfinite(o[0].view(np.float32)).all()
+            bad = [c0 + i for i in range(CHUNK)
+                   if not (np.array_equal(o[i], first[0]) and np.array_equal(w[i], first[1])
+                           and np.array_equal(e[i], first[2]))]
+            assert not bad, f"launches {bad[:8]} (of {len(bad)}) differ from launch 0"
+            _note(f"  launches {c0 + CHUNK}/{LAUNCHES} identical")
+    finally:
+        ctx.set_split_tokens(0)
+    for b in qkv + [outs, aqs, ass]:
+        b.free()
+    kv.close()
+    lut.close()

@@ -70,3 +70,78 @@ def test_host_driver_reference_lut_image(skv, ctx, tmp_path):
     res = _result(run("--rope-lut", str(image), "--layers", "1", "--batch", "2", "--context", "4096",
                       "--steps", "2"))
     assert res["max_abs_output"] > 0
+
+
+def _dump_inputs(skv, ctx, meta):
+    """The driver's q/k/v as the step saw them for the dumped layer: Q15.17
+    [batch][4096] each, from the same synthetic streams (FP32, converted as
+    the step converts them, or split-K partials reduced and finalized)."""
+    import numpy as np
+    import oracle as O
+    B, L, layer, parts = meta["batch"], meta["layers"], meta["layer"], meta["parts"]
+    n_all = L * B * 4096
+    out = []
+    for i, stream in enumerate(meta["input_streams"]):
+        n = parts * n_all
+        buf = ctx.alloc(n * 4)
+        ctx.fill_synthetic(buf, n, meta["input_seed"], stream, meta["distribution"], meta["outliers"] and i == 1)
+        x = buf.download(np.float32, (parts, L, B, 4096))[:, layer]
+        buf.free()
+        out.append(O.finalize_partials(x) if parts > 1 else O.f2q17(x[0]))
+    return out
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode", [[], ["--q17"], ["--parts", "4"], ["--exact"], ["--parts", "4", "--exact"],
+                                  ["--decode", "--t3", "--outliers"], ["--graph"], ["--host-io"]])
+def test_host_driver_dump_matches_the_oracle(skv, ctx, rope_tables, tmp_path, mode):
+    """The native host driver's own outputs, dumped with --dump, against the
+    oracle on the inputs it generated (the reference host dumps and compares
+    its outputs the same way, decode_host.cpp:495-531): the appended row of
+    every (sequence, layer, head) bit-exact; the last call's FP32 output
+    within tolerance and its A14/E8M0 words bit-exact against the rule, or,
+    for --exact, the Q15.17 state and the A14/E8M0 words bit-exact against
+    the oracle's integer recurrence."""
+    import numpy as np
+    import oracle as O
+    from gpu_cases import H, assert_close, oracle_cache_synthetic
+
+    print(f"case: swiftkv_host --dump {' '.join(mode)}", flush=True)
+    sys.stdout.flush()
+    _result(run("--layers", "2", "--batch", "3", "--context", "700", "--steps", "3", "--seed", "91",
+                "--dump", str(tmp_path), *mode))
+    meta = json.loads((tmp_path / "meta.json").read_text())
+    B, L, layer, p0, p = meta["batch"], meta["layers"], meta["layer"], meta["first_position"], meta["position"]
+    assert (B, L, layer) == (3, 2, 1) and p == (p0 + 2 if "--decode" in mode else p0) and p0 == 699
+    cos, sin = rope_tables
+    exact = meta["exact"]
+    out = np.fromfile(tmp_path / "output.bin", np.int32 if exact else np.float32).reshape(B, 4096)
+    words = np.fromfile(tmp_path / "activation_q.bin", np.uint8).reshape(B, 128, 56)
+    codes = np.fromfile(tmp_path / "activation_scale.bin", np.uint8).reshape(B, 128)
+    records = np.fromfile(tmp_path / "appended.bin", np.uint8).reshape(B, L, H, 320)
+
+    # every appended row: each layer's own k/v inputs through the append rule at position p
+    for lyr in range(L):
+        m = dict(meta, layer=lyr)
+        _, kq, vq = _dump_inputs(skv, ctx, m)
+        for b in range(B):
+            krot = O.rope_rotate(kq[b].reshape(H, 128), cos[p], sin[p])
+            kc, ks = O.quantize_rows(krot)
+            vc, vs = O.quantize_rows(vq[b].reshape(H, 128))
+            for h in range(H):
+                assert (records[b, lyr, h] == O.pack_record(kc[h], ks[h], vc[h], vs[h])).all(), (b, lyr, h)
+
+    qq, kq, vq = _dump_inputs(skv, ctx, meta)
+    for b in range(B):
+        sc = oracle_cache_synthetic(skv, ctx, cos, sin, meta["seed"], b, layer, p0, p + 1,
+                                    dist=meta["distribution"], k_outliers=meta["outliers"])
+        if p > p0:   # --decode: the earlier steps appended the same layer inputs at p0 .. p-1
+            sc.fill_q17(np.repeat(kq[b][None], p - p0, 0), np.repeat(vq[b][None], p - p0, 0), p0, cos, sin)
+        res = sc.step_q17(qq[b], kq[b], vq[b], p, cos[p], sin[p], fp=not exact, integer=exact)
+        if exact:
+            assert (out[b] == res["int"].reshape(-1)).all(), f"sequence {b}: Q15.17 state"
+            q14, e8 = O.a14_q17(res["int"].reshape(128, 32))
+        else:
+            assert_close(out[b].reshape(H, 128), res["fp"], f"sequence {b}")
+            q14, e8 = O.a14(out[b].reshape(128, 32))
+        assert (codes[b] == e8).all() and (words[b] == O.pack_a14(q14)).all(), f"sequence {b}: A14/E8M0"
