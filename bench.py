@@ -142,7 +142,7 @@ def run_gpu(skv, ctx, positions, layers, steps, warmup, seed, outliers=False, di
     # The same steps again, each one bracketed by events (slot i before step
     # i, all on the stream, no host wait between steps): the median step.
     samples = []
-    if not advance:
+    if not advance and layers >= 8:   # one launch per step would time the event pair itself
         n_each = max(MIN_STEP_SAMPLES, min(steps, STEP_SLOTS - 1))
         for s in range(n_each):
             ctx.timer_record(STEP_SLOT0 + s)
