@@ -80,6 +80,7 @@ _SIGNATURES = {
     "swiftkv_kv_cache_import_records": (C.c_int, [_vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp]),
     "swiftkv_attention_f32": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _vp]),
     "swiftkv_attention_q17": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _vp]),
+    "swiftkv_attention_f32_noalloc": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _vp]),
     "swiftkv_attention_partials": (C.c_int, [_vp, _vp, _vp, _vp, _i32, C.c_int64, _vp, _vp, _vp, _vp, _i32, _vp,
                                              _i32, _vp]),
     "swiftkv_set_host_io": (C.c_int, [_vp, _i32]),
@@ -458,6 +459,21 @@ def swiftkv_attention(ctx: Context, q, k, v, kv_cache: KVCache, rope_lut: RopeLu
               rope_lut.handle, _io_ptr(ctx, activation_q, np.uint8, True),
               _io_ptr(ctx, activation_scale, np.uint8, True), int(layer_index), _host_ptr(pos), int(pos.size),
               _io_ptr(ctx, out, np.float32, True)))
+
+
+NOALLOC_WORKSPACE_BYTES = 9 << 20
+
+
+def swiftkv_attention_noalloc(ctx: Context, q, k, v, kv_cache: KVCache, rope_lut: RopeLut,
+                              activation_q, activation_scale, layer_index: int, position, out) -> None:
+    """swiftkv_attention (FP32 inputs) through the allocation-free entry: the
+    split workspace is the library's fixed per-GPU array, so the call never
+    allocates device memory.  Calls that overlap in time on one GPU race.
+    Device pointers only (host-memory I/O mode is refused)."""
+    pos = np.ascontiguousarray(np.atleast_1d(np.asarray(position, dtype=np.int32)))
+    _check(lib().swiftkv_attention_f32_noalloc(ctx.handle, _ptr(q), _ptr(k), _ptr(v), kv_cache.handle,
+                                               rope_lut.handle, _ptr(activation_q), _ptr(activation_scale),
+                                               int(layer_index), _host_ptr(pos), int(pos.size), _ptr(out)))
 
 
 def swiftkv_attention_partials(ctx: Context, q, k, v, parts: int, kv_cache: KVCache, rope_lut: RopeLut,

@@ -16,6 +16,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <string>
 #include <unordered_set>
@@ -35,21 +36,21 @@ constexpr int kMaxSplitTokens = SWIFTKV_MAX_SEQ;
 static_assert(SWIFTKV_HEADS == kHeads && SWIFTKV_HEAD_DIM == kHeadDim, "geometry");
 static_assert(SWIFTKV_ROPE_LUT_BYTES_PER_POSITION == 512, "RoPE LUT image: 8 x 64-byte words per position");
 static_assert(SWIFTKV_RECORD_BYTES == 5 * 64, "record is [meta, K0, K1, V0, V1]");
+static_assert(SWIFTKV_NOALLOC_WORKSPACE_BYTES == kNoAllocScratchBytes, "allocation-free workspace size");
 
-thread_local std::string g_last_error;
+// A fixed buffer, so that reporting an error never allocates.
+thread_local char g_last_error[512];
 
 int fail(int code, const char* fmt, ...) {
-    char buf[512];
     va_list ap;
     va_start(ap, fmt);
-    std::vsnprintf(buf, sizeof(buf), fmt, ap);
+    std::vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
     va_end(ap);
-    g_last_error = buf;
     return code;
 }
 
 int ok() {
-    g_last_error.clear();
+    g_last_error[0] = '\0';
     return SWIFTKV_OK;
 }
 
@@ -66,6 +67,24 @@ struct ProfilePair {
     hipEvent_t end;
     int kind;
 };
+
+// Device address of the allocation-free entry's workspace, per device,
+// resolved and zeroed once (by the first context created on the device).
+std::mutex g_scratch_mutex;
+std::vector<void*> g_scratch;
+
+hipError_t scratch_for_device(int device, int count, hipStream_t s, void** out) {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch.size() < static_cast<size_t>(count)) g_scratch.resize(static_cast<size_t>(count), nullptr);
+    if (!g_scratch[device]) {
+        void* p = nullptr;
+        const hipError_t e = bind_noalloc_scratch(s, &p);
+        if (e != hipSuccess) return e;
+        g_scratch[device] = p;
+    }
+    *out = g_scratch[device];
+    return hipSuccess;
+}
 
 }  // namespace
 
@@ -84,6 +103,7 @@ struct swiftkv_context {
     int64_t graphs = 0;
     std::vector<void*> retired;
     uint32_t* counters = nullptr;   // [kMaxBatchPerLaunch][32] split arrivals (kCounterStride apart), zero between launches
+    uint8_t* scratch = nullptr;     // this device's allocation-free workspace (counters, then partials)
     // timing
     hipEvent_t timers[kTimerSlots] = {};
     bool profiling = false;
@@ -284,13 +304,18 @@ int step_waves(const swiftkv_context* ctx, int32_t grid_splits, int32_t batch, i
     return wide ? kWideWaves : kAttendWaves;
 }
 
-// Dispatch rows of one launch: (position, sequence) longest first (stable,
-// so a uniform batch keeps its natural order).
+// Dispatch rows of one launch: (position, sequence) longest first, equal
+// positions in sequence order (so a uniform batch keeps its natural order).
+// The keys are unique, so an in-place sort of them (no allocation) is stable.
 void set_rows(StepArgs& a, const int32_t* positions) {
-    int32_t idx[kMaxBatchPerLaunch];
-    for (int32_t b = 0; b < a.batch; ++b) idx[b] = b;
-    std::stable_sort(idx, idx + a.batch, [&](int32_t x, int32_t y) { return positions[x] > positions[y]; });
-    for (int32_t z = 0; z < a.batch; ++z) a.rows[z] = pack_row(idx[z], positions[idx[z]]);
+    uint32_t key[kMaxBatchPerLaunch];
+    for (int32_t b = 0; b < a.batch; ++b)
+        key[b] = (static_cast<uint32_t>(kMaxSeq - 1 - positions[b]) << 8) | static_cast<uint32_t>(b);
+    std::sort(key, key + a.batch);
+    for (int32_t z = 0; z < a.batch; ++z) {
+        const int32_t b = static_cast<int32_t>(key[z] & 0xffu);
+        a.rows[z] = pack_row(b, positions[b]);
+    }
 }
 
 // How a step's q/k/v arrive: the format and, for split-K partials, the
@@ -346,13 +371,30 @@ void profile_end(swiftkv_context* ctx, ProfilePair* p) {
     if (p) (void)hipEventRecord(p->end, ctx->stream);
 }
 
+// noalloc: the split workspace is this device's fixed file-scope array
+// instead of the context's growable buffer; a launch that needs more than it
+// holds is refused (SWIFTKV_ERANGE) before anything is enqueued.
 int run_step(swiftkv_context* ctx, const void* q, const void* k, const void* v, StepInput in,
              swiftkv_kv_cache* kv, const swiftkv_rope_lut* lut, uint8_t* act_q, uint8_t* act_scale,
-             int32_t layer, const int32_t* positions, int32_t batch, float* out) {
+             int32_t layer, const int32_t* positions, int32_t batch, float* out, bool noalloc = false) {
     int rc = validate_step(ctx, q, k, v, kv, lut, act_q, act_scale, layer, positions, batch, out);
     if (rc) return rc;
     if ((rc = set_device(ctx))) return rc;
     const size_t elem_bytes = 4;
+    if (noalloc) {   // size every launch first, so a refused call enqueues nothing
+        for (int32_t b0 = 0; b0 < batch; b0 += kMaxBatchPerLaunch) {
+            const int32_t nb = std::min<int32_t>(kMaxBatchPerLaunch, batch - b0);
+            int32_t max_pos = 0;
+            for (int32_t b = 0; b < nb; ++b) max_pos = std::max(max_pos, positions[b0 + b]);
+            const int32_t split = choose_split(ctx, positions + b0, nb);
+            const size_t need = static_cast<size_t>(nb) * kHeads * ((max_pos + split) / split) * kPartialStride *
+                                sizeof(float);
+            if (need > kNoAllocPartialBytes)
+                return fail(SWIFTKV_ERANGE, "the step needs %zu bytes of split workspace; the allocation-free entry "
+                            "holds %zu: pass fewer sequences per call, or a longer split", need,
+                            static_cast<size_t>(kNoAllocPartialBytes));
+        }
+    }
     for (int32_t b0 = 0; b0 < batch; b0 += kMaxBatchPerLaunch) {
         const int32_t nb = std::min<int32_t>(kMaxBatchPerLaunch, batch - b0);
         StepArgs a;
@@ -374,11 +416,16 @@ int run_step(swiftkv_context* ctx, const void* q, const void* k, const void* v, 
         a.split_tokens = choose_split(ctx, positions + b0, nb);
         const int32_t grid_splits = (max_pos + 1 + a.split_tokens - 1) / a.split_tokens;
         a.max_splits = grid_splits;
-        if ((rc = ensure(ctx, ctx->partials, ctx->partial_elems,
-                         static_cast<size_t>(nb) * kHeads * grid_splits * kPartialStride, true)))
-            return rc;
-        a.partials = ctx->partials;
-        a.counters = ctx->counters;
+        if (noalloc) {
+            a.counters = reinterpret_cast<uint32_t*>(ctx->scratch);
+            a.partials = reinterpret_cast<float*>(ctx->scratch + kNoAllocCounterBytes);
+        } else {
+            if ((rc = ensure(ctx, ctx->partials, ctx->partial_elems,
+                             static_cast<size_t>(nb) * kHeads * grid_splits * kPartialStride, true)))
+                return rc;
+            a.partials = ctx->partials;
+            a.counters = ctx->counters;
+        }
         a.out = out + row0;
         a.act_q = act_q ? act_q + static_cast<size_t>(b0) * kHeads * kGroupsPerHead * SWIFTKV_A14_WORD_BYTES
                         : nullptr;
@@ -535,7 +582,7 @@ void free_context(swiftkv_context* ctx) {
 
 extern "C" {
 
-const char* swiftkv_last_error(void) { return g_last_error.c_str(); }
+const char* swiftkv_last_error(void) { return g_last_error; }
 
 const char* swiftkv_version(void) { return "swiftkv-mi355x 0.1 (gfx950)"; }
 
@@ -556,6 +603,9 @@ int swiftkv_context_create(int device, swiftkv_context** out) {
     const size_t counter_bytes = sizeof(uint32_t) * kMaxBatchPerLaunch * kHeads * kCounterStride;
     if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&ctx->counters), counter_bytes);
     if (e == hipSuccess) e = hipMemset(ctx->counters, 0, counter_bytes);
+    void* scratch = nullptr;
+    if (e == hipSuccess) e = scratch_for_device(device, count, ctx->stream, &scratch);
+    ctx->scratch = static_cast<uint8_t*>(scratch);
     if (e != hipSuccess) {
         swiftkv_context_destroy(ctx);
         return fail(SWIFTKV_EHIP, "stream/event creation: %s", hipGetErrorString(e));
@@ -847,6 +897,18 @@ int swiftkv_attention_q17(swiftkv_context* ctx, const int32_t* q, const int32_t*
                           int32_t batch, float* out) {
     return dispatch_step(ctx, false, q, k, v, kQ17Input, kv_cache, rope_lut, activation_q, activation_scale,
                          layer_index, positions, batch, out);
+}
+
+int swiftkv_attention_f32_noalloc(swiftkv_context* ctx, const float* q, const float* k, const float* v,
+                                  swiftkv_kv_cache* kv_cache, const swiftkv_rope_lut* rope_lut,
+                                  uint8_t* activation_q, uint8_t* activation_scale, int32_t layer_index,
+                                  const int32_t* positions, int32_t batch, float* out) {
+    if (!ctx) return fail(SWIFTKV_EINVAL, "null context");
+    if (ctx->host_io)
+        return fail(SWIFTKV_ESTATE, "host-memory I/O mode stages through an allocated buffer: switch it off for "
+                    "the allocation-free entry");
+    return run_step(ctx, q, k, v, kF32Input, kv_cache, rope_lut, activation_q, activation_scale, layer_index,
+                    positions, batch, out, true);
 }
 
 int swiftkv_attention_partials(swiftkv_context* ctx, const float* q, const float* k, const float* v,

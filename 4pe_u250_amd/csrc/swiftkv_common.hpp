@@ -109,6 +109,13 @@ struct BulkArgs {
     int32_t n;
 };
 
+// Workspace of the allocation-free step entry: one file-scope device array
+// per GPU (swiftkv_kernels.hip), the split-arrival counters first, then the
+// split partials.  Bound once per device by bind_noalloc_scratch.
+constexpr size_t kNoAllocCounterBytes = sizeof(uint32_t) * kMaxBatchPerLaunch * kHeads * kCounterStride;
+constexpr size_t kNoAllocPartialBytes = size_t(8) << 20;
+constexpr size_t kNoAllocScratchBytes = kNoAllocCounterBytes + kNoAllocPartialBytes;
+
 // Launchers (swiftkv_kernels.hip).
 // waves: kAttendWaves, or kWideWaves when a.split_tokens is a multiple of
 // kWideWaves * kBlockTokens.
@@ -116,6 +123,9 @@ hipError_t launch_step(const StepArgs& a, int grid_splits, int waves, InputForma
 // Workgroups of the 4-wave step kernel one CU holds at once (0 on error).
 int step_workgroups_per_cu();
 hipError_t launch_append_bulk(const BulkArgs& a, bool q17, hipStream_t s);
+// Device address of the allocation-free workspace on the current device,
+// zero-filled by a kernel on `s` (waits for it).  Call once per device.
+hipError_t bind_noalloc_scratch(hipStream_t s, void** device_ptr);
 // Integer-compatibility step (one workgroup per (sequence, head)); a.out is
 // int32 Q15.17; exp_lut holds the 33 Q30 exp2 entries.
 hipError_t launch_exact(const StepArgs& a, const uint32_t* exp_lut, bool q17, hipStream_t s);

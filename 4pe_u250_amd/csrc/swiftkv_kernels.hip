@@ -29,6 +29,13 @@
 // No MFMA: q_len = 1 multi-head attention is a memory-bound GEMV.
 #include "swiftkv_device.hpp"
 
+// Split workspace of the allocation-free step entry (swiftkv_attention_f32_noalloc):
+// every GPU the library runs on holds its own copy until the process ends.
+// Host code never passes this name to a kernel (on the host it is only a
+// stand-in for the symbol): bind_noalloc_scratch resolves the device address
+// once per device and the entry passes that address.
+static __device__ __align__(256) unsigned char scratch[swiftkv::kNoAllocScratchBytes];
+
 namespace swiftkv {
 namespace {
 
@@ -470,9 +477,27 @@ __global__ __launch_bounds__(256) void convert_kernel(const float* __restrict__ 
     }
 }
 
+__global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* __restrict__ p, size_t n) {
+    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = 0u;
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------- launchers
+
+hipError_t bind_noalloc_scratch(hipStream_t s, void** device_ptr) {
+    static_assert(kNoAllocScratchBytes % 4 == 0 && kNoAllocCounterBytes % 256 == 0, "workspace layout");
+    void* p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    const size_t words = kNoAllocScratchBytes / 4;
+    zero_words_kernel<<<1024, 256, 0, s>>>(static_cast<uint32_t*>(p), words);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if ((e = hipStreamSynchronize(s)) != hipSuccess) return e;
+    *device_ptr = p;
+    return hipSuccess;
+}
 
 template <int WAVES>
 hipError_t launch_step_waves(const StepArgs& a, dim3 grid, InputFormat in, hipStream_t s) {
