@@ -461,7 +461,7 @@ def swiftkv_attention(ctx: Context, q, k, v, kv_cache: KVCache, rope_lut: RopeLu
               _io_ptr(ctx, out, np.float32, True)))
 
 
-NOALLOC_WORKSPACE_BYTES = 9 << 20
+NOALLOC_WORKSPACE_BYTES = 69206016   # 1 MiB of arrival words + 8 splits x 256 sequences x 32 heads of partials
 
 
 def swiftkv_attention_noalloc(ctx: Context, q, k, v, kv_cache: KVCache, rope_lut: RopeLut,

@@ -37,6 +37,7 @@ static_assert(SWIFTKV_HEADS == kHeads && SWIFTKV_HEAD_DIM == kHeadDim, "geometry
 static_assert(SWIFTKV_ROPE_LUT_BYTES_PER_POSITION == 512, "RoPE LUT image: 8 x 64-byte words per position");
 static_assert(SWIFTKV_RECORD_BYTES == 5 * 64, "record is [meta, K0, K1, V0, V1]");
 static_assert(SWIFTKV_NOALLOC_WORKSPACE_BYTES == kNoAllocScratchBytes, "allocation-free workspace size");
+static_assert(SWIFTKV_A14_WORD_BYTES == kA14WordBytes, "A14 word: 32 x 14 bits");
 
 // A fixed buffer, so that reporting an error never allocates.
 thread_local char g_last_error[512];
@@ -94,16 +95,18 @@ struct swiftkv_context {
     int step_per_cu = 3;        // 4-wave step workgroups one CU holds at once
     hipStream_t stream = nullptr;
     int32_t split_tokens = 0;   // 0: heuristic
-    // split-context workspace
-    float* partials = nullptr;
-    size_t partial_elems = 0;
+    // split-context workspace: [partial_rows][32][partial_slots][kSlotWords]
+    // tagged words, zero-filled when allocated (tag 0 is never current)
+    uint64_t* partials = nullptr;
+    int32_t partial_rows = 0;
+    int32_t partial_slots = 0;
     // Graphs record the workspace pointer in their kernel nodes, so a buffer
     // the workspace outgrows while a graph of this context exists is kept
     // here, and released when the last graph is destroyed.
     int64_t graphs = 0;
     std::vector<void*> retired;
-    uint32_t* counters = nullptr;   // [kMaxBatchPerLaunch][32] split arrivals (kCounterStride apart), zero between launches
-    uint8_t* scratch = nullptr;     // this device's allocation-free workspace (counters, then partials)
+    uint64_t* arrivals = nullptr;   // [kMaxBatchPerLaunch][32] arrival words (kArrivalStride apart)
+    uint8_t* scratch = nullptr;     // this device's allocation-free workspace (arrival words, then partials)
     // timing
     hipEvent_t timers[kTimerSlots] = {};
     bool profiling = false;
@@ -175,23 +178,15 @@ int free_retired(swiftkv_context* ctx) {
     return SWIFTKV_OK;
 }
 
-// Device buffer growth.  The old buffer may still be read by queued kernels,
-// so the stream is drained before it is released.  A buffer that recorded
-// graphs may reference (graph_visible) is retired instead while any graph of
-// the context exists: a replay after the growth still finds it allocated.
+// Growth of the host-memory I/O stage.  The old buffer may still be read by
+// queued kernels, so the stream is drained before it is released (graphs
+// never use the stage: host-memory I/O cannot be captured).
 template <typename T>
-int ensure(swiftkv_context* ctx, T*& ptr, size_t& have, size_t need, bool graph_visible) {
+int ensure(swiftkv_context* ctx, T*& ptr, size_t& have, size_t need) {
     if (need <= have) return SWIFTKV_OK;
-    if (ctx->capturing)
-        return fail(SWIFTKV_ESTATE, "split workspace too small during graph capture (%zu < %zu bytes): run the "
-                    "call once before capturing", have * sizeof(T), need * sizeof(T));
     if (ptr) {
-        if (graph_visible && ctx->graphs > 0) {
-            ctx->retired.push_back(ptr);
-        } else {
-            SKV_HIP(hipStreamSynchronize(ctx->stream));
-            SKV_HIP(hipFree(ptr));
-        }
+        SKV_HIP(hipStreamSynchronize(ctx->stream));
+        SKV_HIP(hipFree(ptr));
         ptr = nullptr;
         have = 0;
     }
@@ -200,6 +195,41 @@ int ensure(swiftkv_context* ctx, T*& ptr, size_t& have, size_t need, bool graph_
         return fail(SWIFTKV_ENOMEM, "hipMalloc of %zu bytes failed", need * sizeof(T));
     ptr = static_cast<T*>(p);
     have = need;
+    return SWIFTKV_OK;
+}
+
+// The split workspace for a launch of `rows` sequences split `slots` ways.
+// The layout (rows, slots) stays fixed for the life of a buffer, so a word
+// left by an earlier launch sits where the same (row, head, split) wrote it,
+// with an older generation's tag; a new buffer is zero-filled.
+int ensure_partials(swiftkv_context* ctx, int32_t rows, int32_t slots) {
+    if (rows <= ctx->partial_rows && slots <= ctx->partial_slots) return SWIFTKV_OK;
+    if (ctx->capturing)
+        return fail(SWIFTKV_ESTATE, "split workspace too small during graph capture (%d x %d slots < %d x %d): run "
+                    "the call once before capturing", ctx->partial_rows, ctx->partial_slots, rows, slots);
+    const int32_t new_rows = std::max(rows, ctx->partial_rows);
+    const int32_t new_slots = std::max({slots, ctx->partial_slots, kFixedSlots});
+    if (ctx->partials) {
+        if (ctx->graphs > 0) {
+            ctx->retired.push_back(ctx->partials);
+        } else {
+            SKV_HIP(hipStreamSynchronize(ctx->stream));
+            SKV_HIP(hipFree(ctx->partials));
+        }
+        ctx->partials = nullptr;
+        ctx->partial_rows = ctx->partial_slots = 0;
+    }
+    const size_t bytes = sizeof(uint64_t) * new_rows * kHeads * new_slots * kSlotWords;
+    void* p = nullptr;
+    if (hipMalloc(&p, bytes) != hipSuccess) return fail(SWIFTKV_ENOMEM, "hipMalloc of %zu bytes failed", bytes);
+    const hipError_t e = hipMemsetAsync(p, 0, bytes, ctx->stream);
+    if (e != hipSuccess) {
+        (void)hipFree(p);
+        return fail(SWIFTKV_EHIP, "split workspace zero-fill: %s", hipGetErrorString(e));
+    }
+    ctx->partials = static_cast<uint64_t*>(p);
+    ctx->partial_rows = new_rows;
+    ctx->partial_slots = new_slots;
     return SWIFTKV_OK;
 }
 
@@ -381,18 +411,17 @@ int run_step(swiftkv_context* ctx, const void* q, const void* k, const void* v, 
     if (rc) return rc;
     if ((rc = set_device(ctx))) return rc;
     const size_t elem_bytes = 4;
-    if (noalloc) {   // size every launch first, so a refused call enqueues nothing
+    if (noalloc) {   // check every launch first, so a refused call enqueues nothing
         for (int32_t b0 = 0; b0 < batch; b0 += kMaxBatchPerLaunch) {
             const int32_t nb = std::min<int32_t>(kMaxBatchPerLaunch, batch - b0);
             int32_t max_pos = 0;
             for (int32_t b = 0; b < nb; ++b) max_pos = std::max(max_pos, positions[b0 + b]);
             const int32_t split = choose_split(ctx, positions + b0, nb);
-            const size_t need = static_cast<size_t>(nb) * kHeads * ((max_pos + split) / split) * kPartialStride *
-                                sizeof(float);
-            if (need > kNoAllocPartialBytes)
-                return fail(SWIFTKV_ERANGE, "the step needs %zu bytes of split workspace; the allocation-free entry "
-                            "holds %zu: pass fewer sequences per call, or a longer split", need,
-                            static_cast<size_t>(kNoAllocPartialBytes));
+            const int32_t splits = (max_pos + split) / split;
+            if (splits > kFixedSlots)
+                return fail(SWIFTKV_ERANGE, "the step splits a head %d ways (%d-token splits of up to %d tokens); the "
+                            "allocation-free entry's workspace holds %d splits per head: use longer splits", splits,
+                            split, max_pos + 1, kFixedSlots);
         }
     }
     for (int32_t b0 = 0; b0 < batch; b0 += kMaxBatchPerLaunch) {
@@ -415,16 +444,15 @@ int run_step(swiftkv_context* ctx, const void* q, const void* k, const void* v, 
         set_rows(a, positions + b0);
         a.split_tokens = choose_split(ctx, positions + b0, nb);
         const int32_t grid_splits = (max_pos + 1 + a.split_tokens - 1) / a.split_tokens;
-        a.max_splits = grid_splits;
         if (noalloc) {
-            a.counters = reinterpret_cast<uint32_t*>(ctx->scratch);
-            a.partials = reinterpret_cast<float*>(ctx->scratch + kNoAllocCounterBytes);
+            a.arrivals = reinterpret_cast<uint64_t*>(ctx->scratch);
+            a.partials = reinterpret_cast<uint64_t*>(ctx->scratch + kNoAllocCounterBytes);
+            a.slot_stride = kFixedSlots;
         } else {
-            if ((rc = ensure(ctx, ctx->partials, ctx->partial_elems,
-                             static_cast<size_t>(nb) * kHeads * grid_splits * kPartialStride, true)))
-                return rc;
+            if (grid_splits > 1 && (rc = ensure_partials(ctx, nb, grid_splits))) return rc;
+            a.arrivals = ctx->arrivals;
             a.partials = ctx->partials;
-            a.counters = ctx->counters;
+            a.slot_stride = ctx->partial_slots;
         }
         a.out = out + row0;
         a.act_q = act_q ? act_q + static_cast<size_t>(b0) * kHeads * kGroupsPerHead * SWIFTKV_A14_WORD_BYTES
@@ -510,7 +538,7 @@ int dispatch_step(swiftkv_context* ctx, bool exact, const void* q, const void* k
     const size_t off_k = align(in_bytes), off_v = 2 * align(in_bytes), off_out = 3 * align(in_bytes);
     const size_t off_aq = off_out + align(row_bytes);
     const size_t off_as = off_aq + align(aq_bytes), total = off_as + align(as_bytes);
-    if ((rc = ensure(ctx, ctx->io_stage, ctx->io_bytes, total, false))) return rc;
+    if ((rc = ensure(ctx, ctx->io_stage, ctx->io_bytes, total))) return rc;
     uint8_t* st = ctx->io_stage;
     SKV_HIP(hipMemcpyAsync(st, q, in_bytes, hipMemcpyHostToDevice, ctx->stream));
     SKV_HIP(hipMemcpyAsync(st + off_k, k, in_bytes, hipMemcpyHostToDevice, ctx->stream));
@@ -566,7 +594,7 @@ void free_context(swiftkv_context* ctx) {
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     if (ctx->partials) (void)hipFree(ctx->partials);
     for (void* p : ctx->retired) (void)hipFree(p);
-    if (ctx->counters) (void)hipFree(ctx->counters);
+    if (ctx->arrivals) (void)hipFree(ctx->arrivals);
     if (ctx->io_stage) (void)hipFree(ctx->io_stage);
     for (auto& t : ctx->timers)
         if (t) (void)hipEventDestroy(t);
@@ -600,9 +628,9 @@ int swiftkv_context_create(int device, swiftkv_context** out) {
     if (e == hipSuccess) ctx->step_per_cu = std::max(1, step_workgroups_per_cu());
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
     for (int i = 0; e == hipSuccess && i < kTimerSlots; ++i) e = hipEventCreate(&ctx->timers[i]);
-    const size_t counter_bytes = sizeof(uint32_t) * kMaxBatchPerLaunch * kHeads * kCounterStride;
-    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&ctx->counters), counter_bytes);
-    if (e == hipSuccess) e = hipMemset(ctx->counters, 0, counter_bytes);
+    const size_t arrival_bytes = sizeof(uint64_t) * kMaxBatchPerLaunch * kHeads * kArrivalStride;
+    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&ctx->arrivals), arrival_bytes);
+    if (e == hipSuccess) e = hipMemset(ctx->arrivals, 0, arrival_bytes);
     void* scratch = nullptr;
     if (e == hipSuccess) e = scratch_for_device(device, count, ctx->stream, &scratch);
     ctx->scratch = static_cast<uint8_t*>(scratch);
@@ -953,7 +981,7 @@ int swiftkv_append_tokens(swiftkv_context* ctx, const void* k, const void* v, in
     const size_t rows_bytes = static_cast<size_t>(n) * kModelDim * 4;
     if (ctx->host_io) {   // stage the host rows (see dispatch_step)
         const size_t half = (rows_bytes + 255) & ~static_cast<size_t>(255);
-        if ((rc = ensure(ctx, ctx->io_stage, ctx->io_bytes, 2 * half, false))) return rc;
+        if ((rc = ensure(ctx, ctx->io_stage, ctx->io_bytes, 2 * half))) return rc;
         SKV_HIP(hipMemcpyAsync(ctx->io_stage, k, rows_bytes, hipMemcpyHostToDevice, ctx->stream));
         SKV_HIP(hipMemcpyAsync(ctx->io_stage + half, v, rows_bytes, hipMemcpyHostToDevice, ctx->stream));
         k = ctx->io_stage;

@@ -22,6 +22,7 @@ constexpr int kCodeBytes = kHeadDim;             // 128 B per token per plane
 constexpr int kScaleBytes = 8 * 4;               // 32 B per token
 constexpr int kTokenBytes = 2 * kCodeBytes + kScaleBytes;  // 288 B
 constexpr int kSeqAlign = 64;                    // capacity granularity (tokens)
+constexpr int kA14WordBytes = 56;                // ap_uint<448>: 32 x 14-bit lanes
 
 // Split-context work: a workgroup of kAttendWaves wavefronts scans a range of
 // split_tokens tokens; each wave takes 64-token blocks round-robin.
@@ -32,13 +33,20 @@ constexpr int kAttendWaves = 4;
 constexpr int kWideWaves = 8;
 constexpr int kBlockTokens = 64;
 constexpr int kSplitQuantum = kAttendWaves * kBlockTokens;   // 256
-constexpr int kPartialStride = 4 + kHeadDim;     // (m, l, pad, pad, acc[128]) floats
 constexpr int kMaxSeq = 32768;                   // longest cache this build accepts
 constexpr int kMaxSplits = kMaxSeq / kSplitQuantum;   // 128 partials per (sequence, head)
 
-// Split-arrival counters sit one per 128-byte cache line: the splits of all
-// heads finish together, and counters sharing a line serialize their atomics.
-constexpr int kCounterStride = 32;               // uint32 words
+// A split's partial (m, l, acc[128]) travels as kSlotWords 64-bit words, each
+// the launch's 32-bit tag above the value's bits.
+constexpr int kSlotWords = 2 + kHeadDim;
+// Slots per (row, head) in the allocation-free layout (the heuristic never
+// splits a head more than 8 ways).
+constexpr int kFixedSlots = 8;
+
+// Per (row, head) arrival word {generation:32 | arrivals:32}, one per 128-byte
+// cache line: the splits of all heads finish together, and words sharing a
+// line serialize their atomics.
+constexpr int kArrivalStride = 16;               // uint64 words
 
 // Sequences per launch: positions travel by value in the kernel arguments.
 constexpr int kMaxBatchPerLaunch = 256;
@@ -77,9 +85,12 @@ struct StepArgs {
     int32_t batch;            // sequences in this launch
     int32_t slot0;            // cache slot of sequence 0 of this launch
     int32_t split_tokens;     // multiple of kSplitQuantum
-    int32_t max_splits;       // partial slots per (sequence, head)
-    float* partials;          // [batch][32][max_splits][kPartialStride]
-    uint32_t* counters;       // [batch][32] split arrivals, one per kCounterStride words; zero between launches
+    int32_t slot_stride;      // split slots per (row, head) in `partials`, >= the launch's splits
+    uint64_t* partials;       // [rows][32][slot_stride][kSlotWords] tagged words
+    // [256][32] arrival words, kArrivalStride apart: the generation of the
+    // (row, head) in the upper half, this launch's arrivals (zero between
+    // launches) in the lower half
+    uint64_t* arrivals;
     float* out;               // [batch][4096]
     uint8_t* act_q;           // [batch][128][56] or null
     uint8_t* act_scale;       // [batch][128] or null
@@ -112,8 +123,9 @@ struct BulkArgs {
 // Workspace of the allocation-free step entry: one file-scope device array
 // per GPU (swiftkv_kernels.hip), the split-arrival counters first, then the
 // split partials.  Bound once per device by bind_noalloc_scratch.
-constexpr size_t kNoAllocCounterBytes = sizeof(uint32_t) * kMaxBatchPerLaunch * kHeads * kCounterStride;
-constexpr size_t kNoAllocPartialBytes = size_t(8) << 20;
+constexpr size_t kNoAllocCounterBytes = sizeof(uint64_t) * kMaxBatchPerLaunch * kHeads * kArrivalStride;
+constexpr size_t kNoAllocPartialBytes =
+    sizeof(uint64_t) * kMaxBatchPerLaunch * kHeads * kFixedSlots * kSlotWords;
 constexpr size_t kNoAllocScratchBytes = kNoAllocCounterBytes + kNoAllocPartialBytes;
 
 // Launchers (swiftkv_kernels.hip).

@@ -41,7 +41,7 @@ namespace {
 
 using namespace dev;
 
-static_assert(kMaxSplits <= kHeadDim, "one merge thread per split statistic");
+static_assert(kMaxSplits <= 4 * 64, "one merge thread per split statistic (workgroups have >= 4 waves)");
 
 // Scores are kept in the log2 domain: the query is pre-scaled by
 // 1/sqrt(128) * log2(e) so the softmax uses v_exp_f32 (2^x) directly.
@@ -188,19 +188,35 @@ __device__ __forceinline__ void scan_range(const PageReader& pr, BlockLoads& bl,
     for (int j = 0; j < 16; ++j) acc[j] = across_octets_sum(acc[j]);
 }
 
+// Max over the 16 lanes of an aligned DPP row, as float (every lane gets it).
+__device__ __forceinline__ float row16_maxf(float x) {
+    x = fmaxf(x, dpp_f<kDppQuadXor1>(x));
+    x = fmaxf(x, dpp_f<kDppQuadXor2>(x));
+    x = fmaxf(x, dpp_f<kDppHalfMirror>(x));
+    return fmaxf(x, dpp_f<kDppRowRor8>(x));
+}
+
+__device__ __forceinline__ float readlane_f(float x, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
+}
+
 // Per-(sequence, head) output: FP32 row and, when requested, A14/G32 + E8M0
 // (swiftkv_attention.cpp:1715-1771, 2656-2682): per 32 outputs, e = frexp
 // exponent of max|o| clamped at -127, q = trunc(clamp(o*2^(13-e) +- 0.5,
-// +-8191)), code = e + 127 (0 for an all-zero group).  Called by every thread of the block;
-// threads d < 128 supply output channel d.
+// +-8191)), code = e + 127 (0 for an all-zero group).  Called by waves 0-1
+// only, thread d supplying output channel d: each G32 group is one half-wave,
+// so the group maximum (DPP within 16-lane rows, then the two rows of the
+// half) and the packing of the 14-bit lanes (lane-to-lane reads) stay inside
+// the wave, with no LDS and no barrier.
 __device__ __forceinline__ void finalize_head(const StepArgs& a, int b, int h, float o) {
     const int d = threadIdx.x;
-    const bool active = d < kHeadDim;
-    if (active) a.out[static_cast<size_t>(b) * kModelDim + h * kHeadDim + d] = o;
+    a.out[static_cast<size_t>(b) * kModelDim + h * kHeadDim + d] = o;
     if (a.act_q == nullptr) return;
-    float mx_abs = active ? fabsf(o) : 0.0f;
-#pragma unroll
-    for (int s = 1; s < 32; s <<= 1) mx_abs = fmaxf(mx_abs, __shfl_xor(mx_abs, s));
+    const int lane = d & 63;
+    const float row_max = row16_maxf(fabsf(o));
+    const float lo = fmaxf(readlane_f(row_max, 0), readlane_f(row_max, 16));
+    const float hi = fmaxf(readlane_f(row_max, 32), readlane_f(row_max, 48));
+    const float mx_abs = lane < 32 ? lo : hi;
     int16_t q14 = 0;
     uint8_t code = 0;
     if (mx_abs != 0.0f) {
@@ -217,74 +233,160 @@ __device__ __forceinline__ void finalize_head(const StepArgs& a, int b, int h, f
         q14 = static_cast<int16_t>(static_cast<int>(rr));
         code = static_cast<uint8_t>(e + 127);
     }
-    __shared__ int16_t s_q14[kHeadDim];
-    if (active) s_q14[d] = q14;
-    __syncthreads();
-    const size_t grp0 = static_cast<size_t>(b) * (kHeads * kGroupsPerHead) + h * kGroupsPerHead;
-    if (active && (d & 31) == 0) a.act_scale[grp0 + (d >> 5)] = code;
-    // 4 groups x 14 dwords of packed 14-bit lanes (lane i at bits [14i, 14i+13]).
-    if (d < kGroupsPerHead * 14) {
-        const int g = d / 14, w = d % 14;
+    // Lane gl < 14 of a group builds 32-bit word gl of its 448-bit A14 word
+    // (lane i of the group at bits [14i, 14i+13]): the lanes floor(32gl/14)
+    // to floor((32gl+31)/14), at most four, reach it.
+    const int gl = lane & 31, base = lane & 32;
+    const int i0 = (32 * gl) / 14;
+    const uint32_t q = static_cast<uint32_t>(static_cast<uint16_t>(q14)) & 0x3fffu;
+    uint32_t src[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) src[k] = __shfl(q, base + min(i0 + k, 31));
+    const size_t grp = static_cast<size_t>(b) * (kHeads * kGroupsPerHead) + h * kGroupsPerHead + (d >> 5);
+    if (gl < 14) {
+        const int bit0 = 32 * gl;
         uint32_t word = 0;
-        const int bit0 = 32 * w;
-        for (int i = bit0 / 14; i <= (bit0 + 31) / 14 && i < 32; ++i) {
-            const uint32_t val = static_cast<uint32_t>(static_cast<uint16_t>(s_q14[g * 32 + i])) & 0x3fffu;
-            const int sh = 14 * i - bit0;
-            word |= sh >= 0 ? (val << sh) : (val >> -sh);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int i = i0 + k;
+            if (i < 32 && 14 * i <= bit0 + 31) {
+                const int sh = 14 * i - bit0;
+                word |= sh >= 0 ? (src[k] << sh) : (src[k] >> -sh);
+            }
         }
-        reinterpret_cast<uint32_t*>(a.act_q + (grp0 + g) * 56)[w] = word;
+        reinterpret_cast<uint32_t*>(a.act_q + grp * kA14WordBytes)[gl] = word;
     }
+    if (gl == 0) a.act_scale[grp] = code;
 }
 
-// Split partials are exchanged through device memory inside one launch.
-// Writers publish with agent-scope atomic stores (write-through to the
-// device coherence point, no dirty L2 lines) and wait for their completion;
-// the last split of a head, identified by a device-scope counter, reads them
-// back with agent-scope atomic loads.  No L2 writeback or invalidation is
-// needed on either side.
-__device__ __forceinline__ void publish(float* p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Split partials are exchanged through device memory inside one launch as
+// 64-bit words: the launch's 32-bit tag above the value's bits, written and
+// read with agent-scope atomic accesses (write-through to the device
+// coherence point, no L2 writeback or invalidate on either side).  A 64-bit
+// atomic access is single-copy atomic, so a word that carries this launch's
+// tag holds the value this launch's split wrote: the merger needs no ordering
+// between the words, the arrival count and the stores of other workgroups --
+// splits publish without waiting for their stores, and the merger re-reads a
+// word until its tag is current.  The tag is the (row, head)'s generation
+// plus one; the merger advances the generation for the next launch.
+__device__ __forceinline__ void publish_tagged(uint64_t* p, uint32_t tag, float v) {
+    __hip_atomic_store(p, (static_cast<uint64_t>(tag) << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ float fetch(const float* p) {
-    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ uint64_t fetch_word(const uint64_t* p) {
+    return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Log-sum-exp merge of n split partials; threads d < 128 get output channel d.
-// Every load of the merge goes out at once -- the split statistics (thread j
-// loads split j) and thread d's accumulator column of the first kMergeInline
-// splits -- so up to kMergeInline splits cost one memory round trip and one
-// barrier.  Further splits (only when a caller forces small splits) are
-// fetched in a second pass.  Every thread reduces the statistics in the same
-// order, so all agree on the maximum and the denominator.
+// Re-reads of a word before the merger gives up on it.  Every split it waits
+// for has already counted its arrival, so it is resident and its store is in
+// flight; the bound only keeps a fault in this protocol from hanging the GPU.
+constexpr uint32_t kSpinLimit = 1u << 22;
+
+__device__ __forceinline__ bool current(uint64_t w, uint32_t tag) { return static_cast<uint32_t>(w >> 32) == tag; }
+
+// The value of the word at p (first read w), re-read until it carries `tag`;
+// NaN (which then shows in the output) if the bound runs out.
+__device__ __forceinline__ float tagged_value(const uint64_t* p, uint64_t w, uint32_t tag) {
+    for (uint32_t spin = 0; !current(w, tag); ++spin) {
+        if (spin == kSpinLimit) return __builtin_nanf("");
+        __builtin_amdgcn_s_sleep(1);
+        w = fetch_word(p);
+    }
+    return __uint_as_float(static_cast<uint32_t>(w));
+}
+
+// Log-sum-exp merge of a head's n split partials by the split `own`, which
+// holds its own (m, l, o) in registers; threads d < 128 get output channel d.
+// Up to kMergeInline splits every thread issues all of its reads at once --
+// each split's m and l (the same words in every lane) and its own channel of
+// each split's acc -- and needs no barrier.  More splits (only when a caller
+// forces small splits) take a second, looped pass with the statistics staged
+// through LDS.  The terms are summed in split order whichever split merges,
+// so the result does not depend on the arrival order.
 constexpr int kMergeInline = 8;
 
-__device__ __forceinline__ float merge_partials(const float* part, int n) {
-    const int d = threadIdx.x;
-    __shared__ float s_m[kMaxSplits], s_l[kMaxSplits];
-    float col[kMergeInline];
-    if (d < n) {
-        s_m[d] = fetch(part + d * kPartialStride);
-        s_l[d] = fetch(part + d * kPartialStride + 1);
-    }
+__device__ __forceinline__ float merge_partials(const uint64_t* slots, int n, int own, uint32_t tag, float own_m,
+                                                float own_l, float own_o) {
+    // Inline: called by waves 0-1 only.  Looped: by every wave (it stages the
+    // statistics through LDS behind a barrier); lanes past 127 read channel
+    // 127 and their result is unused.
+    const int d = min(static_cast<int>(threadIdx.x), kHeadDim - 1);
+    if (n <= kMergeInline) {
+        // Own words count as current (tag | own bits): they are never read.
+        const uint64_t own_tag = static_cast<uint64_t>(tag) << 32;
+        uint64_t wm[kMergeInline], wl[kMergeInline], wo[kMergeInline];
 #pragma unroll
-    for (int j = 0; j < kMergeInline; ++j)
-        col[j] = (d < kHeadDim && j < n) ? fetch(part + j * kPartialStride + 4 + d) : 0.0f;
+        for (int j = 0; j < kMergeInline; ++j) {
+            wm[j] = own_tag | __float_as_uint(own_m);
+            wl[j] = own_tag | __float_as_uint(own_l);
+            wo[j] = own_tag | __float_as_uint(own_o);
+            if (j < n && j != own) {
+                const uint64_t* sl = slots + j * kSlotWords;
+                wm[j] = fetch_word(sl);
+                wl[j] = fetch_word(sl + 1);
+                wo[j] = fetch_word(sl + 2 + d);
+            }
+        }
+        // Words whose store had not landed yet are read again, all of them in
+        // one round trip per round.
+        for (uint32_t spin = 0;; ++spin) {
+            bool stale = false;
+#pragma unroll
+            for (int j = 0; j < kMergeInline; ++j)
+                stale |= !current(wm[j], tag) || !current(wl[j], tag) || !current(wo[j], tag);
+            if (!stale) break;
+            if (spin == kSpinLimit) {
+#pragma unroll
+                for (int j = 0; j < kMergeInline; ++j) wo[j] = own_tag | 0x7fc00000u;   // NaN shows in the output
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+            for (int j = 0; j < kMergeInline; ++j) {
+                const uint64_t* sl = slots + j * kSlotWords;
+                if (!current(wm[j], tag)) wm[j] = fetch_word(sl);
+                if (!current(wl[j], tag)) wl[j] = fetch_word(sl + 1);
+                if (!current(wo[j], tag)) wo[j] = fetch_word(sl + 2 + d);
+            }
+        }
+        float m[kMergeInline], l[kMergeInline], o[kMergeInline];
+#pragma unroll
+        for (int j = 0; j < kMergeInline; ++j) {
+            m[j] = __uint_as_float(static_cast<uint32_t>(wm[j]));
+            l[j] = __uint_as_float(static_cast<uint32_t>(wl[j]));
+            o[j] = __uint_as_float(static_cast<uint32_t>(wo[j]));
+        }
+        float mx = m[0];
+#pragma unroll
+        for (int j = 1; j < kMergeInline; ++j)
+            if (j < n) mx = fmaxf(mx, m[j]);
+        float den = 0.0f, num = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kMergeInline; ++j) {
+            if (j < n) {
+                const float w = fast_exp2(m[j] - mx);
+                den += w * l[j];
+                num += w * o[j];
+            }
+        }
+        return num / den;
+    }
+    __shared__ float s_m[kMaxSplits], s_l[kMaxSplits];
+    const int t = threadIdx.x;
+    if (t < n) {
+        const uint64_t* sl = slots + t * kSlotWords;
+        s_m[t] = t == own ? own_m : tagged_value(sl, fetch_word(sl), tag);
+        s_l[t] = t == own ? own_l : tagged_value(sl + 1, fetch_word(sl + 1), tag);
+    }
     __syncthreads();
     float mx = s_m[0];
     for (int j = 1; j < n; ++j) mx = fmaxf(mx, s_m[j]);
     float den = 0.0f, num = 0.0f;
-#pragma unroll
-    for (int j = 0; j < kMergeInline; ++j) {
-        if (j < n) {
-            const float w = fast_exp2(s_m[j] - mx);
-            den += w * s_l[j];
-            num += w * col[j];
-        }
-    }
-    for (int j = kMergeInline; j < n; ++j) {
+    for (int j = 0; j < n; ++j) {
+        const uint64_t* sl = slots + j * kSlotWords + 2 + d;
         const float w = fast_exp2(s_m[j] - mx);
         den += w * s_l[j];
-        if (d < kHeadDim) num += w * fetch(part + j * kPartialStride + 4 + d);
+        num += w * (j == own ? own_o : tagged_value(sl, fetch_word(sl), tag));
     }
     return num / den;
 }
@@ -335,6 +437,12 @@ __global__ __launch_bounds__(WAVES * 64) void step_kernel(StepArgs a) {
     // and discards it: every path then has the same loads in flight.
     BlockLoads bl;
     issue_block(pr, t_first < t_stop ? t_first : t_begin, bl);
+    // The (row, head)'s arrival word, for the tag of a split partial.  Read
+    // on every path (unused by a head held by one split): a load under a
+    // branch would make the compiler wait for the block at the join.
+    const size_t head_row = static_cast<size_t>(b) * kHeads + h;
+    uint64_t* arrival = a.arrivals + head_row * kArrivalStride;
+    const uint64_t arrival_word = fetch_word(arrival);
 
     // Query: each lane converts and rotates its own pair, pre-scales it, and
     // gathers the 16 channels of its chunk c (pairs 8c..8c+7, held by lanes
@@ -396,33 +504,51 @@ __global__ __launch_bounds__(WAVES * 64) void step_kernel(StepArgs a) {
         }
     }
     if (nsplit == 1) {
-        finalize_head(a, b, h, o / l);
+        if (d < kHeadDim) finalize_head(a, b, h, o / l);
         return;
     }
 
-    // Several splits: publish this split's partial, count arrivals, and let
-    // the last split of the head merge all partials and finish the head.
-    const size_t head_row = static_cast<size_t>(b) * kHeads + h;
-    float* parts = a.partials + head_row * a.max_splits * kPartialStride;
+    // Several splits: count this split's arrival, publish its partial as
+    // tagged words without waiting for them to land, and let the split that
+    // arrives last merge the head's partials and finish the head.
+    const uint32_t tag = static_cast<uint32_t>(arrival_word >> 32) + 1u;
+    uint64_t* slots = a.partials + head_row * static_cast<size_t>(a.slot_stride) * kSlotWords;
+    // The count goes out from thread 128, in a wave that publishes nothing,
+    // so waiting for its result never waits for the stores of waves 0-1.
+    constexpr unsigned kCountThread = kHeadDim;
+    static_assert(kCountThread < kAttendWaves * 64, "the counting thread exists in every workgroup");
+    uint64_t before = 0;
+    if (threadIdx.x == kCountThread)
+        before = __hip_atomic_fetch_add(arrival, uint64_t(1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (d < kHeadDim) {
-        float* part = parts + static_cast<size_t>(split) * kPartialStride;
-        publish(part + 4 + d, o);
+        uint64_t* mine = slots + static_cast<size_t>(split) * kSlotWords;
+        publish_tagged(mine + 2 + d, tag, o);
         if (d == 0) {
-            publish(part, mx);
-            publish(part + 1, l);
+            publish_tagged(mine, tag, mx);
+            publish_tagged(mine + 1, tag, l);
         }
     }
-    __builtin_amdgcn_s_waitcnt(0);   // this thread's stores are complete before the barrier
-    __syncthreads();
     __shared__ int s_last;
-    if (threadIdx.x == 0)
-        s_last = __hip_atomic_fetch_add(a.counters + head_row * kCounterStride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                 static_cast<unsigned>(nsplit - 1);
+    if (threadIdx.x == kCountThread) s_last = static_cast<uint32_t>(before) == static_cast<uint32_t>(nsplit - 1);
     __syncthreads();
-    if (!s_last) return;
-    finalize_head(a, b, h, merge_partials(parts, nsplit));
-    if (threadIdx.x == 0)   // ready for the next launch
-        __hip_atomic_store(a.counters + head_row * kCounterStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // Only waves 0-1 (the output channels) merge and finish, except that the
+    // looped merge of more than kMergeInline splits needs every wave at its barrier.
+    if (!s_last || (nsplit <= kMergeInline && d >= kHeadDim)) return;
+    const float merged = merge_partials(slots, nsplit, split, tag, mx, l, o);
+    if (d >= kHeadDim) return;
+    finalize_head(a, b, h, merged);
+    // Every split has counted its arrival and its words have been read: reset
+    // the count and advance the generation for the next launch.  Tags run
+    // over 1 .. 2^32-1; when they wrap, the head's slots are cleared first
+    // (tag 0 is never current), so no word left from 2^32-1 launches ago can
+    // pass for a current one.
+    if (tag == 0xffffffffu) {
+        for (int i = d; i < a.slot_stride * kSlotWords; i += kHeadDim)
+            __hip_atomic_store(slots + i, uint64_t(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (d == 0)
+        __hip_atomic_store(arrival, static_cast<uint64_t>(tag == 0xffffffffu ? 0u : tag) << 32, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------- utilities

@@ -4,11 +4,11 @@ allocating one (swiftkv_attention_f32), through the C ABI.
 Two caches are filled identically; each call runs once through each entry on
 its own cache, and outputs, A14/E8M0 words and every appended row must be
 equal bit for bit.  Two calls in a row: the first a batch of 12 at ragged
-positions with forced 256-token splits (the per-GPU workspace holds the
-partials of 12 x 32 heads x up to 16 splits), the second smaller -- one
-sequence with the heuristic's 8 splits -- so the second call runs on what the
-first left in the shared workspace.  A call whose partials exceed the
-workspace is refused before any work is enqueued.
+positions with forced 512-token splits (up to 8 per head, what the per-GPU
+workspace holds), the second smaller -- one sequence with the heuristic's 8
+splits -- so the second call runs on what the first left in the shared
+workspace.  A call that would split a head more ways than the workspace
+holds is refused before any work is enqueued.
 """
 import ctypes as C
 import sys
@@ -44,7 +44,7 @@ def test_noalloc_entry_matches_the_allocating_entry(skv, ctx):
     aqs = [ctx.alloc(12 * 128 * 56) for _ in range(2)]
     ass = [ctx.alloc(12 * 128) for _ in range(2)]
     rng = np.random.default_rng(517)
-    calls = [(rng.integers(300, 4096, 12).astype(np.int32), 256), (np.array([4095], np.int32), 0)]
+    calls = [(rng.integers(300, 4096, 12).astype(np.int32), 512), (np.array([4095], np.int32), 0)]
     try:
         for n, (positions, split) in enumerate(calls):
             B = positions.size
@@ -67,19 +67,15 @@ def test_noalloc_entry_matches_the_allocating_entry(skv, ctx):
                 for h in (0, 13, 31):
                     x, y = caches[0].read(b, 0, h, p, 1), caches[1].read(b, 0, h, p, 1)
                     assert all(np.array_equal(u, w) for u, w in zip(x, y)), f"appended row, seq {b} head {h}"
-        # 256 sequences x 32 heads x 2 splits x 528 B = 8.65 MB > 8 MiB: refused, nothing enqueued
-        ctx.set_split_tokens(0)
-        big = skv.KVCache(ctx, layers=1, max_batch=256, max_seq_len=2048)
-        wide = [ctx.alloc(256 * 4096 * 4) for _ in range(3)]
-        out_w, aq_w, as_w = ctx.alloc(256 * 4096 * 4), ctx.alloc(256 * 128 * 56), ctx.alloc(256 * 128)
-        ctx.set_split_tokens(1024)
-        rc = _call(skv, L.swiftkv_attention_f32_noalloc, ctx, wide, big, lut, aq_w, as_w,
-                   np.full(256, 2047, np.int32), out_w)
+        # 256-token splits at position 4095: 16 splits per head, more than the workspace holds; refused
+        ctx.set_split_tokens(256)
+        before = outs[1].download(np.uint32, (12, 4096))
+        rc = _call(skv, L.swiftkv_attention_f32_noalloc, ctx, bufs, caches[1], lut, aqs[1], ass[1],
+                   np.array([4095], np.int32), outs[1])
         assert rc == skv.ERANGE and b"allocation-free" in L.swiftkv_last_error()
         ctx.set_split_tokens(0)
-        for x in wide + [out_w, aq_w, as_w]:
-            x.free()
-        big.close()
+        ctx.synchronize()
+        assert np.array_equal(outs[1].download(np.uint32, (12, 4096)), before), "a refused call wrote its output"
         # host-memory I/O mode stages through an allocated buffer: refused
         ctx.set_host_io(True)
         try:
