@@ -52,19 +52,71 @@ constexpr float kScoreScale = (1.0f / 11.313708498984761f) * 1.4426950408889634f
 // (streaming reads reach ~88% of HBM peak this way versus ~78% with
 // default-policy loads).
 
-// 16 int8 codes of one dwordx4 times 16 query values.
-__device__ __forceinline__ float dot16(const float* q, v4i w) {
-    const int32_t d[4] = {w[0], w[1], w[2], w[3]};
-    float acc = 0.0f;
+// The rotated query of a lane's 16-channel chunk as three signed-byte limbs:
+// m_c = q'_c / 2^E rounded, m_c = l0 + 2^8 l1 + 2^16 l2, with the chunk's
+// shift E = max(0, msb(max_c |q'_c|) - 21), so |m_c| <= 2^22 and l2 stays
+// within +-64.  The K dot product is then four signed-byte v_dot4 per limb
+// against the int8 codes, exact in integers; only its conversion to float
+// rounds.  For |q| below 16 (Q15.17 words below 2^21) E = 0 and the products
+// are the exact ones; above, m keeps 22 significant bits.  `scale` =
+// 2^(E-17) * kScoreScale turns the integer dot into the log2-domain score.
+struct QueryChunk {
+    int32_t w[3][4];   // limb k of channels 4j .. 4j+3, one byte each, in dword j
+    float scale;
+};
+
+// Lane l holds the rotated pair (q0, q1) = channels (2l, 2l+1), so chunk c
+// (channels 16c .. 16c+15) lives in lanes 8c .. 8c+7 and is consumed by the
+// lanes with lane & 7 == c.  Each lane splits its own pair, with the shift of
+// its chunk (a DPP maximum over its octet); two neighbouring lanes join their
+// 16-bit limb halves, and each consumer reads its four dwords per limb.
+__device__ __forceinline__ QueryChunk chunk_limbs(int32_t q0, int32_t q1, int c) {
+    uint32_t mx = max(magnitude(q0), magnitude(q1));
+    mx = max(mx, dpp_u<kDppQuadXor1>(mx));
+    mx = max(mx, dpp_u<kDppQuadXor2>(mx));
+    mx = max(mx, dpp_u<kDppHalfMirror>(mx));
+    const int msb = mx ? 31 - static_cast<int>(__clz(mx)) : 0;
+    const int e = max(0, msb - 21);
+    uint32_t half[3] = {0u, 0u, 0u};
+    const int32_t pair[2] = {q0, q1};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-#pragma unroll
-        for (int byte = 0; byte < 4; ++byte) {
-            const float code = static_cast<float>(static_cast<int8_t>(d[j] >> (8 * byte)));
-            acc = __builtin_fmaf(q[4 * j + byte], code, acc);
-        }
+    for (int i = 0; i < 2; ++i) {
+        const int32_t v = pair[i];
+        const int32_t m = e ? (v >> e) + ((v >> (e - 1)) & 1) : v;   // half up; |m| <= 2^22
+        const int32_t l0 = static_cast<int8_t>(static_cast<uint8_t>(m));
+        const int32_t r = (m - l0) >> 8;
+        const int32_t l1 = static_cast<int8_t>(static_cast<uint8_t>(r));
+        const int32_t l2 = (r - l1) >> 8;
+        half[0] |= static_cast<uint32_t>(static_cast<uint8_t>(l0)) << (8 * i);
+        half[1] |= static_cast<uint32_t>(static_cast<uint8_t>(l1)) << (8 * i);
+        half[2] |= static_cast<uint32_t>(static_cast<uint8_t>(l2)) << (8 * i);
     }
-    return acc;
+    QueryChunk Q;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        // even lanes 2p: channels 4p .. 4p+3 of their octet's chunk (valid at even lanes)
+        const uint32_t dword = half[k] | (dpp_u<kDppQuadXor1>(half[k]) << 16);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) Q.w[k][j] = static_cast<int32_t>(__shfl(dword, 8 * c + 2 * j));
+    }
+    Q.scale = ldexpf(kScoreScale, __shfl(e, 8 * c) - 17);
+    return Q;
+}
+
+// 16 int8 codes of one dwordx4 times the chunk's query, as float (before
+// the chunk and token scales): per limb the exact sum of 16 byte products
+// (|sum| <= 16 * 128 * 128), limbs 0 and 1 combined exactly in 32 bits.
+__device__ __forceinline__ float kdot16(const QueryChunk& Q, v4i w) {
+    int32_t s[3];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        int32_t acc = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_sdot4(Q.w[k][j], w[j], acc, false);
+        s[k] = acc;
+    }
+    const int32_t low = s[0] + s[1] * 256;   // |low| < 2^27
+    return __builtin_fmaf(65536.0f, static_cast<float>(s[2]), static_cast<float>(low));
 }
 
 __device__ __forceinline__ void axpy16(float* acc, float w, v4i v) {
@@ -133,13 +185,13 @@ __device__ __forceinline__ void issue_block(const PageReader& pr, int t0, BlockL
 // Online-softmax update with one block [t0, t0+64); MASKED blocks drop
 // tokens >= t_stop.
 template <bool MASKED>
-__device__ __forceinline__ void consume_block(const BlockLoads& bl, const float* qf, int t0, int t_stop, int r,
+__device__ __forceinline__ void consume_block(const BlockLoads& bl, const QueryChunk& Q, int t0, int t_stop, int r,
                                               float& m_run, float& l_run, float* acc) {
     float s[8];
     float blk = -INFINITY;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        s[i] = octet_sum(dot16(qf, bl.k[i]) * bl.s[i][0]);
+        s[i] = octet_sum(kdot16(Q, bl.k[i]) * (Q.scale * bl.s[i][0]));
         if (MASKED && t0 + 8 * i + r >= t_stop) s[i] = -INFINITY;
         blk = fmaxf(blk, s[i]);
     }
@@ -165,7 +217,7 @@ __device__ __forceinline__ void consume_block(const BlockLoads& bl, const float*
 // of the first block into `bl` (so its prologue overlaps them).  On return
 // every lane holds the wave's (m, l) and, for its chunk c, acc[16] summed
 // over the 8 rows.
-__device__ __forceinline__ void scan_range(const PageReader& pr, BlockLoads& bl, const float* qf, int t0,
+__device__ __forceinline__ void scan_range(const PageReader& pr, BlockLoads& bl, const QueryChunk& Q, int t0,
                                            int t_stop, int stride, int r, float& m_run, float& l_run,
                                            float* acc) {
     m_run = -INFINITY;
@@ -177,11 +229,11 @@ __device__ __forceinline__ void scan_range(const PageReader& pr, BlockLoads& bl,
     bool first = true;
     for (; t0 + kBlockTokens <= t_stop; t0 += stride, first = false) {
         if (!first) issue_block(pr, t0, bl);
-        consume_block<false>(bl, qf, t0, t_stop, r, m_run, l_run, acc);
+        consume_block<false>(bl, Q, t0, t_stop, r, m_run, l_run, acc);
     }
     if (t0 < t_stop) {
         if (!first) issue_block(pr, t0, bl);
-        consume_block<true>(bl, qf, t0, t_stop, r, m_run, l_run, acc);
+        consume_block<true>(bl, Q, t0, t_stop, r, m_run, l_run, acc);
     }
     l_run = across_octets_sum(l_run);
 #pragma unroll
@@ -444,27 +496,22 @@ __global__ __launch_bounds__(WAVES * 64) void step_kernel(StepArgs a) {
     uint64_t* arrival = a.arrivals + head_row * kArrivalStride;
     const uint64_t arrival_word = fetch_word(arrival);
 
-    // Query: each lane converts and rotates its own pair, pre-scales it, and
-    // gathers the 16 channels of its chunk c (pairs 8c..8c+7, held by lanes
-    // 8c..8c+7).  The new row's k is rotated and v converted here too, which
-    // frees the raw row registers before the scan.
+    // Query: each lane converts and rotates its own pair and splits it into
+    // byte limbs; each lane then gathers the limbs of its chunk c.  The new
+    // row's k is rotated and v converted here too, which frees the raw row
+    // registers before the scan.
     const int2 qi = in_to_q17<IN>(row_q);
     int32_t q0, q1;
     rope_pair(qi.x, qi.y, row_cs, q0, q1);
     const float qs0 = (static_cast<float>(q0) * 0x1p-17f) * kScoreScale;
     const float qs1 = (static_cast<float>(q1) * 0x1p-17f) * kScoreScale;
-    float qf[16];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        qf[2 * j] = __shfl(qs0, 8 * c + j);
-        qf[2 * j + 1] = __shfl(qs1, 8 * c + j);
-    }
+    const QueryChunk Q = chunk_limbs(q0, q1, c);
     const int2 ki = in_to_q17<IN>(row_k), vi = in_to_q17<IN>(row_v);
     int32_t k0, k1;
     rope_pair(ki.x, ki.y, row_cs, k0, k1);
 
     float m_run, l_run, acc[16];
-    scan_range(pr, bl, qf, t_first, t_stop, WAVES * kBlockTokens, r, m_run, l_run, acc);
+    scan_range(pr, bl, Q, t_first, t_stop, WAVES * kBlockTokens, r, m_run, l_run, acc);
 
     // The new row: quantize, append; forward (k^ . q', v^) into the merge as
     // one more partial.
