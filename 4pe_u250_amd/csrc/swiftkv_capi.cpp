@@ -286,7 +286,7 @@ int upload_lut(swiftkv_context* ctx, std::vector<int2>&& host, int32_t positions
 }
 
 // Tokens per split.  A launch runs best when it fills one residency round:
-// one 8-wave workgroup per CU (step_waves picks 8 waves for such launches),
+// one 16-wave workgroup per CU (step_waves picks 16 waves for such launches),
 // or step_per_cu 4-wave workgroups per CU.  So
 //   batch x 32 heads <= CUs:  splits = CUs / heads (at most 8);
 //   otherwise:                splits = step_per_cu x CUs / heads (at least 1),
@@ -322,15 +322,16 @@ int32_t choose_split(const swiftkv_context* ctx, const int32_t* positions, int32
     return static_cast<int32_t>(std::min<int64_t>(quanta * kSplitQuantum, kMaxSeq));
 }
 
-// Waves per workgroup.  A launch of at most one 8-wave workgroup per CU
-// whose splits are whole multiples of 512 tokens runs 8 waves per workgroup:
-// each wave holds half the blocks and two share a SIMD, which hides more of
-// the memory latency (batch 1 at context 4096: 12.3 against 13.2 us/layer).
-// Larger launches fill the machine either way and keep 4 waves, so more
-// workgroups stay resident per CU.
+// Waves per workgroup.  A launch of at most one workgroup per CU whose
+// splits are whole multiples of 512 tokens runs 16 waves per workgroup on
+// 32-token blocks: four waves share a SIMD and each holds half a block, so
+// less math is left when the last data arrives (32 layers at context 4096:
+// batch 2 17.1 against 17.6 us/layer with 8 waves on 64-token blocks,
+// batch 8 50.6 against 51.0; batch 1 unchanged).  Larger launches fill the
+// machine either way and keep 4 waves, so more workgroups stay resident per CU.
 int step_waves(const swiftkv_context* ctx, int32_t grid_splits, int32_t batch, int32_t split_tokens) {
     const int64_t workgroups = static_cast<int64_t>(grid_splits) * kHeads * batch;
-    const bool wide = workgroups <= ctx->cus && split_tokens % (kWideWaves * kBlockTokens) == 0;
+    const bool wide = workgroups <= ctx->cus && split_tokens % kWideRoundTokens == 0;
     return wide ? kWideWaves : kAttendWaves;
 }
 

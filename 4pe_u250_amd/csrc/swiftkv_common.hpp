@@ -27,11 +27,15 @@ constexpr int kA14WordBytes = 56;                // ap_uint<448>: 32 x 14-bit la
 // Split-context work: a workgroup of kAttendWaves wavefronts scans a range of
 // split_tokens tokens; each wave takes 64-token blocks round-robin.
 constexpr int kAttendWaves = 4;
-// Launches that fit one residency round of 8-wave workgroups (one per CU)
-// with splits of a multiple of 512 tokens use 8 waves: each wave then holds
-// fewer blocks and two waves share a SIMD to overlap the math.
-constexpr int kWideWaves = 8;
 constexpr int kBlockTokens = 64;
+// Launches that fit one residency round of workgroups of one per CU, with
+// splits of a multiple of 512 tokens, use 16 waves on 32-token blocks: four
+// waves share a SIMD and each holds half a block, so less of the math is
+// left when the last data arrives (123 VGPRs, within the 128 that four
+// resident waves per SIMD allow).
+constexpr int kWideWaves = 16;
+constexpr int kWideBlockTokens = 32;
+constexpr int kWideRoundTokens = kWideWaves * kWideBlockTokens;   // 512
 constexpr int kSplitQuantum = kAttendWaves * kBlockTokens;   // 256
 constexpr int kMaxSeq = 32768;                   // longest cache this build accepts
 constexpr int kMaxSplits = kMaxSeq / kSplitQuantum;   // 128 partials per (sequence, head)
@@ -130,7 +134,7 @@ constexpr size_t kNoAllocScratchBytes = kNoAllocCounterBytes + kNoAllocPartialBy
 
 // Launchers (swiftkv_kernels.hip).
 // waves: kAttendWaves, or kWideWaves when a.split_tokens is a multiple of
-// kWideWaves * kBlockTokens.
+// kWideRoundTokens.
 hipError_t launch_step(const StepArgs& a, int grid_splits, int waves, InputFormat in, hipStream_t s);
 // Workgroups of the 4-wave step kernel one CU holds at once (0 on error).
 int step_workgroups_per_cu();

@@ -2,8 +2,9 @@
 // stage.
 //
 // step kernel (one launch per decode step and layer), grid (splits, 32 heads,
-// batch rows) of 4-wave workgroups (8 waves when the launch has at most one
-// workgroup per CU and 512-token-multiple splits); workgroup (j, h, z) owns tokens
+// batch rows) of 4-wave workgroups on 64-token blocks (16 waves on 32-token
+// blocks when the launch has at most one workgroup per CU and
+// 512-token-multiple splits); workgroup (j, h, z) owns tokens
 // [j*C, min((j+1)*C, position+1)) of head h of the sequence that row z names
 // (rows come longest first, so a ragged batch does not end on long heads):
 //   1. every lane loads its channel pair of the new row's q/k/v (Q15.17,
@@ -156,23 +157,26 @@ __device__ __forceinline__ PageReader make_reader(const int8_t* page, int64_t ca
     return pr;
 }
 
-// The 24 loads of one 64-token block: 8 x 16 B of K codes, 8 x 8 B of scale
-// pairs, 8 x 16 B of V codes per lane.
+// The loads of one block of 8 * NI tokens (NI rows per lane): NI x 16 B of K
+// codes, NI x 8 B of scale pairs, NI x 16 B of V codes per lane -- 24 loads
+// for a 64-token block.
+template <int NI>
 struct BlockLoads {
-    v4i k[8], v[8];
-    v2f s[8];
+    v4i k[NI], v[NI];
+    v2f s[NI];
 };
 
-__device__ __forceinline__ void issue_block(const PageReader& pr, int t0, BlockLoads& bl) {
+template <int NI>
+__device__ __forceinline__ void issue_block(const PageReader& pr, int t0, BlockLoads<NI>& bl) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < NI; ++i) {
         const int32_t tok = t0 + 8 * i;
         bl.k[i] = __builtin_amdgcn_raw_buffer_load_b128(pr.rsrc, pr.k_lane, tok * kCodeBytes, kNontemporal);
         bl.s[i] = __builtin_bit_cast(v2f, __builtin_amdgcn_raw_buffer_load_b64(pr.rsrc, pr.s_lane,
                                                                                 tok * kScaleBytes, kNontemporal));
     }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < NI; ++i) {
         const int32_t tok = t0 + 8 * i;
         bl.v[i] = __builtin_amdgcn_raw_buffer_load_b128(pr.rsrc, pr.v_lane, tok * kCodeBytes, kNontemporal);
     }
@@ -182,15 +186,15 @@ __device__ __forceinline__ void issue_block(const PageReader& pr, int t0, BlockL
     __builtin_amdgcn_sched_barrier(0);
 }
 
-// Online-softmax update with one block [t0, t0+64); MASKED blocks drop
+// Online-softmax update with one block [t0, t0 + 8 * NI); MASKED blocks drop
 // tokens >= t_stop.
-template <bool MASKED>
-__device__ __forceinline__ void consume_block(const BlockLoads& bl, const QueryChunk& Q, int t0, int t_stop, int r,
+template <bool MASKED, int NI>
+__device__ __forceinline__ void consume_block(const BlockLoads<NI>& bl, const QueryChunk& Q, int t0, int t_stop, int r,
                                               float& m_run, float& l_run, float* acc) {
-    float s[8];
+    float s[NI];
     float blk = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < NI; ++i) {
         s[i] = octet_sum(kdot16(Q, bl.k[i]) * (Q.scale * bl.s[i][0]));
         if (MASKED && t0 + 8 * i + r >= t_stop) s[i] = -INFINITY;
         blk = fmaxf(blk, s[i]);
@@ -203,7 +207,7 @@ __device__ __forceinline__ void consume_block(const BlockLoads& bl, const QueryC
 #pragma unroll
     for (int j = 0; j < 16; ++j) acc[j] *= alpha;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < NI; ++i) {
         float p = fast_exp2(s[i] - m_new);            // masked: 2^-inf = 0
         float w = p * bl.s[i][1];
         if (MASKED && t0 + 8 * i + r >= t_stop) w = 0.0f;   // never multiply a stale scale
@@ -212,12 +216,13 @@ __device__ __forceinline__ void consume_block(const BlockLoads& bl, const QueryC
     }
 }
 
-// One wave's online-softmax scan over the 64-token blocks t0, t0+stride, ...
+// One wave's online-softmax scan over the blocks of 8 * NI tokens t0, t0+stride, ...
 // below t_stop, lane layout (c, r); the caller has already issued the loads
 // of the first block into `bl` (so its prologue overlaps them).  On return
 // every lane holds the wave's (m, l) and, for its chunk c, acc[16] summed
 // over the 8 rows.
-__device__ __forceinline__ void scan_range(const PageReader& pr, BlockLoads& bl, const QueryChunk& Q, int t0,
+template <int NI>
+__device__ __forceinline__ void scan_range(const PageReader& pr, BlockLoads<NI>& bl, const QueryChunk& Q, int t0,
                                            int t_stop, int stride, int r, float& m_run, float& l_run,
                                            float* acc) {
     m_run = -INFINITY;
@@ -227,13 +232,13 @@ __device__ __forceinline__ void scan_range(const PageReader& pr, BlockLoads& bl,
     // Full blocks, then at most one partial tail block.  (Both variants in one
     // loop body would double the live VGPRs.)
     bool first = true;
-    for (; t0 + kBlockTokens <= t_stop; t0 += stride, first = false) {
+    for (; t0 + 8 * NI <= t_stop; t0 += stride, first = false) {
         if (!first) issue_block(pr, t0, bl);
-        consume_block<false>(bl, Q, t0, t_stop, r, m_run, l_run, acc);
+        consume_block<false, NI>(bl, Q, t0, t_stop, r, m_run, l_run, acc);
     }
     if (t0 < t_stop) {
         if (!first) issue_block(pr, t0, bl);
-        consume_block<true>(bl, Q, t0, t_stop, r, m_run, l_run, acc);
+        consume_block<true, NI>(bl, Q, t0, t_stop, r, m_run, l_run, acc);
     }
     l_run = across_octets_sum(l_run);
 #pragma unroll
@@ -448,6 +453,10 @@ __device__ __forceinline__ float merge_partials(const uint64_t* slots, int n, in
 // Grid (splits, 32 heads, batch), 256 threads; grid row z serves rows[z].
 template <int IN, int WAVES>
 __global__ __launch_bounds__(WAVES * 64) void step_kernel(StepArgs a) {
+    // Rows per lane in a block: 4-wave workgroups scan 64-token blocks (NI = 8),
+    // 16-wave workgroups 32-token blocks (NI = 4).
+    constexpr int NI = (WAVES == kWideWaves ? kWideBlockTokens : kBlockTokens) / 8;
+    constexpr int kBlk = 8 * NI;
     const uint32_t row = a.rows[blockIdx.z];
     const int split = blockIdx.x, h = blockIdx.y, b = static_cast<int>(row & 0xffu);
     const int pos = static_cast<int>(row >> 8);
@@ -483,11 +492,11 @@ __global__ __launch_bounds__(WAVES * 64) void step_kernel(StepArgs a) {
     const InPair<IN> row_k = load_in<IN>(a.k, row_elem, a.part_stride);
     const InPair<IN> row_v = load_in<IN>(a.v, row_elem, a.part_stride);
     const PageReader pr = make_reader(page, cap, c, r);
-    const int t_first = t_begin + wave * kBlockTokens;
+    const int t_first = t_begin + wave * kBlk;
     const int t_stop = owner ? pos : t_end;       // the new token is forwarded, not scanned
     // A wave with no tokens loads the split's first block (always in the page)
     // and discards it: every path then has the same loads in flight.
-    BlockLoads bl;
+    BlockLoads<NI> bl;
     issue_block(pr, t_first < t_stop ? t_first : t_begin, bl);
     // The (row, head)'s arrival word, for the tag of a split partial.  Read
     // on every path (unused by a head held by one split): a load under a
@@ -511,7 +520,7 @@ __global__ __launch_bounds__(WAVES * 64) void step_kernel(StepArgs a) {
     rope_pair(ki.x, ki.y, row_cs, k0, k1);
 
     float m_run, l_run, acc[16];
-    scan_range(pr, bl, Q, t_first, t_stop, WAVES * kBlockTokens, r, m_run, l_run, acc);
+    scan_range<NI>(pr, bl, Q, t_first, t_stop, WAVES * kBlk, r, m_run, l_run, acc);
 
     // The new row: quantize, append; forward (k^ . q', v^) into the merge as
     // one more partial.
@@ -696,7 +705,7 @@ int step_workgroups_per_cu() {
 hipError_t launch_step(const StepArgs& a, int grid_splits, int waves, InputFormat in, hipStream_t s) {
     const dim3 grid(grid_splits, kHeads, a.batch);
     if (waves == kAttendWaves) return launch_step_waves<kAttendWaves>(a, grid, in, s);
-    if (waves == kWideWaves && a.split_tokens % (kWideWaves * kBlockTokens) == 0)
+    if (waves == kWideWaves && a.split_tokens % kWideRoundTokens == 0)
         return launch_step_waves<kWideWaves>(a, grid, in, s);
     return hipErrorInvalidValue;
 }
