@@ -1,7 +1,8 @@
 """Build recipe for libswiftkv.so (gfx950) and the CPU oracle.
 
-    python 4pe_u250_amd/build.py          # library, host driver and oracle (+ oracle/_ref
-                                          # when the reference sources are present)
+    python 4pe_u250_amd/build.py          # library, host driver, the phase-stamp diagnostic
+                                          # library and the oracle (+ oracle/_ref when the
+                                          # reference sources are present)
 
 The library is compiled in-tree with hipcc for gfx950 only.  All HIP code is
 built with packed-FP32 instruction selection disabled.
@@ -56,6 +57,22 @@ def build_library(verbose: bool = False) -> str:
     return LIB
 
 
+STAMPS_LIB = os.path.join(PKG_DIR, "libswiftkv_stamps.so")
+
+
+def build_stamps(verbose: bool = False) -> str:
+    """The instrumented library for phase_stamps.py: the same sources with the
+    step kernel's s_memrealtime phase stamps compiled in (SWIFTKV_PHASE_STAMPS).
+    Diagnostics only; the product is libswiftkv.so."""
+    srcs = [os.path.join(CSRC, s) for s in SOURCES]
+    tmp = STAMPS_LIB + ".tmp"
+    out = _run([HIPCC, *HIP_FLAGS, "-DSWIFTKV_PHASE_STAMPS", "-I", os.path.join(REPO, "include"), *srcs, "-o", tmp])
+    if verbose and out.strip():
+        print(out)
+    os.replace(tmp, STAMPS_LIB)
+    return STAMPS_LIB
+
+
 def build_host(verbose: bool = False) -> str:
     """The native host driver: plain C++ over the C ABI, linked against the
     library next to it (run path $ORIGIN)."""
@@ -84,6 +101,7 @@ def main() -> int:
     build_oracle(verbose=True)
     print(build_library(verbose=True))
     print(build_host(verbose=True))
+    print(build_stamps(verbose=True))
     return 0
 
 

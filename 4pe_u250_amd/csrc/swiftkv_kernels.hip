@@ -37,6 +37,45 @@
 // once per device and the entry passes that address.
 static __device__ __align__(256) unsigned char scratch[swiftkv::kNoAllocScratchBytes];
 
+// Phase stamps (the instrumented build libswiftkv_stamps.so only, compiled
+// with SWIFTKV_PHASE_STAMPS): per workgroup of the step kernel, thread 0
+// records s_memrealtime (100 MHz) at entry, when wave 0's first loads have
+// all arrived (an added wait for them), after the workgroup's LDS merge,
+// when the arrival count is known, after the merge and after the epilogue;
+// lane 0 of every wave records when its first loads arrived and when its
+// scan ended.  The product library compiles every stamp away.
+#ifdef SWIFTKV_PHASE_STAMPS
+constexpr int kStampWorkgroups = 8192;
+constexpr int kStampSlots = 8;   // entry, first loads, LDS merge, arrival, merge, epilogue, flags, XCD
+__device__ unsigned long long g_phase_stamps[kStampWorkgroups * kStampSlots];
+__device__ unsigned long long g_wave_stamps[kStampWorkgroups * 16 * 2];
+#define SKV_STAMP_DECL unsigned long long skv_st[kStampSlots] = {0, 0, 0, 0, 0, 0, 0, 0}
+#define SKV_STAMP(i) do { if (threadIdx.x == 0) skv_st[i] = __builtin_amdgcn_s_memrealtime(); } while (0)
+#define SKV_STAMP_FLAG(f) do { skv_st[6] |= (f); } while (0)
+#define SKV_STAMP_WAIT() __builtin_amdgcn_s_waitcnt(0)
+#define SKV_WAVE_STAMP(k, t) do {                                                                   \
+        const size_t wg_ = (static_cast<size_t>(blockIdx.z) * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x; \
+        if ((threadIdx.x & 63) == 0 && wg_ < kStampWorkgroups)                                      \
+            g_wave_stamps[(wg_ * 16 + (threadIdx.x >> 6)) * 2 + (k)] = (t);                         \
+    } while (0)
+#define SKV_STAMP_FLUSH() do {                                                                      \
+        const size_t wg_ = (static_cast<size_t>(blockIdx.z) * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x; \
+        if (threadIdx.x == 0 && wg_ < kStampWorkgroups) {                                           \
+            unsigned xcc_;                                                                          \
+            asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc_));                    \
+            skv_st[7] = xcc_;                                                                       \
+            for (int i_ = 0; i_ < kStampSlots; ++i_) g_phase_stamps[wg_ * kStampSlots + i_] = skv_st[i_]; \
+        }                                                                                           \
+    } while (0)
+#else
+#define SKV_STAMP_DECL do {} while (0)
+#define SKV_STAMP(i) do {} while (0)
+#define SKV_STAMP_FLAG(f) do {} while (0)
+#define SKV_STAMP_WAIT() do {} while (0)
+#define SKV_WAVE_STAMP(k, t) do {} while (0)
+#define SKV_STAMP_FLUSH() do {} while (0)
+#endif
+
 namespace swiftkv {
 namespace {
 
@@ -457,13 +496,18 @@ __global__ __launch_bounds__(WAVES * 64) void step_kernel(StepArgs a) {
     // 16-wave workgroups 32-token blocks (NI = 4).
     constexpr int NI = (WAVES == kWideWaves ? kWideBlockTokens : kBlockTokens) / 8;
     constexpr int kBlk = 8 * NI;
+    SKV_STAMP_DECL;
+    SKV_STAMP(0);
     const uint32_t row = a.rows[blockIdx.z];
     const int split = blockIdx.x, h = blockIdx.y, b = static_cast<int>(row & 0xffu);
     const int pos = static_cast<int>(row >> 8);
     const int len = pos + 1;
     const int C = a.split_tokens;
     const int t_begin = split * C;
-    if (t_begin >= len) return;
+    if (t_begin >= len) {
+        SKV_STAMP_FLUSH();
+        return;
+    }
     const int t_end = min(t_begin + C, len);
     const int nsplit = (len + C - 1) / C;
     const bool owner = pos < t_end;               // this split holds the new token
@@ -509,6 +553,11 @@ __global__ __launch_bounds__(WAVES * 64) void step_kernel(StepArgs a) {
     // byte limbs; each lane then gathers the limbs of its chunk c.  The new
     // row's k is rotated and v converted here too, which frees the raw row
     // registers before the scan.
+    SKV_STAMP_WAIT();
+    SKV_STAMP(1);
+#ifdef SWIFTKV_PHASE_STAMPS
+    const unsigned long long skv_first = __builtin_amdgcn_s_memrealtime();
+#endif
     const int2 qi = in_to_q17<IN>(row_q);
     int32_t q0, q1;
     rope_pair(qi.x, qi.y, row_cs, q0, q1);
@@ -521,6 +570,10 @@ __global__ __launch_bounds__(WAVES * 64) void step_kernel(StepArgs a) {
 
     float m_run, l_run, acc[16];
     scan_range<NI>(pr, bl, Q, t_first, t_stop, WAVES * kBlk, r, m_run, l_run, acc);
+#ifdef SWIFTKV_PHASE_STAMPS
+    SKV_WAVE_STAMP(0, skv_first);
+    SKV_WAVE_STAMP(1, __builtin_amdgcn_s_memrealtime());
+#endif
 
     // The new row: quantize, append; forward (k^ . q', v^) into the merge as
     // one more partial.
@@ -546,6 +599,7 @@ __global__ __launch_bounds__(WAVES * 64) void step_kernel(StepArgs a) {
         }
     }
     __syncthreads();
+    SKV_STAMP(2);
 
     const int nparts = owner ? WAVES + 1 : WAVES;
     const int d = threadIdx.x;
@@ -561,6 +615,8 @@ __global__ __launch_bounds__(WAVES * 64) void step_kernel(StepArgs a) {
     }
     if (nsplit == 1) {
         if (d < kHeadDim) finalize_head(a, b, h, o / l);
+        SKV_STAMP(5);
+        SKV_STAMP_FLUSH();
         return;
     }
 
@@ -589,10 +645,19 @@ __global__ __launch_bounds__(WAVES * 64) void step_kernel(StepArgs a) {
     __syncthreads();
     // Only waves 0-1 (the output channels) merge and finish, except that the
     // looped merge of more than kMergeInline splits needs every wave at its barrier.
-    if (!s_last || (nsplit <= kMergeInline && d >= kHeadDim)) return;
+    SKV_STAMP(3);
+    SKV_STAMP_FLAG(2);
+    if (!s_last || (nsplit <= kMergeInline && d >= kHeadDim)) {
+        SKV_STAMP_FLUSH();
+        return;
+    }
     const float merged = merge_partials(slots, nsplit, split, tag, mx, l, o);
+    SKV_STAMP(4);
     if (d >= kHeadDim) return;
     finalize_head(a, b, h, merged);
+    SKV_STAMP(5);
+    SKV_STAMP_FLAG(1);
+    SKV_STAMP_FLUSH();
     // Every split has counted its arrival and its words have been read: reset
     // the count and advance the generation for the next launch.  Tags run
     // over 1 .. 2^32-1; when they wrap, the head's slots are cleared first
@@ -667,6 +732,21 @@ __global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* __restrict__ 
 }  // namespace
 
 // ---------------------------------------------------------------- launchers
+
+#ifdef SWIFTKV_PHASE_STAMPS
+// Copies the stamps of the last step launch (workgroups [0, 8192)): phase
+// [8192][8] then wave [8192][16][2] 64-bit words (instrumented build only,
+// not part of the C ABI).
+extern "C" int swiftkv_debug_phase_stamps(unsigned long long* phase, unsigned long long* wave) {
+    if (hipMemcpyFromSymbol(phase, HIP_SYMBOL(g_phase_stamps), sizeof(g_phase_stamps), 0, hipMemcpyDeviceToHost) !=
+        hipSuccess)
+        return -3;
+    return hipMemcpyFromSymbol(wave, HIP_SYMBOL(g_wave_stamps), sizeof(g_wave_stamps), 0, hipMemcpyDeviceToHost) ==
+                   hipSuccess
+               ? 0
+               : -3;
+}
+#endif
 
 hipError_t bind_noalloc_scratch(hipStream_t s, void** device_ptr) {
     static_assert(kNoAllocScratchBytes % 4 == 0 && kNoAllocCounterBytes % 256 == 0, "workspace layout");

@@ -1,0 +1,145 @@
+"""Phase breakdown of the decode-attention step kernel on the GPU.
+
+    python 4pe_u250_amd/phase_stamps.py [--batches 1,2,4] [--position 4095] [--layers 32] [--reps 10]
+
+Runs 32-layer decode steps through the instrumented build libswiftkv_stamps.so
+(built by build.py: the product sources with SWIFTKV_PHASE_STAMPS, whose step
+kernel records s_memrealtime, a 100 MHz clock, at its phase boundaries) and
+prints, per batch size, the phases of the last layer's launch in microseconds
+from the first workgroup's start, medians over the repetitions:
+  - start:       workgroup entry (spread of the dispatch);
+  - first loads: wave 0's first block and row loads all arrived (the build
+                 waits for them there, about 0.2 us later than the product);
+  - stream:      every wave's first-block arrival (p50, max);
+  - scan:        every wave's scan end (p50, max) and the scan time after its
+                 first block arrived;
+  - LDS merge:   the workgroup's waves merged;
+  - arrival:     a split workgroup's count taken (split heads only);
+  - merge:       the last split's fetch and log-sum-exp merge;
+  - epilogue:    FP32 row and A14/E8M0 words written;
+  - launch:      the event-timed time per layer minus the span from the first
+                 workgroup's start to the last one's end (dispatch, completion
+                 and the gap to the next launch).
+Diagnostics only: nothing here is the product path, and the product library
+compiles every stamp away.
+"""
+import argparse
+import ctypes as C
+import importlib
+import json
+import os
+import sys
+
+import numpy as np
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.dirname(PKG))
+STAMPS_LIB = os.path.join(PKG, "libswiftkv_stamps.so")
+WGS, SLOTS = 8192, 8
+TICK_US = 0.01   # s_memrealtime runs at 100 MHz
+
+
+def pct(x, q):
+    x = np.asarray(x, np.float64)
+    x = x[np.isfinite(x)]
+    return float(np.percentile(x, q)) if x.size else float("nan")
+
+
+def launch_phases(ph, wv, nwg):
+    """Phase times (us) of one launch from its stamps."""
+    ph = ph[:nwg].astype(np.int64)
+    wv = wv[:nwg].astype(np.int64)
+    t0 = ph[:, 0].min()
+    rel = lambda x: np.where(x > 0, (x - t0) * TICK_US, np.nan)
+    split = (ph[:, 6] & 2) != 0
+    merger = (ph[:, 6] & 1) != 0
+    entry, first, lds, arrive, merged, done = (rel(ph[:, i]) for i in range(6))
+    wd, we = rel(wv[:, :, 0]), rel(wv[:, :, 1])
+    end = np.fmax(np.where(np.isnan(done), -np.inf, done), np.where(np.isnan(arrive), -np.inf, arrive))
+    d = {"start_max": pct(entry, 100), "first_loads_p50": pct(first, 50), "first_loads_max": pct(first, 100),
+         "stream_p50": pct(wd, 50), "stream_max": pct(wd, 100),
+         "scan_end_p50": pct(we, 50), "scan_end_max": pct(we, 100), "scan_after_data_p50": pct(we - wd, 50),
+         "lds_merge_p50": pct(lds, 50), "lds_merge_max": pct(lds, 100), "span": float(np.max(end))}
+    if merger.any():
+        d.update({"arrival_p50": pct(arrive[split] - lds[split], 50),
+                  "merge_p50": pct(merged[merger] - arrive[merger], 50),
+                  "epilogue_p50": pct(done[merger] - merged[merger], 50),
+                  "last_lds_to_end": float(np.max(end) - np.nanmax(lds))})
+    else:
+        d.update({"epilogue_p50": pct(done - lds, 50), "last_lds_to_end": float(np.max(end) - np.nanmax(lds))})
+    return d
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--batches", default="1,2,4")
+    ap.add_argument("--position", type=int, default=4095)
+    ap.add_argument("--layers", type=int, default=32)
+    ap.add_argument("--reps", type=int, default=10)
+    ap.add_argument("--json", default=None, help="also write the medians here")
+    args = ap.parse_args()
+    if not os.path.exists(STAMPS_LIB):
+        raise SystemExit(f"{STAMPS_LIB} is missing: python 4pe_u250_amd/build.py")
+    skv = importlib.import_module("4pe_u250_amd")
+    skv.LIB_PATH = STAMPS_LIB
+    L = skv.lib()
+    L.swiftkv_debug_phase_stamps.argtypes = [C.c_void_p, C.c_void_p]
+    ctx = skv.Context(0)
+    out = {}
+    for batch in (int(x) for x in args.batches.split(",")):
+        layers, pos = args.layers, args.position
+        lut = skv.RopeLut.generate(ctx, max(pos + 1, 4096))
+        kv = skv.KVCache(ctx, layers=layers, max_batch=batch, max_seq_len=pos + 1)
+        kv.fill_synthetic(lut, ntok=pos, seed=5)
+        n = layers * batch * 4096
+        qkv = [ctx.alloc(n * 4) for _ in range(3)]
+        for i, b in enumerate(qkv):
+            ctx.fill_synthetic(b, n, 9, 100 + i)
+        o, aq, asc = ctx.alloc(batch * 4096 * 4), ctx.alloc(batch * 128 * 56), ctx.alloc(batch * 128)
+        positions = np.full(batch, pos, np.int32)
+        stride = batch * 4096 * 4
+
+        def step():
+            for layer in range(layers):
+                skv.swiftkv_attention(ctx, qkv[0].ptr + layer * stride, qkv[1].ptr + layer * stride,
+                                      qkv[2].ptr + layer * stride, kv, lut, aq, asc, layer, positions, o)
+
+        for _ in range(3):
+            step()
+        ctx.synchronize()
+        rows = []
+        ph = np.zeros((WGS, SLOTS), np.uint64)
+        wv = np.zeros((WGS, 16, 2), np.uint64)
+        for _ in range(args.reps):
+            ph[:] = 0
+            wv[:] = 0
+            ctx.timer_record(0)
+            step()
+            ctx.timer_record(1)
+            us_layer = 1000.0 * ctx.timer_elapsed_ms(0, 1) / layers
+            if L.swiftkv_debug_phase_stamps(ph.ctypes.data, wv.ctypes.data) != 0:
+                raise SystemExit("reading the stamps failed")
+            # workgroups of the last launch: stamps left by an earlier, larger
+            # launch are milliseconds older
+            live = (ph[:, 0] > 0) & (ph[:, 0] >= ph[:, 0].max() - np.uint64(100000))
+            nwg = int(live.sum())
+            d = launch_phases(ph[live], wv[live], nwg)
+            d["us_per_layer"] = us_layer
+            d["launch"] = us_layer - d["span"]
+            d["workgroups"] = nwg
+            rows.append(d)
+        med = {k: round(float(np.median([r[k] for r in rows])), 3) for k in rows[0]}
+        out[f"batch{batch}_position{pos}"] = med
+        print(f"batch {batch}, position {pos}, {layers} layers: " + json.dumps(med), flush=True)
+        for b in qkv + [o, aq, asc]:
+            b.free()
+        kv.close()
+        lut.close()
+    ctx.close()
+    if args.json:
+        with open(args.json, "w") as f:
+            json.dump(out, f, indent=1)
+
+
+if __name__ == "__main__":
+    main()
