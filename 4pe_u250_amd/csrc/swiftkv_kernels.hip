@@ -524,17 +524,25 @@ __global__ __launch_bounds__(WAVES * 64) void step_kernel(StepArgs a) {
     __shared__ float s_m[WAVES + 1], s_l[WAVES + 1];
 
     // Loads go out before any math, in the order they are needed: this
-    // lane's channel pair (2*lane, 2*lane+1) of the new row's q, k, v and its
-    // RoPE pair, then the first cache block.  The conversions below wait only
-    // for the row loads (vector loads retire in issue order), so they overlap
-    // the block's flight.  All of them are unconditional and in bounds: a
-    // load under a branch makes the compiler wait for the prefetched block at
-    // the join.
+    // lane's channel pair (2*lane, 2*lane+1) of the new row's RoPE pair and
+    // q -- and of its k and v in the one wave that appends the row -- then
+    // the first cache block.  The conversions below wait only for the row
+    // loads (vector loads retire in issue order), so they overlap the block's
+    // flight.  The block loads are unconditional and in bounds: a block load
+    // under a branch makes the compiler wait for it at the join.  The k/v
+    // loads are under a wave-uniform branch ahead of the block, so every wait
+    // for a later load keeps its count on both paths.  (Loading q once per
+    // workgroup and handing it to the other waves through LDS measured slower
+    // at batch 1: 12.5-12.9 against 11.7-11.9 us/layer.)
     const size_t row_elem = static_cast<size_t>(b) * kModelDim + h * kHeadDim + 2 * lane;
+    const bool appends = owner && wave == 0;       // this wave writes and forwards the new row
     const int2 row_cs = a.lut[static_cast<size_t>(pos) * kRopePairs + lane];
     const InPair<IN> row_q = load_in<IN>(a.q, row_elem, a.part_stride);
-    const InPair<IN> row_k = load_in<IN>(a.k, row_elem, a.part_stride);
-    const InPair<IN> row_v = load_in<IN>(a.v, row_elem, a.part_stride);
+    InPair<IN> row_k{}, row_v{};
+    if (appends) {
+        row_k = load_in<IN>(a.k, row_elem, a.part_stride);
+        row_v = load_in<IN>(a.v, row_elem, a.part_stride);
+    }
     const PageReader pr = make_reader(page, cap, c, r);
     const int t_first = t_begin + wave * kBlk;
     const int t_stop = owner ? pos : t_end;       // the new token is forwarded, not scanned
@@ -577,7 +585,7 @@ __global__ __launch_bounds__(WAVES * 64) void step_kernel(StepArgs a) {
 
     // The new row: quantize, append; forward (k^ . q', v^) into the merge as
     // one more partial.
-    if (owner && wave == 0) {
+    if (appends) {
         float kh0, kh1, vh0, vh1;
         append_row_dequant(page, a.kv.seq_cap, pos, lane, k0, k1, vi.x, vi.y, kh0, kh1, vh0, vh1);
         float sp = qs0 * kh0 + qs1 * kh1;
