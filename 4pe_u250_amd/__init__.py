@@ -66,6 +66,7 @@ _SIGNATURES = {
     "swiftkv_context_destroy": (C.c_int, [_vp]),
     "swiftkv_synchronize": (C.c_int, [_vp]),
     "swiftkv_set_split_tokens": (C.c_int, [_vp, _i32]),
+    "swiftkv_debug_set_split_generation": (C.c_int, [_vp, C.c_uint32, _i32]),
     "swiftkv_rope_lut_load": (C.c_int, [_vp, _vp, _sz, C.POINTER(_vp)]),
     "swiftkv_rope_lut_generate": (C.c_int, [_vp, _i32, C.c_double, C.POINTER(_vp)]),
     "swiftkv_rope_lut_destroy": (C.c_int, [_vp]),
@@ -219,6 +220,12 @@ class Context:
 
     def set_split_tokens(self, n: int) -> None:
         _check(lib().swiftkv_set_split_tokens(self.handle, int(n)))
+
+    def debug_set_split_generation(self, generation: int, noalloc: bool = False) -> None:
+        """Testing aid: set every generation of the split workspace (the
+        context's, or with noalloc this device's allocation-free one) and zero
+        its partial words, so launches can be run across the tag wrap."""
+        _check(lib().swiftkv_debug_set_split_generation(self.handle, int(generation), 1 if noalloc else 0))
 
     def set_host_io(self, enable: bool) -> None:
         """Host-memory I/O: step and append tensors are numpy arrays, staged

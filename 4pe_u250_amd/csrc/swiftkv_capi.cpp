@@ -95,8 +95,9 @@ struct swiftkv_context {
     int step_per_cu = 3;        // 4-wave step workgroups one CU holds at once
     hipStream_t stream = nullptr;
     int32_t split_tokens = 0;   // 0: heuristic
-    // split-context workspace: [partial_rows][32][partial_slots][kSlotWords]
-    // tagged words, zero-filled when allocated (tag 0 is never current)
+    // split-context workspace: [partial_rows][32] arrival words (kArrivalStride
+    // apart), then [partial_rows][32][partial_slots][kSlotWords] tagged words,
+    // zero-filled when allocated (generation 0; tag 0 is never current)
     uint64_t* partials = nullptr;
     int32_t partial_rows = 0;
     int32_t partial_slots = 0;
@@ -105,7 +106,10 @@ struct swiftkv_context {
     // here, and released when the last graph is destroyed.
     int64_t graphs = 0;
     std::vector<void*> retired;
-    uint64_t* arrivals = nullptr;   // [kMaxBatchPerLaunch][32] arrival words (kArrivalStride apart)
+    // [kMaxBatchPerLaunch][32] arrival words (kArrivalStride apart), zero, for
+    // launches that split no head: the step reads its arrival word on every
+    // path but only a split head's merge writes one
+    uint64_t* arrivals = nullptr;
     uint8_t* scratch = nullptr;     // this device's allocation-free workspace (arrival words, then partials)
     // timing
     hipEvent_t timers[kTimerSlots] = {};
@@ -198,10 +202,20 @@ int ensure(swiftkv_context* ctx, T*& ptr, size_t& have, size_t need) {
     return SWIFTKV_OK;
 }
 
+// Words of a split workspace for `rows` sequences: the arrival words, then
+// the partials of `slots` splits per (row, head).
+size_t arrival_words(int32_t rows) { return static_cast<size_t>(rows) * kHeads * kArrivalStride; }
+size_t workspace_words(int32_t rows, int32_t slots) {
+    return arrival_words(rows) + static_cast<size_t>(rows) * kHeads * slots * kSlotWords;
+}
+
 // The split workspace for a launch of `rows` sequences split `slots` ways.
 // The layout (rows, slots) stays fixed for the life of a buffer, so a word
 // left by an earlier launch sits where the same (row, head, split) wrote it,
-// with an older generation's tag; a new buffer is zero-filled.
+// with an older generation's tag; a new buffer is zero-filled.  Each buffer
+// carries its own arrival words: a buffer kept for a graph counts its own
+// generations, so the tag wrap that clears one buffer's slots can never let
+// another buffer's old words pass for current ones.
 int ensure_partials(swiftkv_context* ctx, int32_t rows, int32_t slots) {
     if (rows <= ctx->partial_rows && slots <= ctx->partial_slots) return SWIFTKV_OK;
     if (ctx->capturing)
@@ -219,7 +233,7 @@ int ensure_partials(swiftkv_context* ctx, int32_t rows, int32_t slots) {
         ctx->partials = nullptr;
         ctx->partial_rows = ctx->partial_slots = 0;
     }
-    const size_t bytes = sizeof(uint64_t) * new_rows * kHeads * new_slots * kSlotWords;
+    const size_t bytes = sizeof(uint64_t) * workspace_words(new_rows, new_slots);
     void* p = nullptr;
     if (hipMalloc(&p, bytes) != hipSuccess) return fail(SWIFTKV_ENOMEM, "hipMalloc of %zu bytes failed", bytes);
     const hipError_t e = hipMemsetAsync(p, 0, bytes, ctx->stream);
@@ -449,11 +463,15 @@ int run_step(swiftkv_context* ctx, const void* q, const void* k, const void* v, 
             a.arrivals = reinterpret_cast<uint64_t*>(ctx->scratch);
             a.partials = reinterpret_cast<uint64_t*>(ctx->scratch + kNoAllocCounterBytes);
             a.slot_stride = kFixedSlots;
-        } else {
-            if (grid_splits > 1 && (rc = ensure_partials(ctx, nb, grid_splits))) return rc;
-            a.arrivals = ctx->arrivals;
-            a.partials = ctx->partials;
+        } else if (grid_splits > 1) {
+            if ((rc = ensure_partials(ctx, nb, grid_splits))) return rc;
+            a.arrivals = ctx->partials;
+            a.partials = ctx->partials + arrival_words(ctx->partial_rows);
             a.slot_stride = ctx->partial_slots;
+        } else {
+            a.arrivals = ctx->arrivals;
+            a.partials = nullptr;   // no head of the launch is split
+            a.slot_stride = 0;
         }
         a.out = out + row0;
         a.act_q = act_q ? act_q + static_cast<size_t>(b0) * kHeads * kGroupsPerHead * SWIFTKV_A14_WORD_BYTES
@@ -674,6 +692,32 @@ int swiftkv_set_split_tokens(swiftkv_context* ctx, int32_t split_tokens) {
         return fail(SWIFTKV_EINVAL, "split_tokens %d must be 0 or a multiple of %d in [%d, %d]", split_tokens,
                     kSplitQuantum, kSplitQuantum, kMaxSplitTokens);
     ctx->split_tokens = split_tokens;
+    return ok();
+}
+
+int swiftkv_debug_set_split_generation(swiftkv_context* ctx, uint32_t generation, int32_t noalloc) {
+    if (!ctx) return fail(SWIFTKV_EINVAL, "null context");
+    int rc = not_capturing(ctx, "swiftkv_debug_set_split_generation");
+    if (rc) return rc;
+    if (generation == 0xffffffffu)
+        return fail(SWIFTKV_EINVAL, "generation 0xffffffff is reserved (a launch's tag is its generation + 1, and "
+                    "tags run over 1 .. 0xffffffff)");
+    if ((rc = set_device(ctx))) return rc;
+    uint64_t* base = nullptr;
+    int32_t rows = 0, slots = 0;
+    if (noalloc) {
+        base = reinterpret_cast<uint64_t*>(ctx->scratch);
+        rows = kMaxBatchPerLaunch;
+        slots = kFixedSlots;
+    } else {
+        base = ctx->partials;
+        rows = ctx->partial_rows;
+        slots = ctx->partial_slots;
+    }
+    if (!base) return ok();   // no split workspace yet: the first one starts at generation 0
+    const size_t arrivals = arrival_words(rows);
+    SKV_HIP(launch_fill_u64(base, arrivals, static_cast<uint64_t>(generation) << 32, ctx->stream));
+    SKV_HIP(launch_fill_u64(base + arrivals, workspace_words(rows, slots) - arrivals, 0, ctx->stream));
     return ok();
 }
 

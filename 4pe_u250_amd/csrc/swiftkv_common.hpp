@@ -91,9 +91,11 @@ struct StepArgs {
     int32_t split_tokens;     // multiple of kSplitQuantum
     int32_t slot_stride;      // split slots per (row, head) in `partials`, >= the launch's splits
     uint64_t* partials;       // [rows][32][slot_stride][kSlotWords] tagged words
-    // [256][32] arrival words, kArrivalStride apart: the generation of the
+    // [rows][32] arrival words, kArrivalStride apart: the generation of the
     // (row, head) in the upper half, this launch's arrivals (zero between
-    // launches) in the lower half
+    // launches) in the lower half.  Each split workspace holds its own, ahead
+    // of its partials, so the tags of one workspace never meet the words of
+    // another.
     uint64_t* arrivals;
     float* out;               // [batch][4096]
     uint8_t* act_q;           // [batch][128][56] or null
@@ -139,6 +141,8 @@ hipError_t launch_step(const StepArgs& a, int grid_splits, int waves, InputForma
 // Workgroups of the 4-wave step kernel one CU holds at once (0 on error).
 int step_workgroups_per_cu();
 hipError_t launch_append_bulk(const BulkArgs& a, bool q17, hipStream_t s);
+// p[0 .. n) = value, on stream s.
+hipError_t launch_fill_u64(uint64_t* p, size_t n, uint64_t value, hipStream_t s);
 // Device address of the allocation-free workspace on the current device,
 // zero-filled by a kernel on `s` (waits for it).  Call once per device.
 hipError_t bind_noalloc_scratch(hipStream_t s, void** device_ptr);

@@ -737,6 +737,11 @@ __global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* __restrict__ 
     for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = 0u;
 }
 
+__global__ __launch_bounds__(256) void fill_u64_kernel(uint64_t* __restrict__ p, size_t n, uint64_t value) {
+    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = value;
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------- launchers
@@ -767,6 +772,13 @@ hipError_t bind_noalloc_scratch(hipStream_t s, void** device_ptr) {
     if ((e = hipStreamSynchronize(s)) != hipSuccess) return e;
     *device_ptr = p;
     return hipSuccess;
+}
+
+hipError_t launch_fill_u64(uint64_t* p, size_t n, uint64_t value, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    const size_t blocks = std::min<size_t>((n + 255) / 256, 4096);
+    fill_u64_kernel<<<static_cast<unsigned>(blocks), 256, 0, s>>>(p, n, value);
+    return hipGetLastError();
 }
 
 template <int WAVES>

@@ -91,6 +91,18 @@ int swiftkv_synchronize(swiftkv_context* ctx);
 /* Tokens per split-context work item; 0 selects the built-in heuristic.
  * Must be 0 or a multiple of 256 in [256, 32768]. */
 int swiftkv_set_split_tokens(swiftkv_context* ctx, int32_t split_tokens);
+/* Testing aid with no counterpart in the reference.  A head split across
+ * workgroups is merged inside the launch through 64-bit words tagged with the
+ * (sequence row, head)'s generation + 1, which every launch that merges the
+ * head advances; tags run over 1 .. 0xffffffff and wrap to 1, clearing the
+ * head's words first.  This sets every generation of the context's split
+ * workspace (noalloc = 0) or of this device's allocation-free workspace
+ * (noalloc != 0) to `generation` and zeroes its partial words, on the context
+ * stream, so a test can run launches across the wrap without 2^32 of them.
+ * A context with no split workspace yet is left as it is (its first one
+ * starts at generation 0).  `generation` 0xffffffff is refused
+ * (SWIFTKV_EINVAL), and so is a call during graph capture (SWIFTKV_ESTATE). */
+int swiftkv_debug_set_split_generation(swiftkv_context* ctx, uint32_t generation, int32_t noalloc);
 
 /* --------------------------------------------------------------------------
  * RoPE table (kernel_HLS/swiftkv_attention.hpp:55-81; rope_lut.bin format of

@@ -62,3 +62,45 @@ def test_split_merge_is_bitwise_repeatable(skv, ctx, batch, position, split):
         b.free()
     kv.close()
     lut.close()
+
+
+@pytest.mark.parametrize("noalloc", [False, True], ids=["context_workspace", "noalloc_workspace"])
+def test_split_merge_across_the_tag_wrap(skv, ctx, noalloc):
+    """The merge's tags are the (row, head)'s generation + 1, 32 bits, and
+    wrap from 0xffffffff to 1 with the head's words cleared.  With every
+    generation set just below the wrap, six launches run with tags 0xfffffffd,
+    0xfffffffe, 0xffffffff, 1, 2, 3: each must give the bits of a launch far
+    from the wrap, on the context's split workspace and on the
+    allocation-free entry's."""
+    batch, position = 2, 4095     # 4 splits of 1024 tokens per head
+    entry = "allocation-free" if noalloc else "regular"
+    _note(f"case: tag wrap, batch {batch}, position {position}, {entry} entry")
+    lut = skv.RopeLut.generate(ctx, 4096)
+    kv = skv.KVCache(ctx, layers=1, max_batch=batch, max_seq_len=position + 1)
+    kv.fill_synthetic(lut, ntok=position, seed=77)
+    qkv = [ctx.alloc(batch * 4096 * 4) for _ in range(3)]
+    for i, b in enumerate(qkv):
+        ctx.fill_synthetic(b, batch * 4096, 78, 30 + i)
+    out, aq, asc = ctx.alloc(batch * 4096 * 4), ctx.alloc(batch * 128 * 56), ctx.alloc(batch * 128)
+    run = skv.swiftkv_attention_noalloc if noalloc else skv.swiftkv_attention
+    positions = np.full(batch, position, np.int32)
+
+    def launch():
+        run(ctx, qkv[0], qkv[1], qkv[2], kv, lut, aq, asc, 0, positions, out)
+        ctx.synchronize()
+        return (out.download(np.uint32, (batch * 4096,)), aq.download(np.uint8, (batch * 128 * 56,)),
+                asc.download(np.uint8, (batch * 128,)))
+
+    first = launch()
+    assert np.isfinite(first[0].view(np.float32)).all()
+    ctx.debug_set_split_generation(0xFFFFFFFC, noalloc)
+    for i, tag in enumerate([0xFFFFFFFD, 0xFFFFFFFE, 0xFFFFFFFF, 1, 2, 3]):
+        got = launch()
+        assert all(np.array_equal(g, f) for g, f in zip(got, first)), f"launch {i} (tag {tag:#x}) differs"
+        _note(f"  tag {tag:#x}: identical")
+    with pytest.raises(skv.SwiftKVError):
+        ctx.debug_set_split_generation(0xFFFFFFFF, noalloc)
+    for b in qkv + [out, aq, asc]:
+        b.free()
+    kv.close()
+    lut.close()
