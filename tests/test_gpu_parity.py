@@ -115,6 +115,30 @@ def test_randomized_configurations(skv, ctx, lut4096, rope_tables, case):
               dist=dist, outliers=outl, split=split, q17=q17)
 
 
+# Seeds whose shapes run the 16-wave launch (every one but 9501 and 9503,
+# which run 4-wave workgroups), with 1 to 8 splits per head.
+@pytest.mark.parametrize("seed", [9500, 9501, 9502, 9503, 9506, 9511, 9514, 9531])
+def test_randomized_small_batches(skv, ctx, lut4096, rope_tables, seed):
+    """Seeded random shapes for small launches (16 waves on 32-token blocks
+    when a launch has at most one workgroup per CU and its split is a
+    multiple of 512 tokens): batch 1..8, ragged positions up to 4095,
+    heuristic or forced split of 512 to 2048 tokens (or 768: 4 waves), FP32
+    or Q15.17 entry, N(0,1) or Student-t(3) data, with or without outlier
+    channels."""
+    case = seed - 9500
+    rng = np.random.default_rng(seed)
+    B = int(rng.integers(1, 9))
+    positions = [int(p) for p in rng.integers(0, 4096, B)]
+    split = int(rng.choice([0, 0, 512, 768, 1024, 1536, 2048]))
+    dist = "t3" if rng.random() < 0.5 else "normal"
+    outl = outlier_channels(9600 + case) if rng.random() < 0.5 else None
+    q17 = bool(rng.random() < 0.5)
+    _note(f"case {case}: batch {B}, positions {positions}, split {split}, {dist}, outliers {outl is not None}, "
+          f"q17 {q17}")
+    _scenario(skv, ctx, lut4096, rope_tables, positions, seed=9700 + 100 * case, dist=dist, outliers=outl,
+              split=split, q17=q17)
+
+
 @pytest.mark.parametrize("split", [0, 256])
 def test_rising_scores(skv, ctx, lut4096, rope_tables, split):
     """Keys growing along the query: the running maximum moves at most
