@@ -1015,6 +1015,8 @@ int swiftkv_append_tokens(swiftkv_context* ctx, const void* k, const void* v, in
                           int32_t seq, int32_t pos0, int32_t n) {
     if (!ctx) return fail(SWIFTKV_EINVAL, "null context");
     if (!k || !v) return fail(SWIFTKV_EINVAL, "null k/v pointer");
+    if (!ctx->host_io && ((reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v)) & 15u))
+        return fail(SWIFTKV_EINVAL, "k and v must be 16-byte aligned (the kernel reads four channels per lane)");
     if (!rope_lut || rope_lut->ctx != ctx) return fail(SWIFTKV_EINVAL, "rope_lut is null or belongs to another context");
     int rc = check_cache_range(ctx, kv_cache, seq, layer_index, 0, pos0, n);
     if (rc) return rc;

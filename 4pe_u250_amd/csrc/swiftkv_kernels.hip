@@ -682,36 +682,83 @@ __global__ __launch_bounds__(WAVES * 64) void step_kernel(StepArgs a) {
 
 // ---------------------------------------------------------------- utilities
 
-constexpr int kAppendTokens = 2;   // prefill rows per wave (their loads in flight together)
+// Prefill rows per wave: one instruction covers two token rows (lane l takes
+// channels 4(l & 31) .. 4(l & 31) + 3 of row l >> 5), and a wave takes
+// kAppendRounds such row pairs with all of their loads in flight together.
+constexpr int kAppendRounds = 1;
+constexpr int kAppendTokens = 2 * kAppendRounds;
 
-// Grid (ceil(n / kAppendTokens), 8): wave = head (4 per workgroup), each
-// wave kAppendTokens consecutive tokens.  All of the wave's loads (k, v and
-// the RoPE pair of every token) go out before any row is quantized, so a
-// wave keeps kAppendTokens rows in flight; tokens past n load the last token
-// and store nothing.
+template <bool Q17>
+__device__ __forceinline__ int4 load_quad(const void* base, size_t elem) {
+    if constexpr (Q17) {
+        return *reinterpret_cast<const int4*>(static_cast<const int32_t*>(base) + elem);
+    } else {
+        const float4 f = *reinterpret_cast<const float4*>(static_cast<const float*>(base) + elem);
+        return make_int4(f32_to_q17(f.x), f32_to_q17(f.y), f32_to_q17(f.z), f32_to_q17(f.w));
+    }
+}
+
+// Max over the 8 lanes of an aligned octet (one G32 group of a row when a
+// lane holds four channels); every lane gets it.
+__device__ __forceinline__ uint32_t octet_max_u(uint32_t x) {
+    x = max(x, dpp_u<kDppQuadXor1>(x));
+    x = max(x, dpp_u<kDppQuadXor2>(x));
+    return max(x, dpp_u<kDppHalfMirror>(x));
+}
+
+__device__ __forceinline__ uint32_t quad_codes(int4 r, uint32_t s) {
+    return g32_code_byte(r.x, s) | (g32_code_byte(r.y, s) << 8) | (g32_code_byte(r.z, s) << 16) |
+           (g32_code_byte(r.w, s) << 24);
+}
+
+__device__ __forceinline__ uint32_t quad_magnitude(int4 r) {
+    return max(max(magnitude(r.x), magnitude(r.y)), max(magnitude(r.z), magnitude(r.w)));
+}
+
+// Grid (ceil(n / kAppendTokens), 8): wave = head (4 per workgroup).  All of
+// a wave's loads (k, v and the RoPE pairs of every row) go out before any
+// row is quantized; rows past n load the last token and store nothing.  The
+// append rule is the step's (row_codes): per G32 group the shift of the
+// magnitude maximum, then the round-half-away codes.
 template <bool Q17>
 __global__ __launch_bounds__(256) void append_bulk_kernel(BulkArgs a) {
     // wave-uniform through readfirstlane, so the page's buffer resource stays in SGPRs
     const int h = blockIdx.y * 4 + __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int lane = threadIdx.x & 63;
+    const int half = lane >> 5, cl = lane & 31;   // row of the pair; channels 4cl .. 4cl+3 (pairs 2cl, 2cl+1)
     const int t0 = blockIdx.x * kAppendTokens;
-    int2 cs[kAppendTokens], ki[kAppendTokens], vi[kAppendTokens];
+    int4 cs[kAppendRounds], ki[kAppendRounds], vi[kAppendRounds];
 #pragma unroll
-    for (int j = 0; j < kAppendTokens; ++j) {
-        const int t = min(t0 + j, a.n - 1);
-        const size_t elem = static_cast<size_t>(t) * kModelDim + h * kHeadDim + 2 * lane;
-        cs[j] = a.lut[static_cast<size_t>(a.pos0 + t) * kRopePairs + lane];
-        ki[j] = load_pair<Q17>(a.k, elem);
-        vi[j] = load_pair<Q17>(a.v, elem);
+    for (int j = 0; j < kAppendRounds; ++j) {
+        const int t = min(t0 + 2 * j + half, a.n - 1);
+        const size_t elem = static_cast<size_t>(t) * kModelDim + h * kHeadDim + 4 * cl;
+        cs[j] = *reinterpret_cast<const int4*>(a.lut + static_cast<size_t>(a.pos0 + t) * kRopePairs + 2 * cl);
+        ki[j] = load_quad<Q17>(a.k, elem);
+        vi[j] = load_quad<Q17>(a.v, elem);
     }
     const __amdgpu_buffer_rsrc_t page = __builtin_amdgcn_make_buffer_rsrc(
         page_ptr(a.kv, a.slot, a.layer, h), static_cast<short>(0), static_cast<int32_t>(a.kv.page_bytes), kBufferWord3);
+    const int cap = a.kv.seq_cap;
 #pragma unroll
-    for (int j = 0; j < kAppendTokens; ++j) {
-        if (t0 + j >= a.n) break;
-        int32_t k0, k1;
-        rope_pair(ki[j].x, ki[j].y, cs[j], k0, k1);
-        store_row(page, a.kv.seq_cap, a.pos0 + t0 + j, lane, row_codes(k0, k1, vi[j].x, vi[j].y));
+    for (int j = 0; j < kAppendRounds; ++j) {
+        if (t0 + 2 * j >= a.n) break;                  // wave-uniform: neither row of the pair exists
+        int4 k;
+        rope_pair(ki[j].x, ki[j].y, make_int2(cs[j].x, cs[j].y), k.x, k.y);
+        rope_pair(ki[j].z, ki[j].w, make_int2(cs[j].z, cs[j].w), k.z, k.w);
+        const uint32_t sk = g32_shift(octet_max_u(quad_magnitude(k)));
+        const uint32_t sv = g32_shift(octet_max_u(quad_magnitude(vi[j])));
+        const uint32_t kw = quad_codes(k, sk), vw = quad_codes(vi[j], sv);
+        if (t0 + 2 * j + half < a.n) {                 // the pair's second row may be past n
+            const int row = a.pos0 + t0 + 2 * j;       // first row of the pair (SGPR); this lane's is row + half
+            __builtin_amdgcn_raw_buffer_store_b32(kw, page, half * kCodeBytes + 4 * cl, row * kCodeBytes, 0);
+            __builtin_amdgcn_raw_buffer_store_b32(vw, page, half * kCodeBytes + 4 * cl, (cap + row) * kCodeBytes, 0);
+            if ((cl & 7) == 0) {
+                const v2f sc = {shift_scale(sk), shift_scale(sv)};
+                __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u, sc), page,
+                                                      half * kScaleBytes + (cl >> 3) * 8,
+                                                      cap * (2 * kCodeBytes) + row * kScaleBytes, 0);
+            }
+        }
     }
 }
 

@@ -363,6 +363,9 @@ def test_error_codes(skv, ctx, lut4096):
     with pytest.raises(skv.SwiftKVError) as ei:
         skv.swiftkv_append_tokens(ctx, buf, buf, kv, lut4096, 0, 0, 120, 16)
     assert ei.value.code == skv.ERANGE
+    with pytest.raises(skv.SwiftKVError) as ei:   # rows read four channels per lane: 16-byte alignment
+        skv.swiftkv_append_tokens(ctx, buf.ptr + 8, buf, kv, lut4096, 0, 0, 0, 1)
+    assert ei.value.code == skv.EINVAL
     with pytest.raises(skv.SwiftKVError) as ei:
         ctx.set_split_tokens(300)
     assert ei.value.code == skv.EINVAL
