@@ -322,12 +322,21 @@ int upload_lut(swiftkv_context* ctx, std::vector<int2>&& host, int32_t positions
 constexpr int64_t kMaxSplitsPerHead = 8;
 constexpr int64_t kMaxSplitTokensHeuristic = 8192;
 
-int32_t choose_split(const swiftkv_context* ctx, const int32_t* positions, int32_t batch) {
-    if (ctx->split_tokens > 0) return ctx->split_tokens;
+// What the launch plan depends on: the device's compute units, the 4-wave
+// step workgroups one CU holds, and the forced split (0: the heuristic).
+struct SplitPolicy {
+    int32_t cus;
+    int32_t step_per_cu;
+    int32_t split_tokens;
+};
+SplitPolicy policy_of(const swiftkv_context* ctx) { return {ctx->cus, ctx->step_per_cu, ctx->split_tokens}; }
+
+int32_t choose_split(const SplitPolicy& pol, const int32_t* positions, int32_t batch) {
+    if (pol.split_tokens > 0) return pol.split_tokens;
     int32_t max_len = 1;
     for (int32_t b = 0; b < batch; ++b) max_len = std::max(max_len, positions[b] + 1);
     const int64_t heads = static_cast<int64_t>(batch) * kHeads;
-    const int64_t slots = heads <= ctx->cus ? ctx->cus : static_cast<int64_t>(ctx->cus) * ctx->step_per_cu;
+    const int64_t slots = heads <= pol.cus ? pol.cus : static_cast<int64_t>(pol.cus) * pol.step_per_cu;
     const int64_t by_length = (max_len + kMaxSplitTokensHeuristic - 1) / kMaxSplitTokensHeuristic;
     const int64_t splits_per_head =
         std::min<int64_t>(kMaxSplitsPerHead, std::max<int64_t>({int64_t(1), slots / heads, by_length}));
@@ -343,9 +352,9 @@ int32_t choose_split(const swiftkv_context* ctx, const int32_t* positions, int32
 // batch 2 17.1 against 17.6 us/layer with 8 waves on 64-token blocks,
 // batch 8 50.6 against 51.0; batch 1 unchanged).  Larger launches fill the
 // machine either way and keep 4 waves, so more workgroups stay resident per CU.
-int step_waves(const swiftkv_context* ctx, int32_t grid_splits, int32_t batch, int32_t split_tokens) {
+int step_waves(const SplitPolicy& pol, int32_t grid_splits, int32_t batch, int32_t split_tokens) {
     const int64_t workgroups = static_cast<int64_t>(grid_splits) * kHeads * batch;
-    const bool wide = workgroups <= ctx->cus && split_tokens % kWideRoundTokens == 0;
+    const bool wide = workgroups <= pol.cus && split_tokens % kWideRoundTokens == 0;
     return wide ? kWideWaves : kAttendWaves;
 }
 
@@ -431,7 +440,7 @@ int run_step(swiftkv_context* ctx, const void* q, const void* k, const void* v, 
             const int32_t nb = std::min<int32_t>(kMaxBatchPerLaunch, batch - b0);
             int32_t max_pos = 0;
             for (int32_t b = 0; b < nb; ++b) max_pos = std::max(max_pos, positions[b0 + b]);
-            const int32_t split = choose_split(ctx, positions + b0, nb);
+            const int32_t split = choose_split(policy_of(ctx), positions + b0, nb);
             const int32_t splits = (max_pos + split) / split;
             if (splits > kFixedSlots)
                 return fail(SWIFTKV_ERANGE, "the step splits a head %d ways (%d-token splits of up to %d tokens); the "
@@ -457,7 +466,7 @@ int run_step(swiftkv_context* ctx, const void* q, const void* k, const void* v, 
         int32_t max_pos = 0;
         for (int32_t b = 0; b < nb; ++b) max_pos = std::max(max_pos, positions[b0 + b]);
         set_rows(a, positions + b0);
-        a.split_tokens = choose_split(ctx, positions + b0, nb);
+        a.split_tokens = choose_split(policy_of(ctx), positions + b0, nb);
         const int32_t grid_splits = (max_pos + 1 + a.split_tokens - 1) / a.split_tokens;
         if (noalloc) {
             a.arrivals = reinterpret_cast<uint64_t*>(ctx->scratch);
@@ -479,7 +488,8 @@ int run_step(swiftkv_context* ctx, const void* q, const void* k, const void* v, 
         a.act_scale = act_scale ? act_scale + static_cast<size_t>(b0) * kHeads * kGroupsPerHead : nullptr;
 
         ProfilePair* p = profile_begin(ctx, SWIFTKV_KERNEL_STEP);
-        SKV_HIP(launch_step(a, grid_splits, step_waves(ctx, grid_splits, nb, a.split_tokens), in.format, ctx->stream));
+        SKV_HIP(launch_step(a, grid_splits, step_waves(policy_of(ctx), grid_splits, nb, a.split_tokens), in.format,
+                            ctx->stream));
         profile_end(ctx, p);
     }
     return ok();
@@ -692,6 +702,37 @@ int swiftkv_set_split_tokens(swiftkv_context* ctx, int32_t split_tokens) {
         return fail(SWIFTKV_EINVAL, "split_tokens %d must be 0 or a multiple of %d in [%d, %d]", split_tokens,
                     kSplitQuantum, kSplitQuantum, kMaxSplitTokens);
     ctx->split_tokens = split_tokens;
+    return ok();
+}
+
+int swiftkv_debug_step_plan(int32_t cus, int32_t workgroups_per_cu, int32_t split_tokens, const int32_t* positions,
+                            int32_t batch, int32_t* out_split_tokens, int32_t* out_grid_splits, int32_t* out_waves,
+                            int32_t* out_rows) {
+    if (!positions || !out_split_tokens || !out_grid_splits || !out_waves)
+        return fail(SWIFTKV_EINVAL, "null argument");
+    if (cus < 1 || workgroups_per_cu < 1)
+        return fail(SWIFTKV_EINVAL, "cus %d and workgroups_per_cu %d must be positive", cus, workgroups_per_cu);
+    if (batch < 1 || batch > kMaxBatchPerLaunch)
+        return fail(SWIFTKV_ERANGE, "batch %d outside [1, %d] (one launch)", batch, kMaxBatchPerLaunch);
+    if (split_tokens != 0 &&
+        (split_tokens < kSplitQuantum || split_tokens > kMaxSplitTokens || split_tokens % kSplitQuantum != 0))
+        return fail(SWIFTKV_EINVAL, "split_tokens %d must be 0 or a multiple of %d in [%d, %d]", split_tokens,
+                    kSplitQuantum, kSplitQuantum, kMaxSplitTokens);
+    int32_t max_pos = 0;
+    for (int32_t b = 0; b < batch; ++b) {
+        if (positions[b] < 0 || positions[b] >= kMaxSeq)
+            return fail(SWIFTKV_ERANGE, "position %d outside [0, %d)", positions[b], kMaxSeq);
+        max_pos = std::max(max_pos, positions[b]);
+    }
+    const SplitPolicy pol{cus, workgroups_per_cu, split_tokens};
+    StepArgs a{};
+    a.batch = batch;
+    set_rows(a, positions);
+    *out_split_tokens = choose_split(pol, positions, batch);
+    *out_grid_splits = (max_pos + *out_split_tokens) / *out_split_tokens;
+    *out_waves = step_waves(pol, *out_grid_splits, batch, *out_split_tokens);
+    if (out_rows)
+        for (int32_t z = 0; z < batch; ++z) out_rows[z] = static_cast<int32_t>(a.rows[z] & 0xffu);
     return ok();
 }
 

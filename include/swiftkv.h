@@ -91,6 +91,20 @@ int swiftkv_synchronize(swiftkv_context* ctx);
 /* Tokens per split-context work item; 0 selects the built-in heuristic.
  * Must be 0 or a multiple of 256 in [256, 32768]. */
 int swiftkv_set_split_tokens(swiftkv_context* ctx, int32_t split_tokens);
+/* Testing aid with no counterpart in the reference, host-only (no device or
+ * context needed): the launch plan the step entries use for one launch of
+ * batch <= 256 sequences at positions[batch], on a device of `cus` compute
+ * units each holding `workgroups_per_cu` 4-wave step workgroups (a context
+ * takes both from the device), with split_tokens as swiftkv_set_split_tokens
+ * sets it (0: the built-in heuristic).  Writes the tokens per split, the
+ * splits of the longest sequence (the grid's split dimension), the waves per
+ * workgroup (4, or 16 for launches of at most one workgroup per CU whose
+ * splits are a multiple of 512 tokens) and, when out_rows is not null, the
+ * sequence served by each grid row (longest first, equal positions in
+ * sequence order). */
+int swiftkv_debug_step_plan(int32_t cus, int32_t workgroups_per_cu, int32_t split_tokens, const int32_t* positions,
+                            int32_t batch, int32_t* out_split_tokens, int32_t* out_grid_splits, int32_t* out_waves,
+                            int32_t* out_rows);
 /* Testing aid with no counterpart in the reference.  A head split across
  * workgroups is merged inside the launch through 64-bit words tagged with the
  * (sequence row, head)'s generation + 1, which every launch that merges the

@@ -144,3 +144,54 @@ def test_host_arrays_need_host_io_mode(skv):
         skv._io_ptr(FakeCtx, np.zeros((4, 4), np.float32)[:, ::2], np.float32)
     with pytest.raises(ValueError):
         skv._check_io_sizes(FakeCtx, 2, np.zeros(4096, np.float32), None, None, None, None, None)
+
+
+@pytest.mark.parametrize("positions,split,want", [
+    ([4095], 0, (512, 8, 16)),                 # batch 1: 8 splits, one 16-wave workgroup per CU
+    ([4095] * 2, 0, (1024, 4, 16)),
+    ([4095] * 4, 0, (2048, 2, 16)),
+    ([4095] * 8, 0, (4096, 1, 16)),            # 256 workgroups: no split
+    ([4095] * 16, 0, (4096, 1, 4)),            # more than one workgroup per CU: 4 waves
+    ([4095] * 64, 0, (4096, 1, 4)),            # the headline launch
+    ([32767] * 16, 0, (8192, 4, 4)),           # no split longer than 8192 tokens
+    ([100, 700, 2047], 0, (1024, 2, 16)),
+    ([5, 100, 100, 3], 0, (256, 1, 4)),        # 256-token split: not a multiple of 512
+    ([4095] * 4, 256, (256, 16, 4)),           # forced splits
+    ([4095], 1536, (1536, 3, 16)),
+    ([4095] * 12, 512, (512, 8, 4)),           # 3,072 workgroups
+])
+def test_step_plan(skv, positions, split, want):
+    """The launch plan on the reference device shape (256 CUs, three 4-wave
+    step workgroups per CU): tokens per split, splits of the longest
+    sequence, waves per workgroup.  Host logic only."""
+    got = skv.step_plan(positions, split_tokens=split)
+    assert got[:3] == want
+
+
+def test_step_plan_orders_rows_longest_first(skv):
+    split, grid, waves, rows = skv.step_plan([5, 100, 100, 3, 4095, 0, 100])
+    assert rows.tolist() == [4, 1, 2, 6, 0, 3, 5]       # equal positions keep sequence order
+    _, _, _, rows = skv.step_plan(list(range(256)))
+    assert rows.tolist() == list(range(255, -1, -1))
+
+
+def test_step_plan_argument_checks(skv):
+    L = skv.lib()
+    pos = np.array([10, 20], np.int32)
+    out = [C.c_int32() for _ in range(3)]
+    p = pos.ctypes.data_as(C.c_void_p)
+
+    def plan(cus=256, per_cu=3, split=0, positions=p, batch=2):
+        return L.swiftkv_debug_step_plan(cus, per_cu, split, positions, batch, C.byref(out[0]), C.byref(out[1]),
+                                         C.byref(out[2]), None)
+
+    assert plan() == skv.OK and (out[0].value, out[1].value, out[2].value) == (256, 1, 4)
+    assert plan(positions=None) == skv.EINVAL
+    assert plan(cus=0) == skv.EINVAL
+    assert plan(per_cu=0) == skv.EINVAL
+    assert plan(batch=0) == skv.ERANGE
+    assert plan(batch=257) == skv.ERANGE
+    assert plan(split=300) == skv.EINVAL
+    bad = np.array([10, 32768], np.int32)
+    assert plan(positions=bad.ctypes.data_as(C.c_void_p)) == skv.ERANGE
+    assert b"position 32768" in L.swiftkv_last_error()
