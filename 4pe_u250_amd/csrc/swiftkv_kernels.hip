@@ -7,25 +7,30 @@
 // 512-token-multiple splits); workgroup (j, h, z) owns tokens
 // [j*C, min((j+1)*C, position+1)) of head h of the sequence that row z names
 // (rows come longest first, so a ragged batch does not end on long heads):
-//   1. every lane loads its channel pair of the new row's q/k/v (Q15.17,
-//      FP32, or the upstream linear stage's split-K FP32 partials, reduced in
-//      the reference's order), then the first cache block, before any math;
-//      it converts and rotates its q pair (integer RoPE from the Q1.17 table)
-//      and gathers the 16 query channels of its chunk from its neighbours;
+//   1. every lane loads its channel pair of the new row's q (and, in the one
+//      wave that appends the row, of k and v) -- Q15.17, FP32, or the
+//      upstream linear stage's split-K FP32 partials, reduced in the
+//      reference's order -- then the first cache block, before any math; it
+//      converts and rotates its q pair (integer RoPE from the Q1.17 table),
+//      splits it into signed-byte limbs and gathers the limbs of its chunk's
+//      16 query channels from its neighbours;
 //   2. the workgroup whose range holds `position` also converts, rotates and
 //      G32-quantizes the new K/V row, appends it to the cache, and forwards it
 //      into its own merge as one more partial -- the new token is written once
 //      and never read back (the reference does the same, hpp:37-41);
-//   3. the waves scan the cached tokens in 64-token blocks.  Lane = (chunk
-//      c = lane&7, row r = lane>>3): one nontemporal dwordx4 per lane reads a
-//      16-channel chunk, so one wave instruction covers 8 full 128-B code
-//      rows.  Codes are dequantized in VGPRs, partial dots reduced over the 8
-//      chunk lanes with DPP, the running (max, sum, acc) stays in VGPRs;
+//   3. the waves scan the cached tokens in 64-token (16 waves: 32-token)
+//      blocks.  Lane = (chunk c = lane&7, row r = lane>>3): one nontemporal
+//      dwordx4 per lane reads a 16-channel chunk, so one wave instruction
+//      covers 8 full 128-B code rows.  K rows are dotted with the query limbs
+//      by v_dot4 on the int8 codes, V codes are dequantized in VGPRs, partial
+//      dots reduced over the 8 chunk lanes with DPP, the running (max, sum,
+//      acc) stays in VGPRs;
 //   4. waves (plus the forwarded row) merge through LDS;
 //   5. a head held by one split is finished in place (FP32 output and the
 //      optional A14/E8M0 words); otherwise each split publishes its partial
-//      (m, l, acc[128]) and the last split of the head to arrive merges them
-//      (log-sum-exp) and finishes the head -- no second kernel.
+//      (m, l, acc[128]) as tagged words and the last split of the head to
+//      count its arrival merges them (log-sum-exp, in split order) and
+//      finishes the head -- no second kernel.
 //
 // No MFMA: q_len = 1 multi-head attention is a memory-bound GEMV.
 #include "swiftkv_device.hpp"
