@@ -104,3 +104,47 @@ def test_split_merge_across_the_tag_wrap(skv, ctx, noalloc):
         b.free()
     kv.close()
     lut.close()
+
+
+def test_two_contexts_interleaved(skv, ctx):
+    """Two contexts on one GPU, each with its own cache and split workspace,
+    their split launches interleaved on two streams: each context's outputs
+    equal what it gives alone, bit for bit (every workspace counts its own
+    generations, so one context's merges never see the other's words)."""
+    _note("case: two contexts, batch 1 (8 splits) and batch 2 (4 splits), interleaved")
+    other = skv.Context(0)
+    setups = []
+    for c, batch, seed in ((ctx, 1, 501), (other, 2, 502)):
+        lut = skv.RopeLut.generate(c, 4096)
+        kv = skv.KVCache(c, layers=1, max_batch=batch, max_seq_len=4096)
+        kv.fill_synthetic(lut, ntok=4095, seed=seed)
+        qkv = [c.alloc(batch * 4096 * 4) for _ in range(3)]
+        for i, b in enumerate(qkv):
+            c.fill_synthetic(b, batch * 4096, seed + 1, 40 + i)
+        out = c.alloc(batch * 4096 * 4)
+        setups.append((c, batch, lut, kv, qkv, out))
+
+    def launch(s):
+        c, batch, lut, kv, qkv, out = s
+        skv.swiftkv_attention(c, qkv[0], qkv[1], qkv[2], kv, lut, None, None, 0, np.full(batch, 4095, np.int32), out)
+
+    def result(s):
+        s[0].synchronize()
+        return s[5].download(np.uint32, (s[1] * 4096,))
+
+    alone = []
+    for s in setups:
+        launch(s)
+        alone.append(result(s))
+    for rnd in range(50):
+        for s in setups:
+            launch(s)
+        if rnd % 10 == 9:
+            for s, want in zip(setups, alone):
+                assert np.array_equal(result(s), want), f"round {rnd}: context with batch {s[1]} differs"
+    for c, batch, lut, kv, qkv, out in setups:
+        for b in qkv + [out]:
+            b.free()
+        kv.close()
+        lut.close()
+    other.close()
