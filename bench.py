@@ -67,13 +67,13 @@ PROFILE_KEYS = ("traffic_bytes_per_launch", "algorithmic_bytes_per_launch", "tra
                 "achieved_occupancy_frac", "vgprs", "bench_ms_per_step", "commit")
 
 
-def profile_summary(batch: int, context: int):
+def profile_summary(batch: int, context: int, ragged: bool = False):
     """The committed rocprofv3 summary of the step kernel on this workload:
     HBM bytes per launch (FETCH_SIZE and WRITE_SIZE, each scaled by the
     copy-kernel calibration), their ratio to the algorithmic bytes, LDS bank
     conflicts, achieved occupancy, and the commit and bench ms/step of the run
     it came from.  ({}, None) when no summary covers the workload."""
-    path = os.path.join(REPO, "profiles", f"step_kernel_batch{batch}_ctx{context}.md")
+    path = os.path.join(REPO, "profiles", f"step_kernel_batch{batch}{'_ragged' if ragged else ''}_ctx{context}.md")
     if not os.path.exists(path):
         return {}, None
     vals = {}
@@ -474,6 +474,9 @@ def main():
     ap.add_argument("--context", type=int, default=4096)
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--split", type=int, default=0, help="tokens per split (0 = heuristic)")
+    ap.add_argument("--ragged", action="store_true",
+                    help="main workload with attended lengths drawn from U{256..context} (seed 4), the ragged "
+                         "configuration, instead of every sequence at position context - 1")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-batch1", action="store_true")
@@ -508,7 +511,11 @@ def main():
         return
     ctx.set_split_tokens(args.split)
     log(f"[bench] {skv.version()}")
-    main_res = run_gpu(skv, ctx, np.full(args.batch, args.context - 1), args.layers, args.steps, args.warmup,
+    if args.ragged:
+        main_positions = np.random.default_rng(4).integers(256, args.context + 1, args.batch) - 1
+    else:
+        main_positions = np.full(args.batch, args.context - 1)
+    main_res = run_gpu(skv, ctx, main_positions, args.layers, args.steps, args.warmup,
                        seed=2026, exact_steps=args.exact_steps, parts=args.parts)
     log(f"[bench] batch {args.batch}: {main_res['us_per_layer']:.1f} us/layer, {main_res['gbps']:.0f} GB/s "
         f"(graph replay {main_res['graph']['us_per_layer']:.1f} us/layer)")
@@ -581,7 +588,7 @@ def main():
                     f"sequence-step")
 
     att = main_res["step_avg_us"]
-    prof, traffic_src = profile_summary(args.batch, args.context)
+    prof, traffic_src = profile_summary(args.batch, args.context, ragged=args.ragged)
     traffic = prof.get("traffic_bytes_per_launch")
     line = {
         "metric": METRIC,
@@ -600,8 +607,10 @@ def main():
         "vs_baseline": None,
         "dtype": "fp32",
         "data": "synthetic (seeded N(0,1) q/k/v and cache rows, cache built on device by the append rule)",
-        "config": {"workload": "decode-attention step: 32 layers x batch 64 x position 4095 (ctx 4096), "
-                               "32 heads x 128, MHA, INT8/G32 KV cache",
+        "config": {"workload": (f"decode-attention step: {args.layers} layers x batch {args.batch} x "
+                                + (f"attended lengths U{{256..{args.context}}} (seed 4)" if args.ragged else
+                                   f"position {args.context - 1} (ctx {args.context})")
+                                + ", 32 heads x 128, MHA, INT8/G32 KV cache"),
                    "batch": args.batch, "context": args.context, "layers": args.layers, "heads": 32,
                    "head_dim": 128, "kv_dtype": "int8+fp32 G32 scales"},
         "us_per_layer": round(main_res["us_per_layer"], 2),
