@@ -187,6 +187,7 @@ struct PageReader {
     int32_t k_lane;       // lane's byte offset in the K plane (row r, chunk c)
     int32_t v_lane;       // the same in the V plane
     int32_t s_lane;       // lane's (K, V) scale pair of group c/2 in the scale plane
+    int32_t past_end;     // added to a lane offset, puts any load of the page past its range
 };
 
 constexpr int kNontemporal = 2;                // cache policy: nt
@@ -198,6 +199,7 @@ __device__ __forceinline__ PageReader make_reader(const int8_t* page, int64_t ca
     pr.k_lane = r * kCodeBytes + c * 16;
     pr.v_lane = static_cast<int32_t>(cap * kCodeBytes) + r * kCodeBytes + c * 16;
     pr.s_lane = static_cast<int32_t>(cap * 2 * kCodeBytes) + r * kScaleBytes + (c >> 1) * 8;
+    pr.past_end = static_cast<int32_t>(cap * kTokenBytes);   // <= 32768 * 288: lane offset + token offset stay < 2^31
     return pr;
 }
 
@@ -227,6 +229,32 @@ __device__ __forceinline__ void issue_block(const PageReader& pr, int t0, BlockL
     // Keep all 24 loads in flight before any math: without this fence the
     // scheduler sinks V loads next to their uses (to save VGPRs) and
     // serializes them at full memory latency.
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// The same loads for a block that may extend past t_stop: the rows at or past
+// it get a lane offset beyond the page's buffer range, so the hardware's
+// range check returns zeros for them without fetching (their scores and
+// weights are masked anyway).  Used for the last block of a range, and for
+// the first block of every wave: a wave with no tokens then issues its loads
+// with every row masked and moves no data.
+template <int NI>
+__device__ __forceinline__ void issue_block_masked(const PageReader& pr, int t0, int t_stop, int r,
+                                                   BlockLoads<NI>& bl) {
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        const int32_t tok = t0 + 8 * i;
+        const int32_t past = tok + r >= t_stop ? pr.past_end : 0;
+        bl.k[i] = __builtin_amdgcn_raw_buffer_load_b128(pr.rsrc, pr.k_lane + past, tok * kCodeBytes, kNontemporal);
+        bl.s[i] = __builtin_bit_cast(v2f, __builtin_amdgcn_raw_buffer_load_b64(pr.rsrc, pr.s_lane + past,
+                                                                                tok * kScaleBytes, kNontemporal));
+    }
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        const int32_t tok = t0 + 8 * i;
+        const int32_t past = tok + r >= t_stop ? pr.past_end : 0;
+        bl.v[i] = __builtin_amdgcn_raw_buffer_load_b128(pr.rsrc, pr.v_lane + past, tok * kCodeBytes, kNontemporal);
+    }
     __builtin_amdgcn_sched_barrier(0);
 }
 
@@ -281,7 +309,7 @@ __device__ __forceinline__ void scan_range(const PageReader& pr, BlockLoads<NI>&
         consume_block<false, NI>(bl, Q, t0, t_stop, r, m_run, l_run, acc);
     }
     if (t0 < t_stop) {
-        if (!first) issue_block(pr, t0, bl);
+        if (!first) issue_block_masked(pr, t0, t_stop, r, bl);
         consume_block<true, NI>(bl, Q, t0, t_stop, r, m_run, l_run, acc);
     }
     l_run = across_octets_sum(l_run);
@@ -551,10 +579,10 @@ __global__ __launch_bounds__(WAVES * 64) void step_kernel(StepArgs a) {
     const PageReader pr = make_reader(page, cap, c, r);
     const int t_first = t_begin + wave * kBlk;
     const int t_stop = owner ? pos : t_end;       // the new token is forwarded, not scanned
-    // A wave with no tokens loads the split's first block (always in the page)
-    // and discards it: every path then has the same loads in flight.
+    // A wave with no tokens issues the split's first block with every row
+    // masked (no data moves): every path then has the same loads in flight.
     BlockLoads<NI> bl;
-    issue_block(pr, t_first < t_stop ? t_first : t_begin, bl);
+    issue_block_masked(pr, t_first < t_stop ? t_first : t_begin, t_first < t_stop ? t_stop : 0, r, bl);
     // The (row, head)'s arrival word, for the tag of a split partial.  Read
     // on every path (unused by a head held by one split): a load under a
     // branch would make the compiler wait for the block at the join.
