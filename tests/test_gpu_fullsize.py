@@ -198,6 +198,60 @@ def test_batch64_32layer_arena(skv, ctx, rope_tables, ragged):
     lut.close()
 
 
+@pytest.mark.parametrize("entry", ["regular", "noalloc"])
+def test_batch300_split_across_two_launches(skv, ctx, rope_tables, entry):
+    """300 sequences at ragged positions 300..1400 with forced 256-token
+    splits: two launches (256 rows, then 44) whose split heads reuse the same
+    workspace rows (the second launch's tags follow the first's), through the
+    regular entry and through the allocation-free one (its fixed workspace).
+    Every sequence's appended row bit-exact; the outputs of sequences on both
+    sides of the launch boundary checked in full against the oracle."""
+    cos, sin = rope_tables
+    batch, seed = 300, 7300
+    rng = np.random.default_rng(seed)
+    positions = rng.integers(300, 1401, batch).astype(np.int32)
+    _note(f"case: batch {batch}, positions 300..1400, 256-token splits, {entry} entry")
+    lut = skv.RopeLut.generate(ctx, 4096)
+    kv = skv.KVCache(ctx, layers=1, max_batch=batch, max_seq_len=1408)
+    kv.fill_synthetic(lut, ntok=1400, seed=seed)
+    n = batch * 4096
+    bufs, host = [], []
+    for i in range(3):
+        b = ctx.alloc(n * 4)
+        ctx.fill_synthetic(b, n, seed + 1, 9200 + i)
+        bufs.append(b)
+        host.append(b.download(np.float32, (batch, 4096)))
+    q, k, v = host
+    out, aq, asc = ctx.alloc(n * 4), ctx.alloc(batch * 128 * 56), ctx.alloc(batch * 128)
+    run = skv.swiftkv_attention_noalloc if entry == "noalloc" else skv.swiftkv_attention
+    ctx.set_split_tokens(256)
+    try:
+        for _ in range(2):   # twice: the second call's tags follow the first's
+            run(ctx, bufs[0], bufs[1], bufs[2], kv, lut, aq, asc, 0, positions, out)
+        ctx.synchronize()
+    finally:
+        ctx.set_split_tokens(0)
+    o = out.download(np.float32, (batch, 4096))
+    words = aq.download(np.uint8, (batch, 128, 56))
+    codes = asc.download(np.uint8, (batch, 128))
+    assert np.isfinite(o).all()
+    for b in range(batch):
+        _appended_rows_match(kv, b, 0, int(positions[b]), k[b], v[b], cos, sin)
+    for b in (0, 255, 256, 299, int(np.argmax(positions))):
+        p = int(positions[b])
+        _note(f"  oracle check of sequence {b}, position {p}")
+        sc = _oracle_cache(skv, ctx, cos, sin, seed, b, 0, p, p + 1)
+        res = sc.step_q17(O.f2q17(q[b]), O.f2q17(k[b]), O.f2q17(v[b]), p, cos[p], sin[p], fp=True)
+        assert_rows_equal(kv, sc, b, 0, 0, p + 1)
+        assert_close(o[b].reshape(H, 128), res["fp"], f"sequence {b} position {p}")
+        q14, e8 = O.a14(o[b].reshape(128, 32))
+        assert (codes[b] == e8).all() and (words[b] == O.pack_a14(q14)).all(), f"sequence {b}: A14"
+    for x in bufs + [out, aq, asc]:
+        x.free()
+    kv.close()
+    lut.close()
+
+
 def test_batch16_context32k_512_steps(skv, ctx):
     """Config-5 shape: 16 sequences, unit-variance Student-t(3) rows, cache
     pre-filled to 32256 tokens, then 512 consecutive decode steps to 32767
