@@ -598,10 +598,12 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(main_res["ms_per_step"], 4),
-        "ms_per_step_median": round(main_res["ms_per_step_median"], 4),
+        "ms_per_step_median": (round(main_res["ms_per_step_median"], 4) if main_res["ms_per_step_median"]
+                               else None),
         "step_timing": (f"ms_per_step: hipEvents around the {args.steps} timed steps / {args.steps}; "
-                        f"ms_per_step_median: median of {main_res['step_samples']} further steps, each between "
-                        "its own pair of events on the stream"),
+                        + (f"ms_per_step_median: median of {main_res['step_samples']} further steps, each between "
+                           "its own pair of events on the stream" if main_res["step_samples"] else
+                           "no per-step median: a step of fewer than 8 launches would time its own event pair")),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -614,7 +616,8 @@ def main():
                    "batch": args.batch, "context": args.context, "layers": args.layers, "heads": 32,
                    "head_dim": 128, "kv_dtype": "int8+fp32 G32 scales"},
         "us_per_layer": round(main_res["us_per_layer"], 2),
-        "us_per_layer_median_step": round(1000.0 * main_res["ms_per_step_median"] / args.layers, 2),
+        "us_per_layer_median_step": (round(1000.0 * main_res["ms_per_step_median"] / args.layers, 2)
+                                     if main_res["ms_per_step_median"] else None),
         "tokens_per_s": round(main_res["tokens_per_s"], 1),
         "pct_of_peak": round(main_res["pct_of_peak"], 2),
         "kernel_avg_us_event_pairs": {k: (round(v, 2) if v else v) for k, v in main_res["kernel_avg_us"].items()},
