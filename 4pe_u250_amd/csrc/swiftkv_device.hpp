@@ -14,6 +14,7 @@ typedef int32_t v4i __attribute__((ext_vector_type(4)));
 typedef int32_t v2i __attribute__((ext_vector_type(2)));
 typedef uint32_t v2u __attribute__((ext_vector_type(2)));
 typedef float v2f __attribute__((ext_vector_type(2)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 
 constexpr int32_t kBufferWord3 = 0x00020000;   // raw buffer resource, gfx9 data format
 

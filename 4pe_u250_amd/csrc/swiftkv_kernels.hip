@@ -715,20 +715,42 @@ __global__ __launch_bounds__(WAVES * 64) void step_kernel(StepArgs a) {
 
 // ---------------------------------------------------------------- utilities
 
-// Prefill rows per wave: one instruction covers two token rows (lane l takes
-// channels 4(l & 31) .. 4(l & 31) + 3 of row l >> 5), and a wave takes
-// kAppendRounds such row pairs with all of their loads in flight together.
-constexpr int kAppendRounds = 1;
-constexpr int kAppendTokens = 2 * kAppendRounds;
+// Prefill rows: one instruction covers two token rows (lane l takes channels
+// 4(l & 31) .. 4(l & 31) + 3 of row l >> 5), and a wave takes kAppendPairs
+// such pairs with all of their loads in flight together.
+constexpr int kAppendPairs = 1;
+constexpr int kAppendTokens = 2 * kAppendPairs;
+constexpr bool kAppendNontemporal = false;
 
-template <bool Q17>
-__device__ __forceinline__ int4 load_quad(const void* base, size_t elem) {
-    if constexpr (Q17) {
-        return *reinterpret_cast<const int4*>(static_cast<const int32_t*>(base) + elem);
-    } else {
-        const float4 f = *reinterpret_cast<const float4*>(static_cast<const float*>(base) + elem);
-        return make_int4(f32_to_q17(f.x), f32_to_q17(f.y), f32_to_q17(f.z), f32_to_q17(f.w));
-    }
+// Q15.17 of four FP32 values by the saturating conversion alone, which maps
+// NaN to 0; the caller sends a wave holding a NaN through f32_to_q17.
+__device__ __forceinline__ int32_t q17_no_nan(float x) {
+    int32_t v;
+    asm("v_cvt_i32_f32 %0, %1" : "=v"(v) : "v"(__builtin_rintf(x * 131072.0f)));
+    return v;
+}
+__device__ __forceinline__ int4 quad_q17_no_nan(float4 f) {
+    return make_int4(q17_no_nan(f.x), q17_no_nan(f.y), q17_no_nan(f.z), q17_no_nan(f.w));
+}
+__device__ __forceinline__ int4 quad_q17(float4 f) {
+    return make_int4(f32_to_q17(f.x), f32_to_q17(f.y), f32_to_q17(f.z), f32_to_q17(f.w));
+}
+
+// The rotation's sat32((a*c - b*s) >> 17) in double precision.  The table's
+// (cos, sin) are signed 19-bit values (generated or loaded, both saturate to
+// 19 bits) and |a|, |b| <= 2^31, so each product has at most 49 significant
+// bits and the fused sum at most 50: every step below is exact, floor is the
+// arithmetic shift, and the double-to-int conversion saturates.
+__device__ __forceinline__ int32_t floor_sat32(double x) {
+    int32_t v;
+    asm("v_cvt_i32_f64 %0, %1" : "=v"(v) : "v"(__builtin_floor(x)));
+    return v;
+}
+__device__ __forceinline__ void rope_pair_f64(int32_t a, int32_t b, int2 cs, int32_t& x0, int32_t& x1) {
+    const double c = static_cast<double>(cs.x) * 0x1p-17, s = static_cast<double>(cs.y) * 0x1p-17;
+    const double da = a, db = b;
+    x0 = floor_sat32(__builtin_fma(da, c, -(db * s)));
+    x1 = floor_sat32(__builtin_fma(da, s, db * c));
 }
 
 // Max over the 8 lanes of an aligned octet (one G32 group of a row when a
@@ -739,50 +761,129 @@ __device__ __forceinline__ uint32_t octet_max_u(uint32_t x) {
     return max(x, dpp_u<kDppHalfMirror>(x));
 }
 
+// The largest magnitude of a quad, at least 1 (the shift rule gives 0 for a
+// maximum of 0 and of 1 alike): max(max r, 0) against 0 - min(min r, 0),
+// which is 2^31 for INT32_MIN.
+__device__ __forceinline__ uint32_t quad_magnitude1(int4 r) {
+    const int32_t hi = max(max(max(max(r.x, r.y), r.z), r.w), 0);
+    const int32_t lo = min(min(min(min(r.x, r.y), r.z), r.w), 0);
+    return max(max(static_cast<uint32_t>(hi), 0u - static_cast<uint32_t>(lo)), 1u);
+}
+
+// G32 shift of a maximum m >= 1: msb(m) - 6, floored at 0.
+__device__ __forceinline__ uint32_t g32_shift1(uint32_t m) {
+    return static_cast<uint32_t>(max(25 - __builtin_clz(m), 0));
+}
+
+__device__ __forceinline__ uint32_t pack_code_bytes(int32_t c0, int32_t c1, int32_t c2, int32_t c3) {
+    const uint32_t lo = __builtin_amdgcn_perm(static_cast<uint32_t>(c1), static_cast<uint32_t>(c0), 0x0c0c0400u);
+    const uint32_t hi = __builtin_amdgcn_perm(static_cast<uint32_t>(c3), static_cast<uint32_t>(c2), 0x0c0c0400u);
+    return lo | (hi << 16);
+}
+
+// Codes of a quad under any shift (g32_code_byte).
 __device__ __forceinline__ uint32_t quad_codes(int4 r, uint32_t s) {
     return g32_code_byte(r.x, s) | (g32_code_byte(r.y, s) << 8) | (g32_code_byte(r.z, s) << 16) |
            (g32_code_byte(r.w, s) << 24);
 }
 
-__device__ __forceinline__ uint32_t quad_magnitude(int4 r) {
-    return max(max(magnitude(r.x), magnitude(r.y)), max(magnitude(r.z), magnitude(r.w)));
+// Codes of a quad whose shift s is in [1, 23]: sign * min(127, (|r| + 2^(s-1))
+// >> s) is clamp((r + 2^(s-1) - [r < 0]) >> s, -127, 127) with an arithmetic
+// shift (for r < 0 the floor of (r + 2^(s-1) - 1) / 2^s is minus the rounded
+// magnitude), and r + 2^(s-1) < 2^31 because |r| < 2^(s+7) <= 2^30.
+__device__ __forceinline__ int32_t code_mid(int32_t r, uint32_t s, int32_t rnd) {
+    return min(max((r + rnd + (r >> 31)) >> s, -127), 127);
+}
+__device__ __forceinline__ uint32_t quad_codes_mid(int4 r, uint32_t s) {
+    const int32_t rnd = static_cast<int32_t>(1u << (s - 1u));
+    return pack_code_bytes(code_mid(r.x, s, rnd), code_mid(r.y, s, rnd), code_mid(r.z, s, rnd),
+                           code_mid(r.w, s, rnd));
 }
 
-// Grid (ceil(n / kAppendTokens), 8): wave = head (4 per workgroup).  All of
-// a wave's loads (k, v and the RoPE pairs of every row) go out before any
-// row is quantized; rows past n load the last token and store nothing.  The
-// append rule is the step's (row_codes): per G32 group the shift of the
-// magnitude maximum, then the round-half-away codes.
+template <bool NT>
+__device__ __forceinline__ v4i load_quad_bits(const void* base, size_t elem) {
+    const v4i* p = reinterpret_cast<const v4i*>(static_cast<const int32_t*>(base) + elem);
+    if constexpr (NT) return __builtin_nontemporal_load(p);
+    else return *p;
+}
+
+// Grid (ceil(n / kAppendTokens), 8): wave = head (4 per workgroup), with
+// kAppendPairs row pairs per wave.  All of a wave's k, v and RoPE loads go
+// out first; rows past n load the last token and store nothing.  The append
+// rule is the step's (row_codes): per G32 group the shift of the magnitude
+// maximum, then the round-half-away codes.  Wave-uniform branches keep the
+// common case short: a wave with a NaN among its FP32 inputs converts them
+// again by the NaN rule, and a row pair with a group shift of 0 or above 23
+// forms its codes by the general rule.
 template <bool Q17>
 __global__ __launch_bounds__(256) void append_bulk_kernel(BulkArgs a) {
     // wave-uniform through readfirstlane, so the page's buffer resource stays in SGPRs
     const int h = blockIdx.y * 4 + __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int lane = threadIdx.x & 63;
-    const int half = lane >> 5, cl = lane & 31;   // row of the pair; channels 4cl .. 4cl+3 (pairs 2cl, 2cl+1)
-    const int t0 = blockIdx.x * kAppendTokens;
-    int4 cs[kAppendRounds], ki[kAppendRounds], vi[kAppendRounds];
+    const int half = lane >> 5, cl = lane & 31;   // row of a pair; channels 4cl .. 4cl+3 (pairs 2cl, 2cl+1)
+    const int t0 = blockIdx.x * kAppendTokens;    // < n: the grid has ceil(n / kAppendTokens) rows
+    int4 cs[kAppendPairs];
+    v4i kq[kAppendPairs], vq[kAppendPairs];       // FP32 or Q15.17 bits
 #pragma unroll
-    for (int j = 0; j < kAppendRounds; ++j) {
+    for (int j = 0; j < kAppendPairs; ++j) {
         const int t = min(t0 + 2 * j + half, a.n - 1);
         const size_t elem = static_cast<size_t>(t) * kModelDim + h * kHeadDim + 4 * cl;
         cs[j] = *reinterpret_cast<const int4*>(a.lut + static_cast<size_t>(a.pos0 + t) * kRopePairs + 2 * cl);
-        ki[j] = load_quad<Q17>(a.k, elem);
-        vi[j] = load_quad<Q17>(a.v, elem);
+        kq[j] = load_quad_bits<kAppendNontemporal>(a.k, elem);
+        vq[j] = load_quad_bits<kAppendNontemporal>(a.v, elem);
+    }
+    int4 ki[kAppendPairs], vi[kAppendPairs];
+    if constexpr (Q17) {
+#pragma unroll
+        for (int j = 0; j < kAppendPairs; ++j) {
+            ki[j] = make_int4(kq[j].x, kq[j].y, kq[j].z, kq[j].w);
+            vi[j] = make_int4(vq[j].x, vq[j].y, vq[j].z, vq[j].w);
+        }
+    } else {
+        // isunordered(x, y): either is NaN, one compare per pair of values,
+        // whose lane masks combine on the scalar unit
+        uint64_t nan = 0;
+#pragma unroll
+        for (int j = 0; j < kAppendPairs; ++j) {
+            const v4f k4 = __builtin_bit_cast(v4f, kq[j]), v4 = __builtin_bit_cast(v4f, vq[j]);
+            const float4 kf = make_float4(k4.x, k4.y, k4.z, k4.w), vf = make_float4(v4.x, v4.y, v4.z, v4.w);
+            ki[j] = quad_q17_no_nan(kf);
+            vi[j] = quad_q17_no_nan(vf);
+            nan |= __builtin_amdgcn_ballot_w64(__builtin_isunordered(kf.x, kf.y)) |
+                   __builtin_amdgcn_ballot_w64(__builtin_isunordered(kf.z, kf.w)) |
+                   __builtin_amdgcn_ballot_w64(__builtin_isunordered(vf.x, vf.y)) |
+                   __builtin_amdgcn_ballot_w64(__builtin_isunordered(vf.z, vf.w));
+        }
+        if (nan != 0) {
+#pragma unroll
+            for (int j = 0; j < kAppendPairs; ++j) {
+                const v4f k4 = __builtin_bit_cast(v4f, kq[j]), v4 = __builtin_bit_cast(v4f, vq[j]);
+                ki[j] = quad_q17(make_float4(k4.x, k4.y, k4.z, k4.w));
+                vi[j] = quad_q17(make_float4(v4.x, v4.y, v4.z, v4.w));
+            }
+        }
     }
     const __amdgpu_buffer_rsrc_t page = __builtin_amdgcn_make_buffer_rsrc(
         page_ptr(a.kv, a.slot, a.layer, h), static_cast<short>(0), static_cast<int32_t>(a.kv.page_bytes), kBufferWord3);
     const int cap = a.kv.seq_cap;
 #pragma unroll
-    for (int j = 0; j < kAppendRounds; ++j) {
-        if (t0 + 2 * j >= a.n) break;                  // wave-uniform: neither row of the pair exists
+    for (int j = 0; j < kAppendPairs; ++j) {
+        if (t0 + 2 * j >= a.n) break;              // wave-uniform: neither row of the pair exists
         int4 k;
-        rope_pair(ki[j].x, ki[j].y, make_int2(cs[j].x, cs[j].y), k.x, k.y);
-        rope_pair(ki[j].z, ki[j].w, make_int2(cs[j].z, cs[j].w), k.z, k.w);
-        const uint32_t sk = g32_shift(octet_max_u(quad_magnitude(k)));
-        const uint32_t sv = g32_shift(octet_max_u(quad_magnitude(vi[j])));
-        const uint32_t kw = quad_codes(k, sk), vw = quad_codes(vi[j], sv);
-        if (t0 + 2 * j + half < a.n) {                 // the pair's second row may be past n
-            const int row = a.pos0 + t0 + 2 * j;       // first row of the pair (SGPR); this lane's is row + half
+        rope_pair_f64(ki[j].x, ki[j].y, make_int2(cs[j].x, cs[j].y), k.x, k.y);
+        rope_pair_f64(ki[j].z, ki[j].w, make_int2(cs[j].z, cs[j].w), k.z, k.w);
+        const uint32_t sk = g32_shift1(octet_max_u(quad_magnitude1(k)));
+        const uint32_t sv = g32_shift1(octet_max_u(quad_magnitude1(vi[j])));
+        uint32_t kw, vw;
+        if (__builtin_amdgcn_ballot_w64(sk - 1u >= 23u || sv - 1u >= 23u) == 0) {
+            kw = quad_codes_mid(k, sk);
+            vw = quad_codes_mid(vi[j], sv);
+        } else {
+            kw = quad_codes(k, sk);
+            vw = quad_codes(vi[j], sv);
+        }
+        if (t0 + 2 * j + half < a.n) {             // the pair's second row may be past n
+            const int row = a.pos0 + t0 + 2 * j;   // first row of the pair (SGPR); this lane's is row + half
             __builtin_amdgcn_raw_buffer_store_b32(kw, page, half * kCodeBytes + 4 * cl, row * kCodeBytes, 0);
             __builtin_amdgcn_raw_buffer_store_b32(vw, page, half * kCodeBytes + 4 * cl, (cap + row) * kCodeBytes, 0);
             if ((cl & 7) == 0) {

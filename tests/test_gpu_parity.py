@@ -271,6 +271,62 @@ def test_records_export_import(skv, ctx, lut4096, rope_tables):
     kv.close()
 
 
+def _special_rows(seed, n):
+    """FP32 K/V rows [n][4096] of N(0,1) values with planted special cases, each
+    confined to a few (row, head) pairs so that the waves holding them and
+    their neighbours take different branches of the bulk append."""
+    f = np.float32
+    bits = lambda u: np.array(u, np.uint32).view(f)
+    k, v = f32_normal(seed, (n, 4096)), f32_normal(seed + 1, (n, 4096))
+    nan_pos, nan_neg, snan_pos, snan_neg = bits([0x7fc00000, 0xffc00000, 0x7f800001, 0xff800001])
+    # NaN of both signs (quiet and signalling), in K of head 0 and V of head 5
+    k[3, 0:4] = [nan_pos, nan_neg, snan_pos, snan_neg]
+    v[3, 5 * 128 + 40:5 * 128 + 42] = [nan_neg, nan_pos]
+    # infinities and values past the Q15.17 range: saturation, shifts 24 and 25
+    k[10, 128:134] = [np.inf, -np.inf, 3e38, -3e38, 16384.0, -16384.0]
+    v[10, 128:132] = [np.inf, -1e30, 20000.0, -20000.0]
+    # one group holding INT32_MIN beside a near-maximum positive value (shift 25)
+    v[12, 3 * 128:3 * 128 + 4] = [-16384.0, 16383.99, 16383.5, -0.25]
+    # the largest values of the common code path: maximum just below 2^30 (shift 23)
+    v[14, 4 * 128:4 * 128 + 32] = np.linspace(-8191.99, 8191.99, 32, dtype=f)
+    # all-zero and tiny groups (shift 0); subnormals, signed zeros, conversion ties
+    k[20, 2 * 128:2 * 128 + 32] = 0.0
+    v[20, 2 * 128:2 * 128 + 32] = np.array([0.0, -0.0, 1e-45, -1e-45, 1e-40, 2.0 ** -18, -2.0 ** -18, 3 * 2.0 ** -18,
+                                            -3 * 2.0 ** -18, 5 * 2.0 ** -18, 127 * 2.0 ** -17, -127 * 2.0 ** -17]
+                                           + [0.0] * 20, f)
+    # code ties at shift 1: |r| = 255, 129, 3, 1 round half away from zero, 255 clamps to 127
+    v[21, 6 * 128:6 * 128 + 8] = np.array([255, -255, 129, -129, 3, -3, 1, -1], f) * f(2.0 ** -17)
+    v[21, 6 * 128 + 8:6 * 128 + 32] = 0.0
+    # a whole row of specials across every head
+    k[30, :] = np.resize(np.array([nan_pos, np.inf, -np.inf, -16384.0, 1e-40, -0.0, 8191.0, -3.5], f), 4096)
+    return k, v
+
+
+def test_prefill_special_values(skv, ctx, lut4096, rope_tables):
+    """Bulk append of rows with NaN, infinities, saturating values, groups whose
+    shift is 0, 23, 24 or 25, subnormals, signed zeros and rounding ties, in two
+    calls (the second starting at an odd position, 61 rows in all, so the last
+    row pair is half past the end): every code and scale equals the oracle's."""
+    _note("case: bulk append of special values")
+    cos, sin = rope_tables
+    n = 61
+    kh, vh = _special_rows(4242, n)
+    kv = skv.KVCache(ctx, layers=1, max_batch=1, max_seq_len=64)
+    for t0, t1 in ((0, 17), (17, n)):
+        dk, dv = ctx.to_device(kh[t0:t1]), ctx.to_device(vh[t0:t1])
+        skv.swiftkv_append_tokens(ctx, dk, dv, kv, lut4096, 0, 0, t0, t1 - t0)
+        ctx.synchronize()
+        dk.free()
+        dv.free()
+    sc = oracle_sequence(cos, sin, kh, vh, n)
+    # the planted cases reach the shifts they are meant to
+    assert sc.vs[3, 12, 0] == 25 and sc.vs[4, 14, 0] == 23 and sc.ks[2, 20, 0] == 0 and sc.vs[6, 21, 0] == 1
+    assert_rows_equal(kv, sc, 0, 0, 0, n)
+    kc, vc, ks, vs = kv.read(0, 0, 0, n, 64 - n)
+    assert not kc.any() and not vc.any() and not ks.any() and not vs.any(), "rows past the prompt were written"
+    kv.close()
+
+
 @pytest.mark.parametrize("dist,outliers", [(0, False), (0, True), (1, False)])
 def test_synthetic_fill_is_the_append_rule(skv, ctx, lut4096, rope_tables, dist, outliers):
     """The device cache filler equals the oracle's append rule applied to the
