@@ -266,7 +266,7 @@ def run_gpu(skv, ctx, positions, layers, steps, warmup, seed, outliers=False, di
     return res
 
 
-def run_prefill(skv, ctx, tokens, layers, reps, seed):
+def run_prefill(skv, ctx, tokens, layers, reps, seed, modes=("own", "shared")):
     """swiftkv_append_tokens: the append rule (conversion, RoPE of k at its own
     position, G32 quantization) over a `tokens`-long prompt of one sequence,
     every layer; bytes = FP32 k and v read plus the 288-B rows written.  Each
@@ -281,7 +281,7 @@ def run_prefill(skv, ctx, tokens, layers, reps, seed):
         ctx.fill_synthetic(ks[layer], n, seed, 2 * layer)
         ctx.fill_synthetic(vs[layer], n, seed, 2 * layer + 1)
     per_layer_s = {}
-    for mode in ("own", "shared"):
+    for mode in modes:
         def prompt():
             for layer in range(layers):
                 i = layer if mode == "own" else 0
@@ -298,12 +298,17 @@ def run_prefill(skv, ctx, tokens, layers, reps, seed):
     kv.close()
     lut.close()
     bytes_per_layer = tokens * 32 * (2 * 128 * 4 + TOKEN_HEAD_BYTES)
-    t, t_shared = per_layer_s["own"], per_layer_s["shared"]
-    return {"us_per_layer": round(t * 1e6, 2), "gbps": round(bytes_per_layer / t / 1e9, 1),
-            "tokens_per_s": round(tokens / t / layers, 1),
-            "one_kv_for_all_layers": {"us_per_layer": round(t_shared * 1e6, 2),
-                                      "gbps": round(bytes_per_layer / t_shared / 1e9, 1)},
-            "sample": f"{reps} prompts of {tokens} tokens x {layers} layers, one sequence, each layer its own k/v"}
+    res = {}
+    if "own" in per_layer_s:
+        t = per_layer_s["own"]
+        res = {"us_per_layer": round(t * 1e6, 2), "gbps": round(bytes_per_layer / t / 1e9, 1),
+               "tokens_per_s": round(tokens / t / layers, 1)}
+    if "shared" in per_layer_s:
+        t = per_layer_s["shared"]
+        res["one_kv_for_all_layers"] = {"us_per_layer": round(t * 1e6, 2), "gbps": round(bytes_per_layer / t / 1e9, 1)}
+    res["bytes_per_layer"] = bytes_per_layer
+    res["sample"] = f"{reps} prompts of {tokens} tokens x {layers} layers, one sequence, each layer its own k/v"
+    return res
 
 
 def run_host_io(skv, ctx, batch, context, reps, seed):
@@ -496,6 +501,10 @@ def main():
                     help="steps of the integer-compatibility entry to time (0 = skip)")
     ap.add_argument("--parts", type=int, default=4,
                     help="also time the step fed by this many split-K FP32 partials (0 = skip)")
+    ap.add_argument("--prefill", type=int, default=0, metavar="TOKENS",
+                    help="only time swiftkv_append_tokens over a prompt of TOKENS tokens, --layers layers, "
+                         "--steps prompts, each layer reading its own k/v (--prefill-shared: one k/v for all)")
+    ap.add_argument("--prefill-shared", action="store_true")
     ap.add_argument("--calibrate", action="store_true",
                     help="only run the FP32->Q15.17 conversion kernel over 256 Mi elements (a copy of known "
                          "size: 1 GiB read, 1 GiB written per launch) to scale HBM byte counters")
@@ -517,6 +526,14 @@ def main():
         ctx.synchronize()
         print(json.dumps({"calibration": "convert_kernel", "elements": n, "read_bytes": 4 * n,
                           "write_bytes": 4 * n, "launches": 3}), flush=True)
+        ctx.close()
+        return
+    if args.prefill:
+        r = run_prefill(skv, ctx, args.prefill, args.layers, args.steps, seed=2034,
+                        modes=("shared",) if args.prefill_shared else ("own",))
+        print(json.dumps({"prefill_tokens": args.prefill, "layers": args.layers, "prompts": args.steps,
+                          "inputs": "one k/v for every layer" if args.prefill_shared else "each layer its own k/v",
+                          **r}), flush=True)
         ctx.close()
         return
     ctx.set_split_tokens(args.split)
