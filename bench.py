@@ -21,7 +21,7 @@ the timed region over the step-kernel launches in it), the integer-compatibility
 reference emulator's attention stage timed on this host (cpu_baseline), and
 the secondary configurations under "configs": batch 1 at position 127 (one
 layer), batch 1 at position 2047 (32 layers), batch 64 with attended lengths
-drawn from U{256..4096} (32 layers), batch 16 decoding 512 steps from
+drawn from U{256..4096} (one layer, and 32 layers), batch 16 decoding 512 steps from
 position 32256 to 32767 on Student-t(3) data (one layer), and the batch-64
 call with host-memory inputs and outputs (PCIe included; never `value`).
 The batch-64 and batch-1 workloads are also timed through the entry that
@@ -574,6 +574,9 @@ def main():
         r = run_gpu(skv, ctx, lengths - 1, 32, args.steps, args.warmup, seed=2030)
         extra["batch64_ragged_32layers"] = dict(summary(r), length_seed=4, sum_attended=r["sum_attended"],
                                                 lengths="U{256..4096}")
+        # the same lengths, one layer timed on its own (its 1.3 GB exceeds the 256 MB MALL)
+        r = run_gpu(skv, ctx, lengths - 1, 1, 100, args.warmup, seed=2030, graph=False)
+        extra["batch64_ragged_1layer"] = dict(summary(r, graph=False), length_seed=4, lengths="U{256..4096}")
         sweep = {}
         for b in (2, 4, 8, 16, 32):   # the batch sizes between the two headline ones, 32 layers at context 4096
             r = run_gpu(skv, ctx, np.full(b, args.context - 1), 32, 5, 1, seed=2040 + b, graph=False)
