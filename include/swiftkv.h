@@ -273,9 +273,8 @@ int swiftkv_set_host_io(swiftkv_context* ctx, int32_t enable);
  * one sequence without attending.  k, v: device [n][4096], FP32 when
  * q17 == 0, Q15.17 int32 otherwise, each 16-byte aligned (SWIFTKV_EINVAL
  * otherwise; swiftkv_device_alloc returns such memory).  The reference has
- * no prefill entry; it
- * feeds prompt tokens through the decode step one at a time
- * (host/decode_host.cpp:1340-1556). */
+ * no prefill entry; it feeds prompt tokens through the decode step one at a
+ * time (host/decode_host.cpp:1340-1556). */
 int swiftkv_append_tokens(swiftkv_context* ctx, const void* k, const void* v, int32_t q17,
                           swiftkv_kv_cache* kv_cache, const swiftkv_rope_lut* rope_lut,
                           int32_t layer_index, int32_t seq, int32_t pos0, int32_t n);
