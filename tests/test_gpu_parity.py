@@ -306,7 +306,8 @@ def test_prefill_special_values(skv, ctx, lut4096, rope_tables):
     """Bulk append of rows with NaN, infinities, saturating values, groups whose
     shift is 0, 23, 24 or 25, subnormals, signed zeros and rounding ties, in two
     calls (the second starting at an odd position, 61 rows in all, so the last
-    row pair is half past the end): every code and scale equals the oracle's."""
+    row pair is half past the end): every code and scale equals the oracle's.
+    Then the same rows through the Q15.17 entry."""
     _note("case: bulk append of special values")
     cos, sin = rope_tables
     n = 61
@@ -324,6 +325,17 @@ def test_prefill_special_values(skv, ctx, lut4096, rope_tables):
     assert_rows_equal(kv, sc, 0, 0, 0, n)
     kc, vc, ks, vs = kv.read(0, 0, 0, n, 64 - n)
     assert not kc.any() and not vc.any() and not ks.any() and not vs.any(), "rows past the prompt were written"
+    # the Q15.17 entry on the converted rows (INT32_MIN and INT32_MAX among them) writes the same rows
+    kq, vq = O.f2q17(kh), O.f2q17(vh)
+    assert (kq == np.iinfo(np.int32).min).any() and (vq == np.iinfo(np.int32).max).any()
+    kv.zero()
+    for t0, t1 in ((0, 33), (33, n)):
+        dk, dv = ctx.to_device(kq[t0:t1]), ctx.to_device(vq[t0:t1])
+        skv.swiftkv_append_tokens(ctx, dk, dv, kv, lut4096, 0, 0, t0, t1 - t0, q17=True)
+        ctx.synchronize()
+        dk.free()
+        dv.free()
+    assert_rows_equal(kv, sc, 0, 0, 0, n)
     kv.close()
 
 
