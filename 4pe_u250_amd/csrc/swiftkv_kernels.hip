@@ -717,7 +717,10 @@ __global__ __launch_bounds__(WAVES * 64) void step_kernel(StepArgs a) {
 
 // Prefill rows: one instruction covers two token rows (lane l takes channels
 // 4(l & 31) .. 4(l & 31) + 3 of row l >> 5), and a wave takes kAppendPairs
-// such pairs with all of their loads in flight together.
+// such pairs with all of their loads in flight together.  One pair per wave
+// and default-policy k/v loads measured fastest: more pairs per wave cost
+// occupancy, and nontemporal loads lose the MALL hits of k/v that a
+// projection has just written.
 constexpr int kAppendPairs = 1;
 constexpr int kAppendTokens = 2 * kAppendPairs;
 constexpr bool kAppendNontemporal = false;
