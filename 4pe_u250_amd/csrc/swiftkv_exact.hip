@@ -34,7 +34,7 @@ namespace {
 using namespace dev;
 
 constexpr int kChunk = 256;                   // cached tokens per chunk (V codes staged in LDS)
-constexpr int kBatch = 16;                    // tokens whose LDS reads go out together in the Y pass
+constexpr int kBatch = 8;                     // tokens whose LDS reads go out together in the Y pass
 static_assert(kChunk % kBatch == 0, "batches tile a chunk");
 static_assert(kBatch % 8 == 0 && 64 % kBatch == 0, "a batch is whole 8-byte shift reads inside one 64-token ballot");
 constexpr int kPasses = kChunk / 32;          // score passes per chunk: 4 waves x 8 token rows each
@@ -197,6 +197,16 @@ __device__ __forceinline__ int32_t value_term(int32_t code, uint32_t shift, uint
     return (m + static_cast<int32_t>(0xffffu >> shift) + bit) >> k;
 }
 
+// The term when the shift is at most 16 (V groups below 64.0, the common
+// case): x is the code itself, k = 17 - shift >= 1, and the rounding offset
+// 2^(k-1) - 1 is 0xffff >> shift.
+__device__ __forceinline__ int32_t value_term_small(int32_t code, uint32_t shift, uint32_t coef) {
+    const int32_t m = __mul24(code, static_cast<int32_t>(coef));
+    const uint32_t k = 17u - shift;
+    const int32_t bit = static_cast<int32_t>(__builtin_amdgcn_ubfe(static_cast<uint32_t>(m), k, 1u));
+    return (m + static_cast<int32_t>(0xffffu >> shift) + bit) >> k;
+}
+
 __device__ __forceinline__ int32_t value_step(int32_t y, uint32_t word, int32_t code, uint32_t shift, int32_t term) {
     if (word & kInit) return dequant_raw(code, shift);
     if (word & kRescale) return __builtin_elementwise_add_sat(mulq17_wrap(y, word & kCoefMask), dequant_raw(code, shift));
@@ -282,8 +292,18 @@ __device__ __forceinline__ void batch_terms(const uint32_t* s_coef, const uint8_
         code[j] = s_vc[i0 + j][ch];
         sh[j] = (shw[j >> 2] >> (8 * (j & 3))) & 0xffu;
     }
+    // A shift byte s is 17 or more exactly when s + 111 sets its top bit (no
+    // byte carries: s <= 25); a wave holding none takes the short form.
+    uint32_t big = 0;
 #pragma unroll
-    for (int j = 0; j < kBatch; ++j) term[j] = value_term(code[j], sh[j], coef[j]);
+    for (int q = 0; q < kBatch / 4; ++q) big |= shw[q] + 0x6f6f6f6fu;
+    if (__builtin_amdgcn_ballot_w64((big & 0x80808080u) != 0u) == 0) {
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) term[j] = value_term_small(code[j], sh[j], coef[j]);
+    } else {
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) term[j] = value_term(code[j], sh[j], coef[j]);
+    }
 }
 
 struct ExactArgs {
