@@ -120,11 +120,14 @@ __device__ __forceinline__ QueryLimbs split_query(const int32_t* q) {
 // The exact sum is taken limb by limb: four signed-byte dot products per limb
 // (each limb's sum stays within 16 * 128 * 128 = 2^18), then combined in 64
 // bits, so it equals the sum of the 16 full products.
+// NL = 3 when the wave's query limbs 3 and 4 are all zero (|q| below about
+// 2^23, i.e. |q| < 64.0, the common case): those limbs add nothing.
+template <int NL>
 __device__ __forceinline__ int64_t half_dot(const QueryLimbs& L, int4 w, uint32_t shift) {
     const int32_t d[4] = {w.x, w.y, w.z, w.w};
     int64_t s = 0;
 #pragma unroll
-    for (int k = 4; k >= 0; --k) {
+    for (int k = NL - 1; k >= 0; --k) {
         int32_t acc = 0;
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_sdot4(L.w[k][j], d[j], acc, false);
@@ -384,6 +387,12 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
         for (int j = 0; j < 16; ++j) qc[j] = s_q[16 * c + j];
         ql = split_query(qc);
     }
+    // Limbs 3 and 4 zero in every lane of the wave: three-limb dot products.
+    // (With four workgroups per head, at batch 1 and 2, the branch measured
+    // 1% slower, so those launches keep five.)
+    const bool q3 = SLICES == 1 &&
+                    __builtin_amdgcn_ballot_w64((ql.w[3][0] | ql.w[3][1] | ql.w[3][2] | ql.w[3][3] | ql.w[4][0] |
+                                                 ql.w[4][1] | ql.w[4][2] | ql.w[4][3]) != 0) == 0;
 
     const int len = pos + 1;
     int32_t run_max = INT32_MIN;   // prefix maximum before the chunk (every thread)
@@ -431,7 +440,8 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
             const int i = wave * 8 + r + 32 * ps;
             const int4 kw = make_int4(kq[ps].x, kq[ps].y, kq[ps].z, kq[ps].w);
             // the token's sum of its 8 half-groups (lanes 8r .. 8r+7), exact
-            const int64_t p = octet_sum64(half_dot(ql, kw, shift_of(__uint_as_float(scl[ps].x))));
+            const uint32_t ksh = shift_of(__uint_as_float(scl[ps].x));
+            const int64_t p = octet_sum64(q3 ? half_dot<3>(ql, kw, ksh) : half_dot<5>(ql, kw, ksh));
             // slots past n are read by the Y pass with a zero coefficient
             if ((c & 1) == 0) s_vs[c >> 1][i] = i < n ? static_cast<uint8_t>(shift_of(__uint_as_float(scl[ps].y))) : 0;
             if (c == 0 && i < n) s_tok[i] = static_cast<uint32_t>(score_of(p));

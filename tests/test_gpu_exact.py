@@ -95,15 +95,20 @@ def test_exact_matches_reference_decode(skv, ctx, lut4096, golden, case):
     kv.close()
 
 
-@pytest.mark.parametrize("positions,dist,q17", [
-    ([0, 1, 255, 256], "normal", False),
-    ([257, 511, 512, 1030], "t3", False),
-    ([1500, 77], "t3", True),
-    ([300, 700], "wide", False),
-    ([300, 700, 5, 257, 256, 511, 1, 0, 64], "wide", False),
+@pytest.mark.parametrize("positions,dist,q17,big_query", [
+    ([0, 1, 255, 256], "normal", False, False),
+    ([257, 511, 512, 1030], "t3", False, False),
+    ([1500, 77], "t3", True, False),
+    ([300, 700], "wide", False, False),
+    ([300, 700, 5, 257, 256, 511, 1, 0, 64], "wide", False, False),
+    ([300, 1030, 1], "normal", False, True),   # one workgroup per head
+    ([700], "t3", False, True),                # four workgroups per head
 ])
-def test_exact_matches_oracle_integer_recurrence(skv, ctx, lut4096, rope_tables, positions, dist, q17):
-    _note(f"case: exact vs oracle, positions {positions}, {dist}, q17={q17}")
+def test_exact_matches_oracle_integer_recurrence(skv, ctx, lut4096, rope_tables, positions, dist, q17, big_query):
+    """big_query: queries past 64.0 in some heads (and saturated channels in
+    one), so the query's upper byte limbs are nonzero and the score dot
+    products take all five limbs; the other heads keep the three-limb form."""
+    _note(f"case: exact vs oracle, positions {positions}, {dist}, q17={q17}, big query={big_query}")
     cos, sin = rope_tables
     seed = 500 + positions[0]
     outl = outlier_channels(seed)
@@ -119,7 +124,12 @@ def test_exact_matches_oracle_integer_recurrence(skv, ctx, lut4096, rope_tables,
     k = f32_normal(seed + 1001, (B, 4096))
     v = f32_normal(seed + 1002, (B, 4096))
     k[:, outl] *= np.float32(20.0)
+    if big_query:
+        q[:, 0:16 * 128] *= np.float32(300.0)                        # heads 0-15 beyond 64.0
+        q[:, 5 * 128:5 * 128 + 8] = np.float32([3e4, -3e4, 1e9, -1e9, 2e4, -2e4, 17000.0, -16384.0])
     qq, kq, vq = O.f2q17(q), O.f2q17(k), O.f2q17(v)
+    if big_query:
+        assert (np.abs(qq[:, :16 * 128].astype(np.int64)) >= 1 << 23).any() and (qq == np.iinfo(np.int32).min).any()
     if q17:
         out, aq, asc = exact_step(skv, ctx, kv, lut4096, layer, positions, qq, kq, vq, q17=True)
     else:
