@@ -272,7 +272,7 @@ __device__ __forceinline__ uint64_t uniform64(uint64_t v) {
 // The codes, shifts and Y terms of tokens [i0, i0 + kBatch) for channel ch:
 // 16-byte reads give the coefficients, 8-byte reads the shifts (stored by
 // group), and one byte read per token the code.
-__device__ __forceinline__ void batch_terms(const uint32_t* s_coef, const uint8_t* s_vs_g,
+__device__ __forceinline__ bool batch_terms(const uint32_t* s_coef, const uint8_t* s_vs_g,
                                             const int8_t (*s_vc)[kHeadDim], int i0, int ch, int32_t* code,
                                             uint32_t* sh, int32_t* term) {
     uint32_t coef[kBatch], shw[kBatch / 4];
@@ -303,11 +303,14 @@ __device__ __forceinline__ void batch_terms(const uint32_t* s_coef, const uint8_
     if (__builtin_amdgcn_ballot_w64((big & 0x80808080u) != 0u) == 0) {
 #pragma unroll
         for (int j = 0; j < kBatch; ++j) term[j] = value_term_small(code[j], sh[j], coef[j]);
-    } else {
-#pragma unroll
-        for (int j = 0; j < kBatch; ++j) term[j] = value_term(code[j], sh[j], coef[j]);
+        return true;
     }
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) term[j] = value_term(code[j], sh[j], coef[j]);
+    return false;
 }
+// A short-form term is at most (2^25 + 2^16) / 2 < 2^24 + 2^15 in magnitude.
+constexpr int64_t kShortTermBound = (1 << 24) + (1 << 15);
 
 struct ExactArgs {
     StepArgs step;
@@ -331,6 +334,12 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
     // operations against 12, so about 9/16 with one composed part; with six,
     // 2/16 measured best (the composed runs round up to whole batches).
     constexpr int kSeqShare16 = kCompParts == 1 ? 9 : 2;
+    // The longest composed run (the rest of a chunk after the ordered share,
+    // split into kCompParts runs of whole batches): its short-form terms sum
+    // within int32.
+    constexpr int kMaxRun =
+        ((kChunk * (16 - kSeqShare16) / 16 + kCompParts - 1) / kCompParts + kBatch - 1) / kBatch * kBatch;
+    static_assert(kMaxRun * kShortTermBound < (int64_t(1) << 31), "short-form sums of a run fit in 32 bits");
     const StepArgs& a = ea.step;
     const uint32_t row = a.rows[blockIdx.y];
     const int h = blockIdx.x / SLICES, slice = blockIdx.x % SLICES, b = static_cast<int>(row & 0xffu);
@@ -552,18 +561,28 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
             const int begin = split + cp * q, end = min(n, begin + q);
             if (begin < n) {
                 int64_t sum = 0;
+                int32_t sum_short = 0;   // the short-form batches' terms (see kMaxRun)
                 int32_t lo = INT32_MIN, hi = INT32_MAX;
                 for (int i0 = begin; i0 < end; i0 += kBatch) {
                     int32_t code[kBatch], term[kBatch];
                     uint32_t sh[kBatch];
-                    batch_terms(s_tok, s_vs[g], s_vc, i0, ch, code, sh, term);
+                    if (batch_terms(s_tok, s_vs[g], s_vc, i0, ch, code, sh, term)) {
 #pragma unroll
-                    for (int j = 0; j < kBatch; ++j) {
-                        sum += term[j];
-                        lo = __builtin_elementwise_add_sat(lo, term[j]);
-                        hi = __builtin_elementwise_add_sat(hi, term[j]);
+                        for (int j = 0; j < kBatch; ++j) {
+                            sum_short += term[j];
+                            lo = __builtin_elementwise_add_sat(lo, term[j]);
+                            hi = __builtin_elementwise_add_sat(hi, term[j]);
+                        }
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < kBatch; ++j) {
+                            sum += term[j];
+                            lo = __builtin_elementwise_add_sat(lo, term[j]);
+                            hi = __builtin_elementwise_add_sat(hi, term[j]);
+                        }
                     }
                 }
+                sum += sum_short;
                 s_map_sum[cp * kCh + cl] = sum;
                 s_map_lo[cp * kCh + cl] = lo;
                 s_map_hi[cp * kCh + cl] = hi;
