@@ -37,7 +37,7 @@ constexpr int kWideWaves = 16;
 constexpr int kWideBlockTokens = 32;
 constexpr int kWideRoundTokens = kWideWaves * kWideBlockTokens;   // 512
 constexpr int kSplitQuantum = kAttendWaves * kBlockTokens;   // 256
-constexpr int kMaxSeq = 32768;                   // longest cache this build accepts
+constexpr int kMaxSeq = 32768;                   // longest cache accepted (tokens per sequence)
 constexpr int kMaxSplits = kMaxSeq / kSplitQuantum;   // 128 partials per (sequence, head)
 
 // A split's partial (m, l, acc[128]) travels as kSlotWords 64-bit words, each

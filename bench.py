@@ -429,7 +429,7 @@ def cpu_fp32_oracle(target_seconds: float, position: int):
     """The FP32 tolerance oracle (oracle/swiftkv_oracle.c: the append rule,
     then the FP32 softmax formula with double accumulation) on this host, one
     thread, one sequence x 32 heads per call at `position`.  Timed separately
-    from the reference: it is the checker, not the reference."""
+    from the reference: it is the oracle, not the reference."""
     cos, sin, sc, (q, k, v) = _cpu_cache(position)
     sc.step_q17(q, k, v, position, cos[position], sin[position], fp=True)   # warm-up call
     times = []
@@ -510,7 +510,7 @@ def main():
                          "size: 1 GiB read, 1 GiB written per launch) to scale HBM byte counters")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (the path shards by "
+        print(json.dumps({"error": "this benchmark runs on one GPU; --gpus must be 1 (the path shards by "
                                    "head/sequence across GPUs by design only)"}))
         sys.exit(2)
 

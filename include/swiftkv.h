@@ -49,7 +49,7 @@ extern "C" {
 #define SWIFTKV_GROUP 32
 #define SWIFTKV_GROUPS_PER_HEAD (SWIFTKV_HEAD_DIM / SWIFTKV_GROUP)
 /* Reference limits: position is ap_uint<12>, SWIFTKV_MAX_SEQ_LEN = 4096
- * (hpp:26-30).  This build accepts longer caches (up to 32768 tokens) with the
+ * (hpp:26-30).  The library accepts longer caches (up to 32768 tokens) with the
  * RoPE table extended by the same closed form. */
 #define SWIFTKV_REFERENCE_MAX_SEQ 4096
 #define SWIFTKV_MAX_SEQ 32768

@@ -1,7 +1,7 @@
 /*
  * swiftkv_oracle.c -- CPU restatement of the SwiftKV decode-attention arithmetic.
  *
- * TEST INFRASTRUCTURE ONLY.  This file is the checker for the HIP path: only
+ * TEST INFRASTRUCTURE ONLY.  This file is the oracle for the HIP path: only
  * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg load it, and
  * only to compare against or to time as a baseline.  The product library
  * (4pe_u250_amd/csrc) never links or calls it.

@@ -114,7 +114,7 @@ def assert_rows_equal(kv, sc, seq, layer, tok0, n, heads=range(H)):
         assert (vs.view(np.uint32) == O.shift_scale_bits(sc.vs[h, tok0:tok0 + n])).all(), f"seq {seq} head {h}: V scales"
 
 
-RTOL, ATOL = 1e-4, 2e-5   # north-star tolerance vs the FP32 formula
+RTOL, ATOL = 1e-4, 2e-5   # tolerance vs the FP32 formula (double-precision oracle)
 
 
 def assert_close(got, ref, what=""):
