@@ -81,6 +81,9 @@ def profile_summary(batch: int, context: int, ragged: bool = False):
         key, sep, rest = line.partition(":")
         if sep and key.strip() in PROFILE_KEYS:
             text = rest.strip()
+            if key.strip() == "commit":
+                vals["commit"] = text
+                continue
             try:
                 vals[key.strip()] = float(text) if "." in text or "e" in text else int(text)
             except ValueError:

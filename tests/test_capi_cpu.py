@@ -195,3 +195,23 @@ def test_step_plan_argument_checks(skv):
     bad = np.array([10, 32768], np.int32)
     assert plan(positions=bad.ctypes.data_as(C.c_void_p)) == skv.ERANGE
     assert b"position 32768" in L.swiftkv_last_error()
+
+
+def test_bench_reads_committed_profiles():
+    """bench.py copies the committed rocprofv3 summaries' figures into its
+    roofline; the commit stays text (a hash such as 84e0131 is not a number)."""
+    import importlib.util
+    import os
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    spec = importlib.util.spec_from_file_location("bench_under_test", os.path.join(root, "bench.py"))
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    for batch, ragged in ((64, False), (1, False), (64, True)):
+        vals, path = bench.profile_summary(batch, 4096, ragged)
+        assert path is not None, (batch, ragged)
+        got = bench.profile_counters(vals)
+        assert isinstance(got["commit"], str) and len(got["commit"]) >= 7
+        assert 0.99 < got["fetch_ratio"] < 1.1
+        assert 0.0 < got["achieved_occupancy_frac"] <= 1.0
+        assert got["trace_avg_us"] > 0 and got["bench_ms_per_step"] > 0
+    assert bench.profile_summary(3, 4096) == ({}, None)
