@@ -18,13 +18,16 @@
 //     dot products over five limbs of the query;
 //   - one thread per token turns its score and the exclusive prefix maximum
 //     into a coefficient word (exp LUT, rescale flag), and the same pass lays
-//     out prefix sums and ballots for Z and Y;
+//     out, per group, the product of the coefficient and the V scale (exact
+//     in FP32), the per-wave coefficient sums and ballots for Z and Y;
 //   - Y, one channel per thread: the first kCh threads run the chunk's
 //     first part in token order, adding independently formed terms, while
 //     the rest of the threads compose the remaining tokens (no first or
 //     rescaling token among them) into clamp-add maps applied after the
-//     barrier; wave 3 also advances Z by prefix-sum differences and steps
-//     only at first and rescaling tokens;
+//     barrier; a term is one fused multiply-add of the code and the product
+//     when the shift is at most 15, an exact FP32 product and rint at 16,
+//     32-bit integer operations above; wave 3 also advances Z by prefix-sum
+//     differences and steps only at first and rescaling tokens;
 // then Y * 1/Z and the integer-path A14/E8M0 epilogue.
 #include "swiftkv_device.hpp"
 
@@ -36,7 +39,7 @@ using namespace dev;
 constexpr int kChunk = 256;                   // cached tokens per chunk (V codes staged in LDS)
 constexpr int kBatch = 8;                     // tokens whose LDS reads go out together in the Y pass
 static_assert(kChunk % kBatch == 0, "batches tile a chunk");
-static_assert(kBatch % 8 == 0 && 64 % kBatch == 0, "a batch is whole 8-byte shift reads inside one 64-token ballot");
+static_assert(kBatch % 4 == 0 && 64 % kBatch == 0, "a batch is whole 16-byte reads inside one 64-token ballot");
 constexpr int kPasses = kChunk / 32;          // score passes per chunk: 4 waves x 8 token rows each
 // Largest batch whose launch splits each head's Y over 4 workgroups (32
 // channels each): at context 4096 this took batch 1 and 2 from 175 to 147-150
@@ -200,16 +203,6 @@ __device__ __forceinline__ int32_t value_term(int32_t code, uint32_t shift, uint
     return (m + static_cast<int32_t>(0xffffu >> shift) + bit) >> k;
 }
 
-// The term when the shift is at most 16 (V groups below 64.0, the common
-// case): x is the code itself, k = 17 - shift >= 1, and the rounding offset
-// 2^(k-1) - 1 is 0xffff >> shift.
-__device__ __forceinline__ int32_t value_term_small(int32_t code, uint32_t shift, uint32_t coef) {
-    const int32_t m = __mul24(code, static_cast<int32_t>(coef));
-    const uint32_t k = 17u - shift;
-    const int32_t bit = static_cast<int32_t>(__builtin_amdgcn_ubfe(static_cast<uint32_t>(m), k, 1u));
-    return (m + static_cast<int32_t>(0xffffu >> shift) + bit) >> k;
-}
-
 __device__ __forceinline__ int32_t value_step(int32_t y, uint32_t word, int32_t code, uint32_t shift, int32_t term) {
     if (word & kInit) return dequant_raw(code, shift);
     if (word & kRescale) return __builtin_elementwise_add_sat(mulq17_wrap(y, word & kCoefMask), dequant_raw(code, shift));
@@ -269,48 +262,113 @@ __device__ __forceinline__ uint64_t uniform64(uint64_t v) {
            static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(v)));
 }
 
-// The codes, shifts and Y terms of tokens [i0, i0 + kBatch) for channel ch:
-// 16-byte reads give the coefficients, 8-byte reads the shifts (stored by
-// group), and one byte read per token the code.
-__device__ __forceinline__ bool batch_terms(const uint32_t* s_coef, const uint8_t* s_vs_g,
-                                            const int8_t (*s_vc)[kHeadDim], int i0, int ch, int32_t* code,
-                                            uint32_t* sh, int32_t* term) {
-    uint32_t coef[kBatch], shw[kBatch / 4];
+// The Y pass reads, per token and G32 group, the product p = c 2^(s-17) of
+// the token's coefficient c (an integer, at most 2^17) and the group's V
+// scale 2^(s-17); the FP32 product is exact.  The no-rescale term is then
+// RNE(code p), since v c 2^-17 = (code 2^s) c 2^-17 for a shift below 17.
+//
+// Shift at most 15 (V groups below 32.0, the common case): |code p| <= 128
+// 2^15 = 2^22, so code p + 1.5 2^23 lies in [2^23, 2^24), where the floats
+// are the integers.  One fused multiply-add rounds the exact sum once, to
+// nearest even, and 1.5 2^23 is an even integer, so the result is 1.5 2^23 +
+// RNE(code p) and its bit pattern is 0x4b400000 + RNE(code p).
+constexpr float kRoundMagic = 12582912.0f;   // 1.5 * 2^23
+constexpr uint32_t kRoundMagicBits = 0x4b400000u;
+__device__ __forceinline__ uint32_t term_bits(int32_t code, float p) {
+    return __float_as_uint(__builtin_fmaf(static_cast<float>(code), p, kRoundMagic));
+}
+// A term of that form is at most 2^22 in magnitude.
+constexpr int64_t kFastTermBound = int64_t{1} << 22;
+
+// The codes and Y terms of tokens [i0, i0 + kBatch) for channel ch, for any
+// shift: the coefficient words come from 16-byte reads, the products p of the
+// channel's group from 16-byte reads, the codes from one byte read per token.
+// A first or rescaling token's p is its V scale alone (its term is not used).
+// wide17: some token of the batch has a shift of 17 or more.  Otherwise every
+// |code c| <= 2^24 is exact in FP32, so code p is exact and rint gives RNE
+// (the short form, returns true); else the shift is recovered from the
+// exponents of p and c and the 32-bit integer form runs (returns false).
+__device__ __forceinline__ bool slow_terms(const uint32_t* s_words, const float* s_p_g,
+                                           const int8_t (*s_vc)[kHeadDim], int i0, int ch, bool wide17,
+                                           int32_t* code, float* p, int32_t* term) {
+    uint32_t coef[kBatch];
 #pragma unroll
     for (int q = 0; q < kBatch / 4; ++q) {
-        const uint4 cq = *reinterpret_cast<const uint4*>(&s_coef[i0 + 4 * q]);
-        coef[4 * q] = cq.x;
-        coef[4 * q + 1] = cq.y;
-        coef[4 * q + 2] = cq.z;
-        coef[4 * q + 3] = cq.w;
+        const uint4 cq = *reinterpret_cast<const uint4*>(&s_words[i0 + 4 * q]);
+        const float4 pq = *reinterpret_cast<const float4*>(&s_p_g[i0 + 4 * q]);
+        coef[4 * q] = cq.x & kCoefMask;
+        coef[4 * q + 1] = cq.y & kCoefMask;
+        coef[4 * q + 2] = cq.z & kCoefMask;
+        coef[4 * q + 3] = cq.w & kCoefMask;
+        p[4 * q] = pq.x;
+        p[4 * q + 1] = pq.y;
+        p[4 * q + 2] = pq.z;
+        p[4 * q + 3] = pq.w;
     }
 #pragma unroll
-    for (int q = 0; q < kBatch / 8; ++q) {
-        const uint2 sw = *reinterpret_cast<const uint2*>(&s_vs_g[i0 + 8 * q]);
-        shw[2 * q] = sw.x;
-        shw[2 * q + 1] = sw.y;
-    }
+    for (int j = 0; j < kBatch; ++j) code[j] = s_vc[i0 + j][ch];
+    if (!wide17) {
 #pragma unroll
-    for (int j = 0; j < kBatch; ++j) {
-        code[j] = s_vc[i0 + j][ch];
-        sh[j] = (shw[j >> 2] >> (8 * (j & 3))) & 0xffu;
-    }
-    // A shift byte s is 17 or more exactly when s + 111 sets its top bit (no
-    // byte carries: s <= 25); a wave holding none takes the short form.
-    uint32_t big = 0;
-#pragma unroll
-    for (int q = 0; q < kBatch / 4; ++q) big |= shw[q] + 0x6f6f6f6fu;
-    if (__builtin_amdgcn_ballot_w64((big & 0x80808080u) != 0u) == 0) {
-#pragma unroll
-        for (int j = 0; j < kBatch; ++j) term[j] = value_term_small(code[j], sh[j], coef[j]);
+        for (int j = 0; j < kBatch; ++j) term[j] = static_cast<int32_t>(__builtin_rintf(static_cast<float>(code[j]) * p[j]));
         return true;
     }
 #pragma unroll
-    for (int j = 0; j < kBatch; ++j) term[j] = value_term(code[j], sh[j], coef[j]);
+    for (int j = 0; j < kBatch; ++j) {
+        // p = c 2^(s-17) exactly, so s = 17 + exponent(p) - exponent(c); a
+        // zero coefficient gives a zero term for any shift.
+        const uint32_t sh = coef[j] == 0u ? 0u
+                                          : min(17u + shift_of(p[j]) - shift_of(static_cast<float>(coef[j])), 25u);
+        term[j] = value_term(code[j], sh, coef[j]);
+    }
     return false;
 }
-// A short-form term is at most (2^25 + 2^16) / 2 < 2^24 + 2^15 in magnitude.
-constexpr int64_t kShortTermBound = (1 << 24) + (1 << 15);
+// A short-form term is at most 128 2^16 = 2^23 in magnitude.
+constexpr int64_t kShortTermBound = int64_t{1} << 23;
+
+// What the fused-multiply-add terms of tokens [i0, i0 + kBatch) for channel
+// ch read: the products p of the channel's group and the codes.
+struct FastBatch {
+    float p[kBatch];
+    int32_t code[kBatch];
+};
+__device__ __forceinline__ FastBatch load_fast(const float* s_p_g, const int8_t (*s_vc)[kHeadDim], int i0, int ch) {
+    FastBatch f;
+#pragma unroll
+    for (int q = 0; q < kBatch / 4; ++q) {
+        const float4 pq = *reinterpret_cast<const float4*>(&s_p_g[i0 + 4 * q]);
+        f.p[4 * q] = pq.x;
+        f.p[4 * q + 1] = pq.y;
+        f.p[4 * q + 2] = pq.z;
+        f.p[4 * q + 3] = pq.w;
+    }
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) f.code[j] = s_vc[i0 + j][ch];
+    return f;
+}
+// The term bits 0x4b400000 + term of such a batch, every shift at most 15.
+__device__ __forceinline__ void fast_term_bits(const FastBatch& f, uint32_t* tb) {
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) tb[j] = term_bits(f.code[j], f.p[j]);
+}
+constexpr uint64_t kBatchMask = (uint64_t{1} << kBatch) - 1u;
+// No partial sum of a batch of fused-multiply-add terms exceeds this.
+constexpr uint32_t kSatMargin = static_cast<uint32_t>(kBatch * kFastTermBound);
+
+// The per-group products p of a chunk and the query's LDS bytes: shared
+// with one workgroup per head (where LDS bounds the residency: four
+// workgroups per CU), separate with four (three per CU by registers).
+template <int G, int CH>
+union ProductsOrQuery {
+    float p[G][kChunk];
+    int32_t q[kHeadDim];
+    int16_t q14[CH];
+};
+template <int G, int CH>
+struct ProductsAndQuery {
+    float p[G][kChunk];
+    int32_t q[kHeadDim];
+    int16_t q14[CH];
+};
 
 struct ExactArgs {
     StepArgs step;
@@ -330,16 +388,20 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
     constexpr int kCh = kHeadDim / SLICES;
     constexpr int kSeqLanes = kCh < 64 ? 64 : kCh;
     constexpr int kCompParts = (256 - kSeqLanes) / kCh;
-    // The ordered part's share of a chunk: a composed token costs about 15
-    // operations against 12, so about 9/16 with one composed part; with six,
-    // 2/16 measured best (the composed runs round up to whole batches).
+    constexpr int kGroups = kCh / 32;   // G32 groups of this workgroup's channels
+    constexpr bool kPrefetchY = SLICES == 4;   // the Y pass reads a batch ahead (registers allow it)
+    // The ordered part's share of a chunk: with the fused-multiply-add terms a
+    // composed token costs about 4 operations against 3, so about 9/16 with
+    // one composed part; with six, 2/16 (the composed runs round up to whole
+    // batches).
     constexpr int kSeqShare16 = kCompParts == 1 ? 9 : 2;
     // The longest composed run (the rest of a chunk after the ordered share,
-    // split into kCompParts runs of whole batches): its short-form terms sum
-    // within int32.
+    // split into kCompParts runs of whole batches): its short-form terms, and
+    // its prefix sums of fused-multiply-add terms, stay within int32.
     constexpr int kMaxRun =
         ((kChunk * (16 - kSeqShare16) / 16 + kCompParts - 1) / kCompParts + kBatch - 1) / kBatch * kBatch;
     static_assert(kMaxRun * kShortTermBound < (int64_t(1) << 31), "short-form sums of a run fit in 32 bits");
+    static_assert(2 * kMaxRun * kFastTermBound < (int64_t(1) << 31), "a run's prefix-sum range fits in 32 bits");
     const StepArgs& a = ea.step;
     const uint32_t row = a.rows[blockIdx.y];
     const int h = blockIdx.x / SLICES, slice = blockIdx.x % SLICES, b = static_cast<int>(row & 0xffu);
@@ -353,23 +415,31 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
     const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
         page, static_cast<short>(0), static_cast<int32_t>(cap * kTokenBytes), kBufferWord3);
 
-    __shared__ int32_t s_q[kHeadDim];
     // Per token of the chunk: the score, then (each thread rewrites its own
-    // token after reading it) the coefficient alone, zero past n.
+    // token after reading it) the coefficient word, zero past n.
     __shared__ __align__(16) uint32_t s_tok[kChunk];
-    __shared__ uint32_t s_word[kChunk];                  // coefficient words of the chunk
-    __shared__ uint32_t s_psum[kChunk];                  // per-wave inclusive sums of ordinary coefficients
     __shared__ int8_t s_vc[kChunk][kHeadDim];            // V codes of the chunk
-    __shared__ __align__(16) uint8_t s_vs[kGroupsPerHead][kChunk];   // V shifts of the chunk, by group
+    // Per group of this workgroup's channels and token of the chunk: the V
+    // scale (the score pass), then the product p = c 2^(s-17) for ordinary
+    // tokens (the coefficient pass).  The rotated query before the token loop
+    // and the A14 codes after it use the same bytes.
+    __shared__ __align__(16) std::conditional_t<SLICES == 1, ProductsOrQuery<kGroups, kCh>, ProductsAndQuery<kGroups, kCh>>
+        s_u;
     __shared__ int32_t s_wave_max[kChunk / 64];
     __shared__ uint32_t s_wave_sum[kChunk / 64];
-    __shared__ uint64_t s_special[kChunk / 64];          // per-wave ballots of first and rescaling tokens
+    // Per-wave ballots: first and rescaling tokens; those and tokens with a V
+    // shift of 16 or more in this workgroup's groups (the slow form); tokens
+    // with a shift of 17 or more.
+    __shared__ uint64_t s_special[kChunk / 64];
+    __shared__ uint64_t s_slow[kChunk / 64];
+    __shared__ uint64_t s_wide17[kChunk / 64];
     __shared__ int64_t s_map_sum[kCompParts * kCh];      // the composed maps of the parts after split
     __shared__ int32_t s_map_lo[kCompParts * kCh];
     __shared__ int32_t s_map_hi[kCompParts * kCh];
     __shared__ uint32_t s_lut[33];
     __shared__ uint32_t s_inv;
-    __shared__ int16_t s_q14[kCh];
+    int32_t* const s_q = s_u.q;
+    int16_t* const s_q14 = s_u.q14;
     if (threadIdx.x < 33) s_lut[threadIdx.x] = ea.exp_lut[threadIdx.x];
 
     // Wave 0 rotates the query into LDS and appends the new row; the barrier
@@ -396,6 +466,7 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
         for (int j = 0; j < 16; ++j) qc[j] = s_q[16 * c + j];
         ql = split_query(qc);
     }
+    if constexpr (SLICES == 1) __syncthreads();   // the score pass below writes the query's bytes (s_u)
     // Limbs 3 and 4 zero in every lane of the wave: three-limb dot products.
     // (With four workgroups per head, at batch 1 and 2, the branch measured
     // 1% slower, so those launches keep five.)
@@ -451,8 +522,12 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
             // the token's sum of its 8 half-groups (lanes 8r .. 8r+7), exact
             const uint32_t ksh = shift_of(__uint_as_float(scl[ps].x));
             const int64_t p = octet_sum64(q3 ? half_dot<3>(ql, kw, ksh) : half_dot<5>(ql, kw, ksh));
-            // slots past n are read by the Y pass with a zero coefficient
-            if ((c & 1) == 0) s_vs[c >> 1][i] = i < n ? static_cast<uint8_t>(shift_of(__uint_as_float(scl[ps].y))) : 0;
+            // the V scale of group c / 2, its exponent alone (the stored
+            // scales are powers of two); slots past n take the scale of shift
+            // 0 and are read by the Y pass with a zero coefficient
+            if ((c & 1) == 0 && (SLICES == 1 || (c >> 1) == slice))
+                s_u.p[SLICES == 1 ? c >> 1 : 0][i] =
+                    __uint_as_float(i < n ? scl[ps].y & 0x7f800000u : 110u << 23);
             if (c == 0 && i < n) s_tok[i] = static_cast<uint32_t>(score_of(p));
         }
         __builtin_amdgcn_s_waitcnt(0);   // the V codes are in LDS before the barrier
@@ -463,11 +538,14 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
         // Coefficient words, one token per thread: the exclusive prefix
         // maximum (wave scan, then the maxima of the waves before) gives each
         // token's running maximum.  The same pass lays out what Y and Z read:
-        // the coefficients alone, the per-wave inclusive sums of the
-        // coefficients of ordinary tokens (first and rescaling tokens count
-        // zero) with the wave totals, and per-wave ballots of the first and
-        // rescaling tokens.
+        // the coefficient words, the products p of the coefficient and each
+        // group's V scale (the scale alone for first and rescaling tokens),
+        // the per-wave sums of the coefficients of ordinary tokens, and the
+        // per-wave ballots.
         const int32_t sv = d < n ? static_cast<int32_t>(s_tok[d]) : INT32_MIN;
+        float sc[kGroups];   // the token's V scales, read with its score
+#pragma unroll
+        for (int gl = 0; gl < kGroups; ++gl) sc[gl] = s_u.p[gl][d];
         const int32_t incl = wave_scan_max(sv);
         if (lane == 63) s_wave_max[wave] = incl;
         int32_t excl = dpp_shifted<kDppWaveShr1, 0xF>(INT32_MIN, incl);
@@ -479,11 +557,22 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
         const bool special = (word & (kInit | kRescale)) != 0u;
         const uint32_t psum = wave_scan_add(special ? 0u : (word & kCoefMask));
         const uint64_t special_mask = __ballot(special);
-        s_word[d] = word;
-        s_tok[d] = word & kCoefMask;
-        s_psum[d] = psum;
+        const float cf = static_cast<float>(word & kCoefMask);
+        bool wide16 = false, wide17 = false;   // a V shift of 16 (scale 2^-1) or more, of 17 (2^0) or more
+#pragma unroll
+        for (int gl = 0; gl < kGroups; ++gl) {
+            wide16 |= sc[gl] >= 0.5f;
+            wide17 |= sc[gl] >= 1.0f;
+            s_u.p[gl][d] = special ? sc[gl] : cf * sc[gl];   // exact: an integer below 2^18 times a power of two
+        }
+        const uint64_t slow_mask = __ballot(special || wide16), wide17_mask = __ballot(wide17);
+        s_tok[d] = word;
         if (lane == 63) s_wave_sum[wave] = psum;
-        if (lane == 0) s_special[wave] = special_mask;
+        if (lane == 0) {
+            s_special[wave] = special_mask;
+            s_slow[wave] = slow_mask;
+            s_wide17[wave] = wide17_mask;
+        }
 #pragma unroll
         for (int w = 0; w < kChunk / 64; ++w) run_max = max(run_max, s_wave_max[w]);
         __syncthreads();
@@ -493,7 +582,9 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
         // into kCompParts runs of q tokens and compose each run into one map
         // Y -> clamp(Y + A, L, H) (every ordinary token is Y -> sat32(Y + t),
         // and such maps compose: A adds t, L and H take sat32(. + t)), which
-        // the ordered threads apply in order after the barrier.  split is
+        // the ordered threads apply in order after the barrier.  A batch or
+        // run with a first or rescaling token, or a shift of 16 or more,
+        // takes the slow form (the ballots say which).  split is
         // about kSeqShare16/16 of n, past the chunk's last first or rescaling
         // token, and a multiple of kBatch, and so is q.  Slots past n have a
         // zero coefficient, so a zero term.
@@ -513,26 +604,62 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
         const int q = rest > 0 ? ((rest + kCompParts - 1) / kCompParts + kBatch - 1) & ~(kBatch - 1) : 0;
         const int cp = d < kSeqLanes ? 0 : (d - kSeqLanes) / kCh;   // composed part of a composing thread
         const int cl = d < kSeqLanes ? d % kCh : (d - kSeqLanes) % kCh;
-        const int ch = slice * kCh + cl, g = ch >> 5;
+        const int ch = slice * kCh + cl;
+        const float* s_p_g = s_u.p[cl >> 5];   // this channel's group
         if (d < kCh) {
-            // A batch with no first or rescaling token (the ballots say which)
-            // only adds its terms.
+            // With four workgroups per head a CU holds one of them, so the
+            // ordered part's LDS latency is exposed: the next batch's reads go
+            // out while this one's terms are formed.
+            FastBatch next;
+            if constexpr (kPrefetchY)
+                if (split > 0) next = load_fast(s_p_g, s_vc, 0, ch);
             for (int span = 0; span < split; span += 64) {
                 const uint64_t spans = uniform64(s_special[span >> 6]);
+                const uint64_t slows = uniform64(s_slow[span >> 6]);
+                const uint64_t wides = uniform64(s_wide17[span >> 6]);
                 const int end = min(span + 64, split);
                 for (int i0 = span; i0 < end; i0 += kBatch) {
-                    int32_t code[kBatch], term[kBatch];
-                    uint32_t sh[kBatch];
-                    batch_terms(s_tok, s_vs[g], s_vc, i0, ch, code, sh, term);
-                    if (((spans >> (i0 - span)) & ((1ull << kBatch) - 1u)) == 0u) {
+                    const int at = i0 - span;
+                    FastBatch cur;
+                    if constexpr (kPrefetchY) {
+                        cur = next;
+                        if (i0 + kBatch < split) next = load_fast(s_p_g, s_vc, i0 + kBatch, ch);
+                    }
+                    if (((slows >> at) & kBatchMask) == 0u) {
+                        // No first or rescaling token and every shift at most
+                        // 15: fused-multiply-add terms.  Where no Y of the
+                        // wave lies within kBatch 2^22 of either end of the
+                        // int32 range no partial sum saturates, and the batch
+                        // adds its terms at once (modulo 2^32, then exact).
+                        if constexpr (!kPrefetchY) cur = load_fast(s_p_g, s_vc, i0, ch);
+                        uint32_t tb[kBatch];
+                        fast_term_bits(cur, tb);
+                        const bool safe = static_cast<uint32_t>(y) + (0x80000000u - kSatMargin) <= ~(2u * kSatMargin);
+                        if (__builtin_amdgcn_ballot_w64(!safe) == 0u) {
+                            uint32_t acc = static_cast<uint32_t>(y) - kBatch * kRoundMagicBits;
 #pragma unroll
-                        for (int j = 0; j < kBatch; ++j) y = __builtin_elementwise_add_sat(y, term[j]);
+                            for (int j = 0; j < kBatch; ++j) acc += tb[j];
+                            y = static_cast<int32_t>(acc);
+                        } else {
+#pragma unroll
+                            for (int j = 0; j < kBatch; ++j)
+                                y = __builtin_elementwise_add_sat(y, static_cast<int32_t>(tb[j] - kRoundMagicBits));
+                        }
                     } else {
+                        int32_t code[kBatch], term[kBatch];
+                        float pv[kBatch];
+                        slow_terms(s_tok, s_p_g, s_vc, i0, ch, ((wides >> at) & kBatchMask) != 0u, code, pv, term);
+                        if (((spans >> at) & kBatchMask) == 0u) {
 #pragma unroll
-                        for (int j = 0; j < kBatch; ++j) {
-                            const uint32_t w = static_cast<uint32_t>(
-                                __builtin_amdgcn_readfirstlane(static_cast<int>(s_word[i0 + j])));
-                            y = value_step(y, w, code[j], sh[j], term[j]);
+                            for (int j = 0; j < kBatch; ++j) y = __builtin_elementwise_add_sat(y, term[j]);
+                        } else {
+                            // A first or rescaling token's p is its V scale.
+#pragma unroll
+                            for (int j = 0; j < kBatch; ++j) {
+                                const uint32_t w = static_cast<uint32_t>(
+                                    __builtin_amdgcn_readfirstlane(static_cast<int>(s_tok[i0 + j])));
+                                y = value_step(y, w, code[j], shift_of(pv[j]), term[j]);
+                            }
                         }
                     }
                 }
@@ -541,51 +668,115 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
             if (wave == 3) {
                 // Z: ordinary tokens add their coefficients modulo 2^30, so
                 // between two first or rescaling tokens Z advances by a
-                // difference of prefix sums, and only those tokens step in order.
-                uint32_t done = 0u, offset = 0u;   // prefix sum already added; sum of the waves before
+                // difference of prefix sums, and only those tokens step in
+                // order.  The prefix sums of a 64-token span that holds such
+                // a token come from a wave scan of its coefficient words.
+                uint32_t done = 0u, offset = 0u;   // prefix sum already added; sum of the spans before
 #pragma unroll
                 for (int w = 0; w < kChunk / 64; ++w) {
                     uint64_t m = uniform64(s_special[w]);
-                    while (m != 0u) {
-                        const int i = w * 64 + __builtin_ctzll(m);
-                        const uint32_t upto = offset + s_psum[i];   // sum of the ordinary tokens before i
-                        z = (z + (upto - done)) & kMask30;
-                        done = upto;
-                        z = z_step(z, static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(s_word[i]))));
-                        m &= m - 1u;
+                    if (m != 0u) {
+                        const uint32_t wd = s_tok[64 * w + lane];
+                        const uint32_t incl = wave_scan_add((wd & (kInit | kRescale)) != 0u ? 0u : (wd & kCoefMask));
+                        while (m != 0u) {
+                            const int i = __builtin_ctzll(m);
+                            // the sum of the ordinary tokens before i (i itself counts zero)
+                            const uint32_t upto =
+                                offset + static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl), i));
+                            z = (z + (upto - done)) & kMask30;
+                            done = upto;
+                            z = z_step(z, static_cast<uint32_t>(
+                                              __builtin_amdgcn_readfirstlane(static_cast<int>(s_tok[64 * w + i]))));
+                            m &= m - 1u;
+                        }
                     }
                     offset += s_wave_sum[w];
                 }
                 z = (z + (offset - done)) & kMask30;
             }
+            // A composing thread's run [begin, end) holds no first or
+            // rescaling token.  With kCh = 32 a wave holds two parts, so what
+            // depends on the run is read per lane.
             const int begin = split + cp * q, end = min(n, begin + q);
             if (begin < n) {
-                int64_t sum = 0;
-                int32_t sum_short = 0;   // the short-form batches' terms (see kMaxRun)
-                int32_t lo = INT32_MIN, hi = INT32_MAX;
-                for (int i0 = begin; i0 < end; i0 += kBatch) {
-                    int32_t code[kBatch], term[kBatch];
-                    uint32_t sh[kBatch];
-                    if (batch_terms(s_tok, s_vs[g], s_vc, i0, ch, code, sh, term)) {
+                // Slow-form tokens in [split, n) (wave-uniform), then, with
+                // two parts per wave, in this lane's run.
+                bool slow_run = false;
 #pragma unroll
-                        for (int j = 0; j < kBatch; ++j) {
-                            sum_short += term[j];
-                            lo = __builtin_elementwise_add_sat(lo, term[j]);
-                            hi = __builtin_elementwise_add_sat(hi, term[j]);
-                        }
-                    } else {
+                for (int w = 0; w < kChunk / 64; ++w) {
+                    const int lo_t = max(split - 64 * w, 0), hi_t = min(n - 64 * w, 64);
+                    if (lo_t < hi_t)
+                        slow_run |= (uniform64(s_slow[w]) & (~0ull >> (64 - (hi_t - lo_t))) << lo_t) != 0u;
+                }
+                if (kCompParts > 1 && slow_run) {
+                    slow_run = false;
 #pragma unroll
-                        for (int j = 0; j < kBatch; ++j) {
-                            sum += term[j];
-                            lo = __builtin_elementwise_add_sat(lo, term[j]);
-                            hi = __builtin_elementwise_add_sat(hi, term[j]);
-                        }
+                    for (int w = 0; w < kChunk / 64; ++w) {
+                        const int lo_t = max(begin - 64 * w, 0), hi_t = min(end - 64 * w, 64);
+                        if (lo_t < hi_t)
+                            slow_run |= (s_slow[w] & (~0ull >> (64 - (hi_t - lo_t))) << lo_t) != 0u;
                     }
                 }
-                sum += sum_short;
-                s_map_sum[cp * kCh + cl] = sum;
-                s_map_lo[cp * kCh + cl] = lo;
-                s_map_hi[cp * kCh + cl] = hi;
+                if (!slow_run) {
+                    // Fused-multiply-add terms.  With prefix sums P_k (P_0 =
+                    // 0) the map is A = P_n, L = INT32_MIN + P_n - min P_k,
+                    // H = INT32_MAX + P_n - max P_k: the sat32 recursion of L
+                    // and H in closed form, exact while neither reaches the
+                    // far end of the int32 range (|P_k| < 2^30, see kMaxRun).
+                    int32_t pk = 0, pmin = 0, pmax = 0;
+                    FastBatch next;
+                    if constexpr (kPrefetchY) next = load_fast(s_p_g, s_vc, begin, ch);
+                    for (int i0 = begin; i0 < end; i0 += kBatch) {
+                        FastBatch cur;
+                        if constexpr (kPrefetchY) {
+                            cur = next;
+                            if (i0 + kBatch < end) next = load_fast(s_p_g, s_vc, i0 + kBatch, ch);
+                        } else {
+                            cur = load_fast(s_p_g, s_vc, i0, ch);
+                        }
+                        uint32_t tb[kBatch];
+                        fast_term_bits(cur, tb);
+#pragma unroll
+                        for (int j = 0; j < kBatch; j += 2) {
+                            const int32_t p1 = pk + static_cast<int32_t>(tb[j] - kRoundMagicBits);
+                            const int32_t p2 = p1 + static_cast<int32_t>(tb[j + 1] - kRoundMagicBits);
+                            pmin = min(pmin, min(p1, p2));
+                            pmax = max(pmax, max(p1, p2));
+                            pk = p2;
+                        }
+                    }
+                    s_map_sum[cp * kCh + cl] = pk;
+                    s_map_lo[cp * kCh + cl] = INT32_MIN + (pk - pmin);
+                    s_map_hi[cp * kCh + cl] = INT32_MAX + (pk - pmax);
+                } else {
+                    int64_t sum = 0;
+                    int32_t sum_short = 0;   // the short-form batches' terms (see kMaxRun)
+                    int32_t lo = INT32_MIN, hi = INT32_MAX;
+                    for (int i0 = begin; i0 < end; i0 += kBatch) {
+                        int32_t code[kBatch], term[kBatch];
+                        float pv[kBatch];
+                        const bool wide = ((s_wide17[i0 >> 6] >> (i0 & 63)) & kBatchMask) != 0u;
+                        if (slow_terms(s_tok, s_p_g, s_vc, i0, ch, wide, code, pv, term)) {
+#pragma unroll
+                            for (int j = 0; j < kBatch; ++j) {
+                                sum_short += term[j];
+                                lo = __builtin_elementwise_add_sat(lo, term[j]);
+                                hi = __builtin_elementwise_add_sat(hi, term[j]);
+                            }
+                        } else {
+#pragma unroll
+                            for (int j = 0; j < kBatch; ++j) {
+                                sum += term[j];
+                                lo = __builtin_elementwise_add_sat(lo, term[j]);
+                                hi = __builtin_elementwise_add_sat(hi, term[j]);
+                            }
+                        }
+                    }
+                    sum += sum_short;
+                    s_map_sum[cp * kCh + cl] = sum;
+                    s_map_lo[cp * kCh + cl] = lo;
+                    s_map_hi[cp * kCh + cl] = hi;
+                }
             }
         }
         __syncthreads();
@@ -610,7 +801,6 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
     // exponent e, q = trunc(clamp(raw*2^-17 * 2^(13-e) +- 0.5, +-8191)),
     // code = e + 127.  Threads d < kCh own channel slice * kCh + d; a group
     // is 32 lanes of one wave.
-    constexpr int kGroups = kCh / 32;   // G32 groups of this workgroup
     const size_t grp0 = static_cast<size_t>(b) * (kHeads * kGroupsPerHead) + h * kGroupsPerHead + slice * kGroups;
     if (d < kCh) {
         const int32_t o = mulq17_wrap(y, s_inv);

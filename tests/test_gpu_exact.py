@@ -177,6 +177,63 @@ def test_exact_every_token_a_new_maximum(skv, ctx, lut4096, rope_tables, batch):
     kv.close()
 
 
+def saturating_history(n, mag, lead, flip):
+    """Keys zero, so every score is 0 and every coefficient exp(0) = 1.0 (no
+    token after the first is a new maximum), and V = +-mag on alternate
+    channels: -sign before token `lead`, +sign up to `flip`, -sign after, so
+    Y (Q15.17, 2^31 = 16384.0) climbs from -lead mag to either end of the
+    int32 range, stays there, and comes back.  mag 31.0 quantizes to shift 15
+    and mag 40.0 to shift 16."""
+    t = np.arange(n)
+    run = np.where((t >= lead) & (t < flip), 1.0, -1.0)
+    sign = np.where(np.arange(4096) % 2 == 0, 1.0, -1.0)
+    return np.zeros((n, 4096), np.float32), (mag * run[:, None] * sign[None, :]).astype(np.float32)
+
+
+def saturation_cases(mag, batch):
+    """(position, lead, flip) per sequence: Y first saturates after 16384 / mag
+    tokens (lead 0), or at token 968, 200 tokens into its 256-token chunk (the
+    composed part there), with lead = (968 - 16384 / mag) / 2."""
+    late = int(round((968 - 16384 / mag) / 2))
+    return [(1300, 0, 1000), (1250, late, 1100), (1100, 0, 900)][:batch]
+
+
+@pytest.mark.parametrize("mag,batch", [(31.0, 1), (31.0, 3), (40.0, 1), (40.0, 3)])
+def test_exact_y_saturates(skv, ctx, lut4096, rope_tables, mag, batch):
+    """Y reaches INT32_MAX and INT32_MIN (alternate channels) early in a chunk
+    (its ordered part) or late in one (its composed part), stays, and comes
+    back: the saturating adds, the batch sums taken at once away from the
+    ends of the range, and the composed clamp-add maps, against the oracle's
+    integer recurrence bit for bit.  Shift 15 takes the fused-multiply-add
+    term form, shift 16 the rint form."""
+    _note(f"case: exact, saturating Y, |V| = {mag}, batch {batch}")
+    cos, sin = rope_tables
+    cases = saturation_cases(mag, batch)
+    positions = [c[0] for c in cases]
+    kv = skv.KVCache(ctx, layers=1, max_batch=batch, max_seq_len=max(positions) + 1)
+    scs = []
+    for b, (p, lead, flip) in enumerate(cases):
+        kh, vh = saturating_history(p, mag, lead, flip)
+        prefill(skv, ctx, kv, lut4096, 0, b, kh, vh)
+        scs.append(oracle_sequence(cos, sin, kh, vh, p + 1))
+        assert (scs[-1].vs[:, :p] == (15 if mag < 32 else 16)).all()
+    q = f32_normal(9100, (batch, 4096))
+    k = np.zeros((batch, 4096), np.float32)
+    v = (-mag * np.where(np.arange(4096) % 2 == 0, 1.0, -1.0)).astype(np.float32)[None].repeat(batch, 0)
+    qq, kq, vq = O.f2q17(q), O.f2q17(k), O.f2q17(v)
+    out, aq, asc = exact_step(skv, ctx, kv, lut4096, 0, positions, qq, kq, vq, q17=True)
+    for b, p in enumerate(positions):
+        res = scs[b].step_q17(qq[b], kq[b], vq[b], p, cos[p], sin[p], fp=True, integer=True)
+        ref = res["int"].reshape(4096)
+        # saturation changed the result: the unsaturated mean is far away
+        assert np.abs(ref * 2.0 ** -17 - res["fp"].reshape(4096)).min() > 1.0
+        diff = np.flatnonzero(out[b] != ref)
+        assert diff.size == 0, f"seq {b} position {p}: {diff.size} Q15.17 values differ (first {diff[:4]})"
+        q14, e8 = O.a14_q17(ref.reshape(128, 32))
+        assert (asc[b] == e8).all() and (aq[b] == O.pack_a14(q14)).all(), f"seq {b}: A14"
+    kv.close()
+
+
 def test_exact_batch_over_one_launch(skv, ctx, lut4096, rope_tables):
     """The exact entry over 260 sequences (two launches), against the oracle's
     integer recurrence on a sample of sequences from both launches."""
