@@ -514,7 +514,11 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
     for (int t0 = 0; t0 < len; t0 += kChunk) {
         const int n = min(kChunk, len - t0);
         issue(t0, !kPrefetch, true);
-        // Scores of tokens [t0, t0+n).
+        // Scores of tokens [t0, t0+n).  Every lane of an octet ends a pass
+        // with its token's sum; lane c keeps pass c's, so each lane scales,
+        // rounds and saturates one sum per chunk.
+        static_assert(kPasses == 8, "one pass per lane of an octet");
+        int64_t own = 0;
 #pragma unroll
         for (int ps = 0; ps < kPasses; ++ps) {
             const int i = wave * 8 + r + 32 * ps;
@@ -522,13 +526,17 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
             // the token's sum of its 8 half-groups (lanes 8r .. 8r+7), exact
             const uint32_t ksh = shift_of(__uint_as_float(scl[ps].x));
             const int64_t p = octet_sum64(q3 ? half_dot<3>(ql, kw, ksh) : half_dot<5>(ql, kw, ksh));
+            if (c == ps) own = p;
             // the V scale of group c / 2, its exponent alone (the stored
             // scales are powers of two); slots past n take the scale of shift
             // 0 and are read by the Y pass with a zero coefficient
             if ((c & 1) == 0 && (SLICES == 1 || (c >> 1) == slice))
                 s_u.p[SLICES == 1 ? c >> 1 : 0][i] =
                     __uint_as_float(i < n ? scl[ps].y & 0x7f800000u : 110u << 23);
-            if (c == 0 && i < n) s_tok[i] = static_cast<uint32_t>(score_of(p));
+        }
+        {
+            const int i = wave * 8 + r + 32 * c;   // the token of pass c
+            if (i < n) s_tok[i] = static_cast<uint32_t>(score_of(own));
         }
         __builtin_amdgcn_s_waitcnt(0);   // the V codes are in LDS before the barrier
         if constexpr (kPrefetch)
