@@ -390,11 +390,11 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
     constexpr int kCompParts = (256 - kSeqLanes) / kCh;
     constexpr int kGroups = kCh / 32;   // G32 groups of this workgroup's channels
     constexpr bool kPrefetchY = SLICES == 4;   // the Y pass reads a batch ahead (registers allow it)
-    // The ordered part's share of a chunk: with the fused-multiply-add terms a
-    // composed token costs about 4 operations against 3, so about 9/16 with
-    // one composed part; with six, 2/16 (the composed runs round up to whole
+    // The ordered part's share of a chunk, measured: 8/16 with one composed
+    // part (9/16 and 10/16 ran up to 3% slower at batch 16), 2/16 with six
+    // (3/16 ran 7% slower at batch 1; the composed runs round up to whole
     // batches).
-    constexpr int kSeqShare16 = kCompParts == 1 ? 9 : 2;
+    constexpr int kSeqShare16 = kCompParts == 1 ? 8 : 2;
     // The longest composed run (the rest of a chunk after the ordered share,
     // split into kCompParts runs of whole batches): its short-form terms, and
     // its prefix sums of fused-multiply-add terms, stay within int32.
