@@ -29,6 +29,8 @@
 //     32-bit integer operations above; wave 3 also advances Z by prefix-sum
 //     differences and steps only at first and rescaling tokens;
 // then Y * 1/Z and the integer-path A14/E8M0 epilogue.
+#include <type_traits>
+
 #include "swiftkv_device.hpp"
 
 namespace swiftkv {
