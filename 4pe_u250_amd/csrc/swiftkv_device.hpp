@@ -145,11 +145,14 @@ __device__ __forceinline__ int2 load_pair(const void* base, size_t elem) {
 // conversion that follows saturates a NaN by its sign bit, so a NaN sum takes
 // a defined sign: that of a NaN operand (the first, if both are NaN), or, for
 // inf - inf, the negative default NaN that x86 SSE arithmetic (the platform of
-// the reference's C model) produces.
+// the reference's C model) produces.  Selects, not branches: a branch here
+// splits the step's prologue into blocks at whose join the compiler waits for
+// every load in flight, the first cache block included.
 __device__ __forceinline__ float add_partials(float a, float b) {
     const float s = __fadd_rn(a, b);
-    if (!__builtin_isnan(s)) return s;
-    return __builtin_isnan(a) ? a : (__builtin_isnan(b) ? b : __uint_as_float(0xffc00000u));
+    const uint32_t ua = __float_as_uint(a), ub = __float_as_uint(b), us = __float_as_uint(s);
+    const uint32_t nan_sum = (ua << 1) > 0xff000000u ? ua : ((ub << 1) > 0xff000000u ? ub : 0xffc00000u);
+    return __uint_as_float((us << 1) > 0xff000000u ? nan_sum : us);
 }
 
 template <int NP>

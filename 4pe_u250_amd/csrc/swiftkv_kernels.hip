@@ -664,6 +664,11 @@ __global__ __launch_bounds__(WAVES * 64) void step_kernel(StepArgs a) {
     // Several splits: count this split's arrival, publish its partial as
     // tagged words without waiting for them to land, and let the split that
     // arrives last merge the head's partials and finish the head.
+    // Both halves of the word stay in their registers until here: with the
+    // low half dead early, the compiler reused its register in the prologue,
+    // and a write to a register that a load is still filling waits for every
+    // load in flight, the first cache block included.
+    asm volatile("" ::"v"(arrival_word));
     const uint32_t tag = static_cast<uint32_t>(arrival_word >> 32) + 1u;
     uint64_t* slots = a.partials + head_row * static_cast<size_t>(a.slot_stride) * kSlotWords;
     // The count goes out from thread 128, in a wave that publishes nothing,

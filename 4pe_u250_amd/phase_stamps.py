@@ -1,6 +1,7 @@
 """Phase breakdown of the decode-attention step kernel on the GPU.
 
     python 4pe_u250_amd/phase_stamps.py [--batches 1,2,4] [--position 4095] [--layers 32] [--reps 10]
+                                        [--parts 4]
 
 Runs 32-layer decode steps through the instrumented build libswiftkv_stamps.so
 (built by build.py: the product sources with SWIFTKV_PHASE_STAMPS, whose step
@@ -20,6 +21,8 @@ from the first workgroup's start, medians over the repetitions:
   - launch:      the event-timed time per layer minus the span from the first
                  workgroup's start to the last one's end (dispatch, completion
                  and the gap to the next launch).
+With --parts N (2 or 4) the steps go through swiftkv_attention_partials, fed
+N split-K FP32 partials of q, k and v.
 Diagnostics only: nothing here is the product path, and the product library
 compiles every stamp away.
 """
@@ -77,6 +80,7 @@ def main():
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--reps", type=int, default=10)
     ap.add_argument("--json", default=None, help="also write the medians here")
+    ap.add_argument("--parts", type=int, default=0, help="feed N split-K FP32 partials (swiftkv_attention_partials)")
     args = ap.parse_args()
     if not os.path.exists(STAMPS_LIB):
         raise SystemExit(f"{STAMPS_LIB} is missing: python 4pe_u250_amd/build.py")
@@ -91,18 +95,23 @@ def main():
         lut = skv.RopeLut.generate(ctx, max(pos + 1, 4096))
         kv = skv.KVCache(ctx, layers=layers, max_batch=batch, max_seq_len=pos + 1)
         kv.fill_synthetic(lut, ntok=pos, seed=5)
-        n = layers * batch * 4096
+        parts = args.parts
+        per_layer = batch * 4096 * max(parts, 1)          # elements of one layer's q (all its parts)
+        n = layers * per_layer
         qkv = [ctx.alloc(n * 4) for _ in range(3)]
         for i, b in enumerate(qkv):
             ctx.fill_synthetic(b, n, 9, 100 + i)
         o, aq, asc = ctx.alloc(batch * 4096 * 4), ctx.alloc(batch * 128 * 56), ctx.alloc(batch * 128)
         positions = np.full(batch, pos, np.int32)
-        stride = batch * 4096 * 4
+        stride = per_layer * 4
 
         def step():
             for layer in range(layers):
-                skv.swiftkv_attention(ctx, qkv[0].ptr + layer * stride, qkv[1].ptr + layer * stride,
-                                      qkv[2].ptr + layer * stride, kv, lut, aq, asc, layer, positions, o)
+                q, k, v = (buf.ptr + layer * stride for buf in qkv)
+                if parts:
+                    skv.swiftkv_attention_partials(ctx, q, k, v, parts, kv, lut, aq, asc, layer, positions, o)
+                else:
+                    skv.swiftkv_attention(ctx, q, k, v, kv, lut, aq, asc, layer, positions, o)
 
         for _ in range(3):
             step()
@@ -129,8 +138,9 @@ def main():
             d["workgroups"] = nwg
             rows.append(d)
         med = {k: round(float(np.median([r[k] for r in rows])), 3) for k in rows[0]}
-        out[f"batch{batch}_position{pos}"] = med
-        print(f"batch {batch}, position {pos}, {layers} layers: " + json.dumps(med), flush=True)
+        tag = f", {parts} partials" if parts else ""
+        out[f"batch{batch}_position{pos}" + (f"_parts{parts}" if parts else "")] = med
+        print(f"batch {batch}, position {pos}, {layers} layers{tag}: " + json.dumps(med), flush=True)
         for b in qkv + [o, aq, asc]:
             b.free()
         kv.close()
