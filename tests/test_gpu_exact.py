@@ -234,6 +234,48 @@ def test_exact_y_saturates(skv, ctx, lut4096, rope_tables, mag, batch):
     kv.close()
 
 
+@pytest.mark.parametrize("seed,batch", [(99001, 1), (99004, 3)])
+def test_exact_y_saturates_mixed_shifts(skv, ctx, lut4096, rope_tables, seed, batch):
+    """Y saturates while the V shifts change from token to token (magnitudes
+    15 to 130 per token and 1024-channel block: shifts 14 to 18), so batches
+    and composed runs switch between the fused-multiply-add, rint and integer
+    term forms around the saturation points; keys zero except a few tokens
+    that set new maxima.  Bit for bit against the oracle's recurrence."""
+    _note(f"case: exact, saturating Y with mixed shifts, seed {seed}, batch {batch}")
+    cos, sin = rope_tables
+    rng = np.random.default_rng(seed)
+    positions = [int(p) for p in rng.integers(500, 1400, batch)]
+    kv = skv.KVCache(ctx, layers=1, max_batch=batch, max_seq_len=max(positions) + 1)
+    scs = []
+    chan_sign = np.where(np.arange(4096) % 2 == 0, 1.0, -1.0)
+    for b, p in enumerate(positions):
+        k = np.zeros((p, 4096), np.float32)
+        k[rng.integers(0, p, 6), :] = f32_normal(seed + 10 * b, (6, 4096)) * np.float32(0.05)
+        mags = np.repeat(rng.choice([15.0, 31.0, 40.0, 60.0, 100.0, 130.0], size=(p, 4)), 1024, axis=1)
+        sign_t = np.where((np.arange(p) // int(rng.integers(200, 700))) % 2 == 0, 1.0, -1.0)
+        v = (mags * sign_t[:, None] * chan_sign[None, :]).astype(np.float32)
+        prefill(skv, ctx, kv, lut4096, 0, b, k, v)
+        scs.append(oracle_sequence(cos, sin, k, v, p + 1))
+        shifts = set(np.unique(scs[-1].vs[:, :p]).tolist())
+        assert {15, 16, 17}.issubset(shifts), shifts
+    q = f32_normal(seed + 1000, (batch, 4096))
+    k = np.zeros((batch, 4096), np.float32)
+    v = (31.0 * chan_sign).astype(np.float32)[None].repeat(batch, 0)
+    qq, kq, vq = O.f2q17(q), O.f2q17(k), O.f2q17(v)
+    out, aq, asc = exact_step(skv, ctx, kv, lut4096, 0, positions, qq, kq, vq, q17=True)
+    saturated = 0
+    for b, p in enumerate(positions):
+        res = scs[b].step_q17(qq[b], kq[b], vq[b], p, cos[p], sin[p], fp=True, integer=True)
+        ref = res["int"].reshape(4096)
+        saturated += int(np.abs(ref * 2.0 ** -17 - res["fp"].reshape(4096)).max() > 1.0)
+        diff = np.flatnonzero(out[b] != ref)
+        assert diff.size == 0, f"seq {b} position {p}: {diff.size} Q15.17 values differ (first {diff[:4]})"
+        q14, e8 = O.a14_q17(ref.reshape(128, 32))
+        assert (asc[b] == e8).all() and (aq[b] == O.pack_a14(q14)).all(), f"seq {b}: A14"
+    assert saturated > 0
+    kv.close()
+
+
 def test_exact_batch_over_one_launch(skv, ctx, lut4096, rope_tables):
     """The exact entry over 260 sequences (two launches), against the oracle's
     integer recurrence on a sample of sequences from both launches."""
