@@ -6,8 +6,8 @@
 // comparison with the FPGA / C model; the sequential chains bound it, not HBM.
 //
 // Grid (32 heads x SLICES, batch rows), 256 threads per (sequence, head,
-// slice of 128 / SLICES channels); SLICES is 4 for the smallest batches and
-// 1 otherwise.  Wave 0 first appends the new row like the fast step; then
+// slice of 128 / SLICES channels); SLICES is 4 for the smallest batches, 2
+// up to batch 8 and 1 otherwise.  Wave 0 first appends the new row like the fast step; then
 // tokens [0, position] are processed in chunks of kChunk:
 //   - the 4 waves issue all of the chunk's loads at once through one buffer
 //     resource (K codes and scales into registers, V codes straight into
@@ -48,6 +48,11 @@ constexpr int kPasses = kChunk / 32;          // score passes per chunk: 4 waves
 // us, was even at batch 4 and slower from batch 8 on, where one workgroup per
 // head already fills the machine and the 4x score work shows.
 constexpr int kExactSlicedMaxBatch = 2;
+// Largest batch whose launch splits each head's Y over 2 workgroups (64
+// channels each): batch 3 and 4 ran 16-21% faster than with one workgroup
+// per head (whose 128 workgroups leave half the CUs idle), batch 6 and 8 up
+// to 6%; from batch 12 on the doubled score work made it slower.
+constexpr int kExactHalfSlicedMaxBatch = 8;
 constexpr int64_t kScoreScaleQ17 = 11585;     // RNE(2^17 / sqrt(128)) (swiftkv_attention.cpp:1101-1102)
 constexpr int64_t kLog2eQ21 = 3025551;        // RNE(log2(e) * 2^21) (cpp:207-208)
 
@@ -383,7 +388,7 @@ struct ExactArgs {
 // write the same bytes.
 template <bool Q17, int SLICES>
 __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
-    static_assert(SLICES == 1 || SLICES == 4, "128 or 32 channels per workgroup");
+    static_assert(SLICES == 1 || SLICES == 2 || SLICES == 4, "128, 64 or 32 channels per workgroup");
     // Y roles: threads [0, kCh) run the ordered part (one channel each),
     // threads [kSeqLanes, 256) compose kCompParts parts of kCh channels,
     // threads in between (wave 0's upper half when kCh = 32) idle.
@@ -396,7 +401,7 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
     // part (9/16 and 10/16 ran up to 3% slower at batch 16), 2/16 with six
     // (3/16 ran 7% slower at batch 1; the composed runs round up to whole
     // batches).
-    constexpr int kSeqShare16 = kCompParts == 1 ? 8 : 2;
+    constexpr int kSeqShare16 = kCompParts == 1 ? 8 : kCompParts == 3 ? 4 : 2;
     // The longest composed run (the rest of a chunk after the ordered share,
     // split into kCompParts runs of whole batches): its short-form terms, and
     // its prefix sums of fused-multiply-add terms, stay within int32.
@@ -511,7 +516,7 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
     // chunk's coefficient and Y passes run; its V codes, which go to LDS,
     // follow at the top of its own iteration (the barrier after the scores
     // waits for every write into LDS, so they cannot be outstanding there).
-    constexpr bool kPrefetch = SLICES == 4;
+    constexpr bool kPrefetch = SLICES > 1;
     if constexpr (kPrefetch) issue(0, true, false);
     for (int t0 = 0; t0 < len; t0 += kChunk) {
         const int n = min(kChunk, len - t0);
@@ -532,8 +537,8 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs ea) {
             // the V scale of group c / 2, its exponent alone (the stored
             // scales are powers of two); slots past n take the scale of shift
             // 0 and are read by the Y pass with a zero coefficient
-            if ((c & 1) == 0 && (SLICES == 1 || (c >> 1) == slice))
-                s_u.p[SLICES == 1 ? c >> 1 : 0][i] =
+            if ((c & 1) == 0 && (c >> 1) / kGroups == slice)
+                s_u.p[(c >> 1) % kGroups][i] =
                     __uint_as_float(i < n ? scl[ps].y & 0x7f800000u : 110u << 23);
         }
         {
@@ -857,6 +862,10 @@ hipError_t launch_exact(const StepArgs& a, const uint32_t* exp_lut, bool q17, hi
         const dim3 grid(kHeads * 4, a.batch);
         if (q17) exact_kernel<true, 4><<<grid, 256, 0, s>>>(ea);
         else exact_kernel<false, 4><<<grid, 256, 0, s>>>(ea);
+    } else if (a.batch <= kExactHalfSlicedMaxBatch) {
+        const dim3 grid(kHeads * 2, a.batch);
+        if (q17) exact_kernel<true, 2><<<grid, 256, 0, s>>>(ea);
+        else exact_kernel<false, 2><<<grid, 256, 0, s>>>(ea);
     } else {
         const dim3 grid(kHeads, a.batch);
         if (q17) exact_kernel<true, 1><<<grid, 256, 0, s>>>(ea);
