@@ -215,3 +215,15 @@ def test_bench_reads_committed_profiles():
         assert 0.0 < got["achieved_occupancy_frac"] <= 1.0
         assert got["trace_avg_us"] > 0 and got["bench_ms_per_step"] > 0
     assert bench.profile_summary(3, 4096) == ({}, None)
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py runs on one GPU: --gpus above 1 exits with a message before any device work."""
+    import json
+    import os
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in json.loads(r.stdout.strip().splitlines()[-1])["error"]
