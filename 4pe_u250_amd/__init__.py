@@ -67,6 +67,7 @@ _SIGNATURES = {
     "swiftkv_synchronize": (C.c_int, [_vp]),
     "swiftkv_set_split_tokens": (C.c_int, [_vp, _i32]),
     "swiftkv_debug_set_split_generation": (C.c_int, [_vp, C.c_uint32, _i32]),
+    "swiftkv_debug_force_merge_timeout": (C.c_int, [_vp, _i32]),
     "swiftkv_debug_step_plan": (C.c_int, [_i32, _i32, _i32, _vp, _i32, _vp, _vp, _vp, _vp]),
     "swiftkv_rope_lut_load": (C.c_int, [_vp, _vp, _sz, C.POINTER(_vp)]),
     "swiftkv_rope_lut_generate": (C.c_int, [_vp, _i32, C.c_double, C.POINTER(_vp)]),
@@ -227,6 +228,12 @@ class Context:
         context's, or with noalloc this device's allocation-free one) and zero
         its partial words, so launches can be run across the tag wrap."""
         _check(lib().swiftkv_debug_set_split_generation(self.handle, int(generation), 1 if noalloc else 0))
+
+    def debug_force_merge_timeout(self, enable: bool) -> None:
+        """Testing aid: while enabled, every split merge of this context's step
+        launches gives up after one poll (NaN in the merged heads' outputs,
+        SwiftKVError EHIP from the next synchronize, step or graph launch)."""
+        _check(lib().swiftkv_debug_force_merge_timeout(self.handle, 1 if enable else 0))
 
     def set_host_io(self, enable: bool) -> None:
         """Host-memory I/O: step and append tensors are numpy arrays, staged
@@ -531,8 +538,10 @@ def swiftkv_attention_exact(ctx: Context, q, k, v, kv_cache: KVCache, rope_lut: 
     single-pass (max, Z, Y) recurrence of int4_swiftkv_attention_peN
     (swiftkv_attention.cpp:934-1880), so activation_q / activation_scale are
     bit-identical to the reference's.  out_q17: device [batch][4096] int32,
-    the normalized Q15.17 state.  A verification path: one workgroup per
-    (sequence, head), sequential in the token index.
+    the normalized Q15.17 state.  A verification path: one to four
+    workgroups per (sequence, head), sequential in the token index.  Every
+    position must be below 4096, the reference's bound (SwiftKVError ERANGE
+    otherwise, with nothing enqueued).
     """
     pos = np.ascontiguousarray(np.atleast_1d(np.asarray(position, dtype=np.int32)))
     _check_io_sizes(ctx, pos.size, q, k, v, out_q17, activation_q, activation_scale)

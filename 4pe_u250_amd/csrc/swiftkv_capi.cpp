@@ -19,6 +19,7 @@
 #include <mutex>
 #include <new>
 #include <string>
+#include <unordered_map>
 #include <unordered_set>
 #include <vector>
 
@@ -101,16 +102,26 @@ struct swiftkv_context {
     uint64_t* partials = nullptr;
     int32_t partial_rows = 0;
     int32_t partial_slots = 0;
-    // Graphs record the workspace pointer in their kernel nodes, so a buffer
-    // the workspace outgrows while a graph of this context exists is kept
-    // here, and released when the last graph is destroyed.
-    int64_t graphs = 0;
+    // Graphs record the workspace pointer in their kernel nodes.  Each graph
+    // names the buffer it recorded (if any), with a count of live graphs per
+    // buffer here; a buffer the workspace outgrows is freed at once unless a
+    // live graph recorded it, and is then kept in `retired` until the last
+    // such graph is destroyed.
+    std::unordered_map<void*, int64_t> graph_refs;
     std::vector<void*> retired;
+    bool capture_uses_workspace = false;   // a split launch of the capture in progress used `partials`
     // [kMaxBatchPerLaunch][32] arrival words (kArrivalStride apart), zero, for
     // launches that split no head: the step reads its arrival word on every
     // path but only a split head's merge writes one
     uint64_t* arrivals = nullptr;
     uint8_t* scratch = nullptr;     // this device's allocation-free workspace (arrival words, then partials)
+    // Fault word of the split merges: pinned host memory that a step kernel
+    // writes (system scope) when a merge gives up on a partial, read without
+    // a device round trip by swiftkv_synchronize, the step entries and graph
+    // launches, which report it once and clear it.
+    uint32_t* fault_host = nullptr;
+    uint32_t* fault_dev = nullptr;
+    bool merge_fault_test = false;  // testing aid: merges wait for a tag no word carries
     // timing
     hipEvent_t timers[kTimerSlots] = {};
     bool profiling = false;
@@ -133,6 +144,7 @@ struct swiftkv_graph {
     swiftkv_context* ctx = nullptr;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
+    void* workspace = nullptr;   // the split workspace buffer its launches recorded, if any
 };
 
 struct swiftkv_rope_lut {
@@ -173,12 +185,32 @@ int not_capturing(const swiftkv_context* ctx, const char* what) {
     return SWIFTKV_OK;
 }
 
-// Releases the buffers retired while graphs existed (none may be left).
-int free_retired(swiftkv_context* ctx) {
-    if (ctx->retired.empty()) return SWIFTKV_OK;
-    SKV_HIP(hipStreamSynchronize(ctx->stream));
-    for (void* p : ctx->retired) SKV_HIP(hipFree(p));
-    ctx->retired.clear();
+// A split merge that gave up waiting for another split's partial (its head's
+// output holds NaN) left slot * 32 + head + 1 in the context's fault word:
+// report it once, as a HIP-side failure, and clear the word.
+int take_fault(swiftkv_context* ctx) {
+    if (!ctx->fault_host) return SWIFTKV_OK;
+    const uint32_t f = __atomic_exchange_n(ctx->fault_host, 0u, __ATOMIC_ACQ_REL);
+    if (f == 0) return SWIFTKV_OK;
+    const uint32_t slot = (f - 1) / kHeads, head = (f - 1) % kHeads;
+    return fail(SWIFTKV_EHIP, "a split merge of an earlier step gave up waiting for another split's partial "
+                "(cache slot %u, head %u, perhaps among others): that head's output holds NaN", slot, head);
+}
+
+// A graph that recorded workspace buffer `p` has been destroyed: when no live
+// graph records it any more and the workspace has outgrown it, free it.
+int release_graph_workspace(swiftkv_context* ctx, void* p) {
+    auto it = ctx->graph_refs.find(p);
+    if (it == ctx->graph_refs.end() || --it->second > 0) return SWIFTKV_OK;
+    ctx->graph_refs.erase(it);
+    auto r = std::find(ctx->retired.begin(), ctx->retired.end(), p);
+    if (r == ctx->retired.end()) return SWIFTKV_OK;   // still the current workspace
+    ctx->retired.erase(r);
+    const hipError_t sync = hipStreamSynchronize(ctx->stream);
+    const hipError_t fr = hipFree(p);
+    if (sync != hipSuccess || fr != hipSuccess)
+        return fail(SWIFTKV_EHIP, "releasing a split workspace: %s",
+                    hipGetErrorString(sync != hipSuccess ? sync : fr));
     return SWIFTKV_OK;
 }
 
@@ -224,7 +256,7 @@ int ensure_partials(swiftkv_context* ctx, int32_t rows, int32_t slots) {
     const int32_t new_rows = std::max(rows, ctx->partial_rows);
     const int32_t new_slots = std::max({slots, ctx->partial_slots, kFixedSlots});
     if (ctx->partials) {
-        if (ctx->graphs > 0) {
+        if (ctx->graph_refs.count(ctx->partials)) {
             ctx->retired.push_back(ctx->partials);
         } else {
             SKV_HIP(hipStreamSynchronize(ctx->stream));
@@ -300,7 +332,7 @@ int upload_lut(swiftkv_context* ctx, std::vector<int2>&& host, int32_t positions
 }
 
 // Tokens per split.  A launch runs best when it fills one residency round:
-// one 16-wave workgroup per CU (step_waves picks 16 waves for such launches),
+// one 16-wave workgroup per CU (step_shape picks 16 waves for such launches),
 // or step_per_cu 4-wave workgroups per CU.  So
 //   batch x 32 heads <= CUs:  splits = CUs / heads (at most 8);
 //   otherwise:                splits = step_per_cu x CUs / heads (at least 1),
@@ -345,17 +377,17 @@ int32_t choose_split(const SplitPolicy& pol, const int32_t* positions, int32_t b
     return static_cast<int32_t>(std::min<int64_t>(quanta * kSplitQuantum, kMaxSeq));
 }
 
-// Waves per workgroup.  A launch of at most one workgroup per CU whose
+// Launch shape.  A launch of at most one workgroup per CU whose
 // splits are whole multiples of 512 tokens runs 16 waves per workgroup on
 // 32-token blocks: four waves share a SIMD and each holds half a block, so
 // less math is left when the last data arrives (32 layers at context 4096:
 // batch 2 17.1 against 17.6 us/layer with 8 waves on 64-token blocks,
 // batch 8 50.6 against 51.0; batch 1 unchanged).  Larger launches fill the
 // machine either way and keep 4 waves, so more workgroups stay resident per CU.
-int step_waves(const SplitPolicy& pol, int32_t grid_splits, int32_t batch, int32_t split_tokens) {
+StepShape step_shape(const SplitPolicy& pol, int32_t grid_splits, int32_t batch, int32_t split_tokens) {
     const int64_t workgroups = static_cast<int64_t>(grid_splits) * kHeads * batch;
     const bool wide = workgroups <= pol.cus && split_tokens % kWideRoundTokens == 0;
-    return wide ? kWideWaves : kAttendWaves;
+    return wide ? kWideShape : kNarrowShape;
 }
 
 // Dispatch rows of one launch: (position, sequence) longest first, equal
@@ -390,10 +422,21 @@ constexpr StepInput kF32Input{kInF32, 0}, kQ17Input{kInQ17, 0};
 // every extent computed from it far from overflow.
 constexpr int64_t kMaxPartStride = int64_t(1) << 40;
 
+// Positions the integer-compatibility entry accepts: the reference's own
+// bound.  Its position is ap_uint<12> and SWIFTKV_MAX_SEQ_LEN = 4096
+// (swiftkv_attention.hpp:26-30); Z, a Q13.17 sum of at most position + 1
+// coefficients of at most 1.0 wrapped to 30 bits, cannot wrap only while the
+// sequence stays below 2^13 tokens, which the reference asserts at compile
+// time (swiftkv_attention.cpp:112-119).  Past the bound the recurrence would
+// wrap where the reference has no defined result.
+constexpr int32_t kExactPositions = SWIFTKV_REFERENCE_MAX_SEQ;
+
+// exact: the integer-compatibility entry, which also refuses positions at or
+// past kExactPositions.
 int validate_step(swiftkv_context* ctx, const void* q, const void* k, const void* v,
                   const swiftkv_kv_cache* kv, const swiftkv_rope_lut* lut, const uint8_t* act_q,
                   const uint8_t* act_scale, int32_t layer, const int32_t* positions, int32_t batch,
-                  const float* out) {
+                  const float* out, bool exact = false) {
     if (!ctx) return fail(SWIFTKV_EINVAL, "null context");
     if (!q || !k || !v || !out) return fail(SWIFTKV_EINVAL, "null q/k/v/out pointer");
     if (!kv || kv->ctx != ctx) return fail(SWIFTKV_EINVAL, "kv_cache is null or belongs to another context");
@@ -410,6 +453,12 @@ int validate_step(swiftkv_context* ctx, const void* q, const void* k, const void
         if (positions[b] < 0 || positions[b] >= limit)
             return fail(SWIFTKV_ERANGE, "positions[%d] = %d outside [0, %d) (cache %d, RoPE table %d)", b,
                         positions[b], limit, kv->seq_cap, lut->positions);
+    if (exact)
+        for (int32_t b = 0; b < batch; ++b)
+            if (positions[b] >= kExactPositions)
+                return fail(SWIFTKV_ERANGE, "positions[%d] = %d: the integer-compatibility entry keeps the "
+                            "reference's bound position < %d (its Q13.17 normalizer may wrap beyond it)", b,
+                            positions[b], kExactPositions);
     return SWIFTKV_OK;
 }
 
@@ -474,6 +523,7 @@ int run_step(swiftkv_context* ctx, const void* q, const void* k, const void* v, 
             a.slot_stride = kFixedSlots;
         } else if (grid_splits > 1) {
             if ((rc = ensure_partials(ctx, nb, grid_splits))) return rc;
+            if (ctx->capturing) ctx->capture_uses_workspace = true;
             a.arrivals = ctx->partials;
             a.partials = ctx->partials + arrival_words(ctx->partial_rows);
             a.slot_stride = ctx->partial_slots;
@@ -486,9 +536,12 @@ int run_step(swiftkv_context* ctx, const void* q, const void* k, const void* v, 
         a.act_q = act_q ? act_q + static_cast<size_t>(b0) * kHeads * kGroupsPerHead * SWIFTKV_A14_WORD_BYTES
                         : nullptr;
         a.act_scale = act_scale ? act_scale + static_cast<size_t>(b0) * kHeads * kGroupsPerHead : nullptr;
+        a.merge_polls = ctx->merge_fault_test ? 1u : kMergePolls;
+        a.merge_tag_skew = ctx->merge_fault_test ? 1u : 0u;
+        a.fault = ctx->fault_dev;
 
         ProfilePair* p = profile_begin(ctx, SWIFTKV_KERNEL_STEP);
-        SKV_HIP(launch_step(a, grid_splits, step_waves(policy_of(ctx), grid_splits, nb, a.split_tokens), in.format,
+        SKV_HIP(launch_step(a, grid_splits, step_shape(policy_of(ctx), grid_splits, nb, a.split_tokens), in.format,
                             ctx->stream));
         profile_end(ctx, p);
     }
@@ -510,7 +563,7 @@ int run_exact(swiftkv_context* ctx, const void* q, const void* k, const void* v,
               swiftkv_kv_cache* kv, const swiftkv_rope_lut* lut, uint8_t* act_q, uint8_t* act_scale,
               int32_t layer, const int32_t* positions, int32_t batch, int32_t* out) {
     int rc = validate_step(ctx, q, k, v, kv, lut, act_q, act_scale, layer, positions, batch,
-                           reinterpret_cast<const float*>(out));
+                           reinterpret_cast<const float*>(out), true);
     if (rc) return rc;
     if ((rc = set_device(ctx))) return rc;
     for (int32_t b0 = 0; b0 < batch; b0 += kMaxBatchPerLaunch) {
@@ -549,6 +602,7 @@ int dispatch_step(swiftkv_context* ctx, bool exact, const void* q, const void* k
                   swiftkv_kv_cache* kv, const swiftkv_rope_lut* lut, uint8_t* act_q, uint8_t* act_scale,
                   int32_t layer, const int32_t* positions, int32_t batch, void* out) {
     if (!ctx) return fail(SWIFTKV_EINVAL, "null context");
+    if (int rc = take_fault(ctx)) return rc;
     if (!ctx->host_io) {
         return exact ? run_exact(ctx, q, k, v, in, kv, lut, act_q, act_scale, layer, positions, batch,
                                  static_cast<int32_t*>(out))
@@ -556,7 +610,7 @@ int dispatch_step(swiftkv_context* ctx, bool exact, const void* q, const void* k
                                 static_cast<float*>(out));
     }
     int rc = validate_step(ctx, q, k, v, kv, lut, act_q, act_scale, layer, positions, batch,
-                           static_cast<const float*>(out));
+                           static_cast<const float*>(out), exact);
     if (rc) return rc;
     if ((rc = set_device(ctx))) return rc;
     auto align = [](size_t x) { return (x + 255) & ~static_cast<size_t>(255); };
@@ -585,6 +639,7 @@ int dispatch_step(swiftkv_context* ctx, bool exact, const void* q, const void* k
         SKV_HIP(hipMemcpyAsync(act_scale, d_as, as_bytes, hipMemcpyDeviceToHost, ctx->stream));
     }
     SKV_HIP(hipStreamSynchronize(ctx->stream));
+    if ((rc = take_fault(ctx))) return rc;
     return ok();
 }
 
@@ -625,6 +680,7 @@ void free_context(swiftkv_context* ctx) {
     for (void* p : ctx->retired) (void)hipFree(p);
     if (ctx->arrivals) (void)hipFree(ctx->arrivals);
     if (ctx->io_stage) (void)hipFree(ctx->io_stage);
+    if (ctx->fault_host) (void)hipHostFree(ctx->fault_host);
     for (auto& t : ctx->timers)
         if (t) (void)hipEventDestroy(t);
     for (auto& p : ctx->profile_pool) {
@@ -663,6 +719,15 @@ int swiftkv_context_create(int device, swiftkv_context** out) {
     void* scratch = nullptr;
     if (e == hipSuccess) e = scratch_for_device(device, count, ctx->stream, &scratch);
     ctx->scratch = static_cast<uint8_t*>(scratch);
+    void* fault = nullptr;
+    if (e == hipSuccess) e = hipHostMalloc(&fault, sizeof(uint32_t), hipHostMallocMapped | hipHostMallocCoherent);
+    if (e == hipSuccess) {
+        ctx->fault_host = static_cast<uint32_t*>(fault);
+        *ctx->fault_host = 0u;
+        void* dev = nullptr;
+        e = hipHostGetDevicePointer(&dev, fault, 0);
+        ctx->fault_dev = static_cast<uint32_t*>(dev);
+    }
     if (e != hipSuccess) {
         swiftkv_context_destroy(ctx);
         return fail(SWIFTKV_EHIP, "stream/event creation: %s", hipGetErrorString(e));
@@ -692,6 +757,13 @@ int swiftkv_synchronize(swiftkv_context* ctx) {
     rc = set_device(ctx);
     if (rc) return rc;
     SKV_HIP(hipStreamSynchronize(ctx->stream));
+    if ((rc = take_fault(ctx))) return rc;
+    return ok();
+}
+
+int swiftkv_debug_force_merge_timeout(swiftkv_context* ctx, int32_t enable) {
+    if (!ctx) return fail(SWIFTKV_EINVAL, "null context");
+    ctx->merge_fault_test = enable != 0;
     return ok();
 }
 
@@ -730,7 +802,7 @@ int swiftkv_debug_step_plan(int32_t cus, int32_t workgroups_per_cu, int32_t spli
     set_rows(a, positions);
     *out_split_tokens = choose_split(pol, positions, batch);
     *out_grid_splits = (max_pos + *out_split_tokens) / *out_split_tokens;
-    *out_waves = step_waves(pol, *out_grid_splits, batch, *out_split_tokens);
+    *out_waves = step_shape(pol, *out_grid_splits, batch, *out_split_tokens).waves;
     if (out_rows)
         for (int32_t z = 0; z < batch; ++z) out_rows[z] = static_cast<int32_t>(a.rows[z] & 0xffu);
     return ok();
@@ -1018,6 +1090,7 @@ int swiftkv_attention_f32_noalloc(swiftkv_context* ctx, const float* q, const fl
                                   uint8_t* activation_q, uint8_t* activation_scale, int32_t layer_index,
                                   const int32_t* positions, int32_t batch, float* out) {
     if (!ctx) return fail(SWIFTKV_EINVAL, "null context");
+    if (int rc = take_fault(ctx)) return rc;
     if (ctx->host_io)
         return fail(SWIFTKV_ESTATE, "host-memory I/O mode stages through an allocated buffer: switch it off for "
                     "the allocation-free entry");
@@ -1263,6 +1336,7 @@ int swiftkv_capture_begin(swiftkv_context* ctx) {
     if (rc) return rc;
     SKV_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
     ctx->capturing = true;
+    ctx->capture_uses_workspace = false;
     return ok();
 }
 
@@ -1290,8 +1364,13 @@ int swiftkv_capture_end(swiftkv_context* ctx, swiftkv_graph** out) {
     g->ctx = ctx;
     g->graph = graph;
     g->exec = exec;
+    // A capture cannot grow the workspace, so every split launch it recorded
+    // used the current buffer.
+    if (ctx->capture_uses_workspace) {
+        g->workspace = ctx->partials;
+        ++ctx->graph_refs[g->workspace];
+    }
     ++ctx->children;
-    ++ctx->graphs;
     *out = g;
     return ok();
 }
@@ -1301,6 +1380,7 @@ int swiftkv_graph_launch(swiftkv_context* ctx, const swiftkv_graph* graph) {
     if (graph->ctx != ctx) return fail(SWIFTKV_EINVAL, "graph belongs to another context");
     int rc = not_capturing(ctx, "swiftkv_graph_launch");
     if (rc) return rc;
+    if ((rc = take_fault(ctx))) return rc;
     if ((rc = set_device(ctx))) return rc;
     SKV_HIP(hipGraphLaunch(graph->exec, ctx->stream));
     return ok();
@@ -1314,9 +1394,8 @@ int swiftkv_graph_destroy(swiftkv_graph* graph) {
     (void)hipStreamSynchronize(ctx->stream);
     if (graph->exec) (void)hipGraphExecDestroy(graph->exec);
     if (graph->graph) (void)hipGraphDestroy(graph->graph);
+    const int rc = graph->workspace ? release_graph_workspace(ctx, graph->workspace) : SWIFTKV_OK;
     delete graph;
-    int rc = SWIFTKV_OK;
-    if (--ctx->graphs == 0) rc = free_retired(ctx);
     release_child(ctx);
     return rc ? rc : ok();
 }

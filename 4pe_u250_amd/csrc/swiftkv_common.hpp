@@ -36,6 +36,15 @@ constexpr int kBlockTokens = 64;
 constexpr int kWideWaves = 16;
 constexpr int kWideBlockTokens = 32;
 constexpr int kWideRoundTokens = kWideWaves * kWideBlockTokens;   // 512
+
+// A step launch's shape: waves per workgroup and tokens per block.
+struct StepShape {
+    int waves;
+    int block_tokens;
+    constexpr bool operator==(const StepShape& o) const { return waves == o.waves && block_tokens == o.block_tokens; }
+};
+constexpr StepShape kNarrowShape{kAttendWaves, kBlockTokens};
+constexpr StepShape kWideShape{kWideWaves, kWideBlockTokens};
 constexpr int kSplitQuantum = kAttendWaves * kBlockTokens;   // 256
 constexpr int kMaxSeq = 32768;                   // longest cache accepted (tokens per sequence)
 constexpr int kMaxSplits = kMaxSeq / kSplitQuantum;   // 128 partials per (sequence, head)
@@ -46,6 +55,11 @@ constexpr int kSlotWords = 2 + kHeadDim;
 // Slots per (row, head) in the allocation-free layout (the heuristic never
 // splits a head more than 8 ways).
 constexpr int kFixedSlots = 8;
+
+// Polls a split merger makes in all (each a round of re-reads of the words
+// still missing, about a microsecond) before it gives up on a partial that
+// never arrives: seconds, far beyond any wait the protocol can need.
+constexpr uint32_t kMergePolls = 1u << 22;
 
 // Per (row, head) arrival word {generation:32 | arrivals:32}, one per 128-byte
 // cache line: the splits of all heads finish together, and words sharing a
@@ -100,6 +114,13 @@ struct StepArgs {
     float* out;               // [batch][4096]
     uint8_t* act_q;           // [batch][128][56] or null
     uint8_t* act_scale;       // [batch][128] or null
+    // Split merges: the polls a merger makes in all before it gives up
+    // (kMergePolls), a testing aid's skew of the tag it waits for (0 in
+    // service), and the context's fault word, where a merger that gave up
+    // leaves its slot * 32 + head + 1.
+    uint32_t merge_polls;
+    uint32_t merge_tag_skew;
+    uint32_t* fault;
     // Dispatch row z serves sequence rows[z] & 0xff at position rows[z] >> 8
     // (one scalar load gives both).  The host orders rows by descending
     // position, longest first, so ragged batches do not end on a tail of long
@@ -135,9 +156,9 @@ constexpr size_t kNoAllocPartialBytes =
 constexpr size_t kNoAllocScratchBytes = kNoAllocCounterBytes + kNoAllocPartialBytes;
 
 // Launchers (swiftkv_kernels.hip).
-// waves: kAttendWaves, or kWideWaves when a.split_tokens is a multiple of
+// shape: kNarrowShape, or kWideShape when a.split_tokens is a multiple of
 // kWideRoundTokens.
-hipError_t launch_step(const StepArgs& a, int grid_splits, int waves, InputFormat in, hipStream_t s);
+hipError_t launch_step(const StepArgs& a, int grid_splits, StepShape shape, InputFormat in, hipStream_t s);
 // Workgroups of the 4-wave step kernel one CU holds at once (0 on error).
 int step_workgroups_per_cu();
 hipError_t launch_append_bulk(const BulkArgs& a, bool q17, hipStream_t s);

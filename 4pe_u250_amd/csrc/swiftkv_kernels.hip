@@ -48,10 +48,12 @@ static __device__ __align__(256) unsigned char scratch[swiftkv::kNoAllocScratchB
 // all arrived (an added wait for them), after the workgroup's LDS merge,
 // when the arrival count is known, after the merge and after the epilogue;
 // lane 0 of every wave records when its first loads arrived and when its
-// scan ended.  The product library compiles every stamp away.
+// scan ended; slot 7 holds the workgroup's XCD (low half) and HW_ID register
+// (high half: CU, shader array and engine).  The product library compiles
+// every stamp away.
 #ifdef SWIFTKV_PHASE_STAMPS
 constexpr int kStampWorkgroups = 8192;
-constexpr int kStampSlots = 8;   // entry, first loads, LDS merge, arrival, merge, epilogue, flags, XCD
+constexpr int kStampSlots = 8;   // entry, first loads, LDS merge, arrival, merge, epilogue, flags, XCD + HW_ID
 __device__ unsigned long long g_phase_stamps[kStampWorkgroups * kStampSlots];
 __device__ unsigned long long g_wave_stamps[kStampWorkgroups * 16 * 2];
 #define SKV_STAMP_DECL unsigned long long skv_st[kStampSlots] = {0, 0, 0, 0, 0, 0, 0, 0}
@@ -66,9 +68,10 @@ __device__ unsigned long long g_wave_stamps[kStampWorkgroups * 16 * 2];
 #define SKV_STAMP_FLUSH() do {                                                                      \
         const size_t wg_ = (static_cast<size_t>(blockIdx.z) * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x; \
         if (threadIdx.x == 0 && wg_ < kStampWorkgroups) {                                           \
-            unsigned xcc_;                                                                          \
+            unsigned xcc_, hw_;                                                                     \
             asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc_));                    \
-            skv_st[7] = xcc_;                                                                       \
+            asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw_));                      \
+            skv_st[7] = xcc_ | (static_cast<unsigned long long>(hw_) << 32);                        \
             for (int i_ = 0; i_ < kStampSlots; ++i_) g_phase_stamps[wg_ * kStampSlots + i_] = skv_st[i_]; \
         }                                                                                           \
     } while (0)
@@ -406,22 +409,39 @@ __device__ __forceinline__ uint64_t fetch_word(const uint64_t* p) {
     return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Re-reads of a word before the merger gives up on it.  Every split it waits
-// for has already counted its arrival, so it is resident and its store is in
-// flight; the bound only keeps a fault in this protocol from hanging the GPU.
-constexpr uint32_t kSpinLimit = 1u << 22;
+// Polls (rounds of re-reads) a merger makes in all before it gives up
+// (StepArgs::merge_polls; the host passes kMergePolls).  Every split it waits
+// for has counted its arrival, so it is resident, and nothing its waves 0-1
+// do before their stores waits for another workgroup: its words will land.
+// The bound only keeps a fault in this protocol from hanging the GPU.  A
+// merger that gives up takes NaN for the words it still lacks (so the fault
+// shows in the output) and records its (slot, head) in the context's fault
+// word, which the host reports.
 
 __device__ __forceinline__ bool current(uint64_t w, uint32_t tag) { return static_cast<uint32_t>(w >> 32) == tag; }
 
-// The value of the word at p (first read w), re-read until it carries `tag`;
-// NaN (which then shows in the output) if the bound runs out.
-__device__ __forceinline__ float tagged_value(const uint64_t* p, uint64_t w, uint32_t tag) {
-    for (uint32_t spin = 0; !current(w, tag); ++spin) {
-        if (spin == kSpinLimit) return __builtin_nanf("");
+// The value of the word at p (first read w), re-read until it carries `tag`
+// while the thread's poll budget lasts -- one budget for every word the
+// thread waits for, so a merge that cannot complete gives up after `budget`
+// polls in all -- and NaN, with gave_up set, once it has run out.
+__device__ __forceinline__ float tagged_value(const uint64_t* p, uint64_t w, uint32_t tag, uint32_t& budget,
+                                              bool& gave_up) {
+    while (!current(w, tag)) {
+        if (budget == 0) {
+            gave_up = true;
+            return __builtin_nanf("");
+        }
+        --budget;
         __builtin_amdgcn_s_sleep(1);
         w = fetch_word(p);
     }
     return __uint_as_float(static_cast<uint32_t>(w));
+}
+
+// Records a merge that gave up: the fault word is host memory, written through
+// at system scope so the host sees it once the launch has ended (or earlier).
+__device__ __forceinline__ void report_merge_fault(uint32_t* fault, uint32_t code) {
+    __hip_atomic_store(fault, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 // Log-sum-exp merge of a head's n split partials by the split `own`, which
@@ -434,8 +454,8 @@ __device__ __forceinline__ float tagged_value(const uint64_t* p, uint64_t w, uin
 // so the result does not depend on the arrival order.
 constexpr int kMergeInline = 8;
 
-__device__ __forceinline__ float merge_partials(const uint64_t* slots, int n, int own, uint32_t tag, float own_m,
-                                                float own_l, float own_o) {
+__device__ __forceinline__ float merge_partials(const uint64_t* slots, int n, int own, uint32_t tag, uint32_t polls,
+                                                float own_m, float own_l, float own_o, bool& gave_up) {
     // Inline: called by waves 0-1 only.  Looped: by every wave (it stages the
     // statistics through LDS behind a barrier); lanes past 127 read channel
     // 127 and their result is unused.
@@ -464,9 +484,10 @@ __device__ __forceinline__ float merge_partials(const uint64_t* slots, int n, in
             for (int j = 0; j < kMergeInline; ++j)
                 stale |= !current(wm[j], tag) || !current(wl[j], tag) || !current(wo[j], tag);
             if (!stale) break;
-            if (spin == kSpinLimit) {
+            if (spin == polls) {
 #pragma unroll
                 for (int j = 0; j < kMergeInline; ++j) wo[j] = own_tag | 0x7fc00000u;   // NaN shows in the output
+                gave_up = true;
                 break;
             }
             __builtin_amdgcn_s_sleep(1);
@@ -502,10 +523,11 @@ __device__ __forceinline__ float merge_partials(const uint64_t* slots, int n, in
     }
     __shared__ float s_m[kMaxSplits], s_l[kMaxSplits];
     const int t = threadIdx.x;
+    uint32_t budget = polls;
     if (t < n) {
         const uint64_t* sl = slots + t * kSlotWords;
-        s_m[t] = t == own ? own_m : tagged_value(sl, fetch_word(sl), tag);
-        s_l[t] = t == own ? own_l : tagged_value(sl + 1, fetch_word(sl + 1), tag);
+        s_m[t] = t == own ? own_m : tagged_value(sl, fetch_word(sl), tag, budget, gave_up);
+        s_l[t] = t == own ? own_l : tagged_value(sl + 1, fetch_word(sl + 1), tag, budget, gave_up);
     }
     __syncthreads();
     float mx = s_m[0];
@@ -515,19 +537,17 @@ __device__ __forceinline__ float merge_partials(const uint64_t* slots, int n, in
         const uint64_t* sl = slots + j * kSlotWords + 2 + d;
         const float w = fast_exp2(s_m[j] - mx);
         den += w * s_l[j];
-        num += w * (j == own ? own_o : tagged_value(sl, fetch_word(sl), tag));
+        num += w * (j == own ? own_o : tagged_value(sl, fetch_word(sl), tag, budget, gave_up));
     }
     return num / den;
 }
 
 // ---------------------------------------------------------------- step
 
-// Grid (splits, 32 heads, batch), 256 threads; grid row z serves rows[z].
-template <int IN, int WAVES>
+// Grid (splits, 32 heads, batch) of WAVES-wave workgroups scanning blocks of
+// 8 * NI tokens (NI rows per lane); grid row z serves rows[z].
+template <int IN, int WAVES, int NI>
 __global__ __launch_bounds__(WAVES * 64) void step_kernel(StepArgs a) {
-    // Rows per lane in a block: 4-wave workgroups scan 64-token blocks (NI = 8),
-    // 16-wave workgroups 32-token blocks (NI = 4).
-    constexpr int NI = (WAVES == kWideWaves ? kWideBlockTokens : kBlockTokens) / 8;
     constexpr int kBlk = 8 * NI;
     SKV_STAMP_DECL;
     SKV_STAMP(0);
@@ -697,8 +717,13 @@ __global__ __launch_bounds__(WAVES * 64) void step_kernel(StepArgs a) {
         SKV_STAMP_FLUSH();
         return;
     }
-    const float merged = merge_partials(slots, nsplit, split, tag, mx, l, o);
+    // The merger waits for words tagged `tag` (a testing aid can make it wait
+    // for a tag no word carries, so that the wait gives up).
+    bool gave_up = false;
+    const float merged = merge_partials(slots, nsplit, split, tag + a.merge_tag_skew, a.merge_polls, mx, l, o,
+                                        gave_up);
     SKV_STAMP(4);
+    if (gave_up) report_merge_fault(a.fault, static_cast<uint32_t>(a.slot0 + b) * kHeads + h + 1u);
     if (d >= kHeadDim) return;
     finalize_head(a, b, h, merged);
     SKV_STAMP(5);
@@ -970,14 +995,15 @@ hipError_t launch_fill_u64(uint64_t* p, size_t n, uint64_t value, hipStream_t s)
     return hipGetLastError();
 }
 
-template <int WAVES>
-hipError_t launch_step_waves(const StepArgs& a, dim3 grid, InputFormat in, hipStream_t s) {
+template <int WAVES, int BLOCK>
+hipError_t launch_step_shape(const StepArgs& a, dim3 grid, InputFormat in, hipStream_t s) {
+    constexpr int NI = BLOCK / 8;
     const dim3 block(WAVES * 64);
     switch (in) {
-    case kInF32: step_kernel<kInF32, WAVES><<<grid, block, 0, s>>>(a); break;
-    case kInQ17: step_kernel<kInQ17, WAVES><<<grid, block, 0, s>>>(a); break;
-    case kInParts2: step_kernel<kInParts2, WAVES><<<grid, block, 0, s>>>(a); break;
-    case kInParts4: step_kernel<kInParts4, WAVES><<<grid, block, 0, s>>>(a); break;
+    case kInF32: step_kernel<kInF32, WAVES, NI><<<grid, block, 0, s>>>(a); break;
+    case kInQ17: step_kernel<kInQ17, WAVES, NI><<<grid, block, 0, s>>>(a); break;
+    case kInParts2: step_kernel<kInParts2, WAVES, NI><<<grid, block, 0, s>>>(a); break;
+    case kInParts4: step_kernel<kInParts4, WAVES, NI><<<grid, block, 0, s>>>(a); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -985,17 +1011,17 @@ hipError_t launch_step_waves(const StepArgs& a, dim3 grid, InputFormat in, hipSt
 
 int step_workgroups_per_cu() {
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, step_kernel<kInF32, kAttendWaves>, kAttendWaves * 64, 0) !=
-        hipSuccess)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, step_kernel<kInF32, kAttendWaves, kBlockTokens / 8>,
+                                                     kAttendWaves * 64, 0) != hipSuccess)
         return 0;
     return n;
 }
 
-hipError_t launch_step(const StepArgs& a, int grid_splits, int waves, InputFormat in, hipStream_t s) {
+hipError_t launch_step(const StepArgs& a, int grid_splits, StepShape shape, InputFormat in, hipStream_t s) {
     const dim3 grid(grid_splits, kHeads, a.batch);
-    if (waves == kAttendWaves) return launch_step_waves<kAttendWaves>(a, grid, in, s);
-    if (waves == kWideWaves && a.split_tokens % kWideRoundTokens == 0)
-        return launch_step_waves<kWideWaves>(a, grid, in, s);
+    if (shape == kNarrowShape) return launch_step_shape<kAttendWaves, kBlockTokens>(a, grid, in, s);
+    if (shape == kWideShape && a.split_tokens % kWideRoundTokens == 0)
+        return launch_step_shape<kWideWaves, kWideBlockTokens>(a, grid, in, s);
     return hipErrorInvalidValue;
 }
 

@@ -242,6 +242,12 @@ Config parse_args(int argc, char** argv, bool* help) {
         msg << "the run reaches position " << last << ", beyond the cache limit " << SWIFTKV_MAX_SEQ - 1;
         throw std::runtime_error(msg.str());
     }
+    if (c.exact && last >= SWIFTKV_REFERENCE_MAX_SEQ) {
+        std::ostringstream msg;
+        msg << "the run reaches position " << last << "; --exact keeps the reference's bound (positions below "
+            << SWIFTKV_REFERENCE_MAX_SEQ << ")";
+        throw std::runtime_error(msg.str());
+    }
     return c;
 }
 

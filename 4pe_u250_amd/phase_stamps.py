@@ -1,7 +1,7 @@
 """Phase breakdown of the decode-attention step kernel on the GPU.
 
     python 4pe_u250_amd/phase_stamps.py [--batches 1,2,4] [--position 4095] [--layers 32] [--reps 10]
-                                        [--parts 4]
+                                        [--parts 4] [--raw DIR]
 
 Runs 32-layer decode steps through the instrumented build libswiftkv_stamps.so
 (built by build.py: the product sources with SWIFTKV_PHASE_STAMPS, whose step
@@ -81,6 +81,9 @@ def main():
     ap.add_argument("--reps", type=int, default=10)
     ap.add_argument("--json", default=None, help="also write the medians here")
     ap.add_argument("--parts", type=int, default=0, help="feed N split-K FP32 partials (swiftkv_attention_partials)")
+    ap.add_argument("--raw", default=None, metavar="DIR",
+                    help="also save each repetition's stamps of the last launch (live workgroups, with their "
+                         "grid index) as DIR/stamps_batch<B>.npz")
     args = ap.parse_args()
     if not os.path.exists(STAMPS_LIB):
         raise SystemExit(f"{STAMPS_LIB} is missing: python 4pe_u250_amd/build.py")
@@ -116,7 +119,7 @@ def main():
         for _ in range(3):
             step()
         ctx.synchronize()
-        rows = []
+        rows, raw = [], []
         ph = np.zeros((WGS, SLOTS), np.uint64)
         wv = np.zeros((WGS, 16, 2), np.uint64)
         for _ in range(args.reps):
@@ -132,6 +135,8 @@ def main():
             # launch are milliseconds older
             live = (ph[:, 0] > 0) & (ph[:, 0] >= ph[:, 0].max() - np.uint64(100000))
             nwg = int(live.sum())
+            if args.raw:
+                raw.append((np.flatnonzero(live), ph[live].copy(), wv[live].copy()))
             d = launch_phases(ph[live], wv[live], nwg)
             d["us_per_layer"] = us_layer
             d["launch"] = us_layer - d["span"]
@@ -141,6 +146,13 @@ def main():
         tag = f", {parts} partials" if parts else ""
         out[f"batch{batch}_position{pos}" + (f"_parts{parts}" if parts else "")] = med
         print(f"batch {batch}, position {pos}, {layers} layers{tag}: " + json.dumps(med), flush=True)
+        if args.raw:
+            os.makedirs(args.raw, exist_ok=True)
+            split, grid, waves, order = skv.step_plan(positions)
+            np.savez_compressed(os.path.join(args.raw, f"stamps_batch{batch}.npz"),
+                                index=np.stack([r[0] for r in raw]), phase=np.stack([r[1] for r in raw]),
+                                wave=np.stack([r[2] for r in raw]), grid=np.array([grid, 32, batch]),
+                                split_tokens=split, waves=waves, position=pos)
         for b in qkv + [o, aq, asc]:
             b.free()
         kv.close()

@@ -30,6 +30,13 @@
  *     HOST pointers;
  *   - work is issued asynchronously on the context's HIP stream; call
  *     swiftkv_synchronize() before reading results on the host;
+ *   - a failure found on the device is reported by the next call that looks
+ *     for it: a split merge that gave up waiting for another split's partial
+ *     (its head's output then holds NaN) makes swiftkv_synchronize, or the
+ *     next step entry or graph launch (which then enqueue nothing), return
+ *     SWIFTKV_EHIP with a message naming the cache slot and head, once (the
+ *     reference host turns a stalled run into an error the same way,
+ *     decode_host.cpp:1433-1467);
  *   - calls on one context are not thread-safe; distinct contexts are.
  */
 #ifndef SWIFTKV_H
@@ -49,8 +56,9 @@ extern "C" {
 #define SWIFTKV_GROUP 32
 #define SWIFTKV_GROUPS_PER_HEAD (SWIFTKV_HEAD_DIM / SWIFTKV_GROUP)
 /* Reference limits: position is ap_uint<12>, SWIFTKV_MAX_SEQ_LEN = 4096
- * (hpp:26-30).  The library accepts longer caches (up to 32768 tokens) with the
- * RoPE table extended by the same closed form. */
+ * (hpp:26-30).  The FP32 step entries accept longer caches (up to 32768
+ * tokens) with the RoPE table extended by the same closed form; the
+ * integer-compatibility entry keeps the reference's bound. */
 #define SWIFTKV_REFERENCE_MAX_SEQ 4096
 #define SWIFTKV_MAX_SEQ 32768
 /* Byte sizes of the reference formats. */
@@ -87,6 +95,8 @@ int swiftkv_context_create(int device, swiftkv_context** out);
  * then refuses new work (SWIFTKV_ESTATE) but stays valid for those destroy
  * calls, and its resources are released with the last of them. */
 int swiftkv_context_destroy(swiftkv_context* ctx);
+/* Waits for the context's work; SWIFTKV_EHIP if a split merge of that work
+ * gave up (see above). */
 int swiftkv_synchronize(swiftkv_context* ctx);
 /* Tokens per split-context work item; 0 selects the built-in heuristic.
  * Must be 0 or a multiple of 256 in [256, 32768]. */
@@ -114,9 +124,18 @@ int swiftkv_debug_step_plan(int32_t cus, int32_t workgroups_per_cu, int32_t spli
  * (noalloc != 0) to `generation` and zeroes its partial words, on the context
  * stream, so a test can run launches across the wrap without 2^32 of them.
  * A context with no split workspace yet is left as it is (its first one
- * starts at generation 0).  `generation` 0xffffffff is refused
- * (SWIFTKV_EINVAL), and so is a call during graph capture (SWIFTKV_ESTATE). */
+ * starts at generation 0).  Buffers the context keeps only for graphs that
+ * recorded them (see the graph section) are not reached.  `generation`
+ * 0xffffffff is refused (SWIFTKV_EINVAL), and so is a call during graph
+ * capture (SWIFTKV_ESTATE). */
 int swiftkv_debug_set_split_generation(swiftkv_context* ctx, uint32_t generation, int32_t noalloc);
+/* Testing aid with no counterpart in the reference.  While enabled, every split
+ * merge of the context's step launches waits for a tag that no partial carries,
+ * so it gives up after one poll: the merged heads' outputs hold NaN and the
+ * failure is reported as above.  Every kernel still exits normally and the
+ * split workspace stays consistent, so steps after it is disabled are exact
+ * again.  Host-only; affects launches enqueued while it is on. */
+int swiftkv_debug_force_merge_timeout(swiftkv_context* ctx, int32_t enable);
 
 /* --------------------------------------------------------------------------
  * RoPE table (kernel_HLS/swiftkv_attention.hpp:55-81; rope_lut.bin format of
@@ -248,10 +267,15 @@ int swiftkv_attention_partials(swiftkv_context* ctx, const float* q, const float
  * and the integer-path A14/E8M0 epilogue (swiftkv_attention.cpp:1694-1771).
  * activation_q / activation_scale equal what int4_swiftkv_attention_peN
  * writes, bit for bit.  The recurrence is sequential in the token index, so
- * this entry is a compatibility and verification path (one workgroup per
- * (sequence, head)), not the fast path.
+ * this entry is a compatibility and verification path (one to four
+ * workgroups per (sequence, head)), not the fast path.
  *   q, k, v   device [batch][4096], FP32 when q17 == 0, Q15.17 int32 otherwise
  *   out_q17   device [batch][4096] int32: the normalized Q15.17 state
+ *   positions each below SWIFTKV_REFERENCE_MAX_SEQ (4096), the reference's
+ *             own bound (position is ap_uint<12>; its Q13.17 normalizer is
+ *             proven not to wrap only below 2^13 tokens,
+ *             swiftkv_attention.cpp:112-119): a call with any position at or
+ *             past it returns SWIFTKV_ERANGE and enqueues nothing
  * Other arguments as for swiftkv_attention_f32. */
 int swiftkv_attention_exact(swiftkv_context* ctx, const void* q, const void* k, const void* v,
                             int32_t q17, swiftkv_kv_cache* kv_cache, const swiftkv_rope_lut* rope_lut,
@@ -345,8 +369,9 @@ int swiftkv_a14_decode(const uint8_t* words, const uint8_t* e8m0, size_t groups,
  * positions, so a replay repeats exactly the recorded work.  Run each
  * recorded call once outside capture first: the split workspace must already
  * be large enough.  Eager calls after a capture may still grow the workspace:
- * the buffer a graph was recorded with stays allocated until the last graph
- * of the context is destroyed, so replays remain valid.  While capturing,
+ * the buffer a graph recorded stays allocated until the last graph that
+ * recorded it is destroyed, so replays remain valid (a buffer no graph
+ * recorded is freed when the workspace outgrows it).  While capturing,
  * calls that synchronize, copy, allocate or memset return SWIFTKV_ESTATE.
  * ------------------------------------------------------------------------ */
 int swiftkv_capture_begin(swiftkv_context* ctx);

@@ -6,15 +6,21 @@ bit for bit:
     emulator's attention stage): A14 codes and scales of every step, chained;
   - the oracle's integer recurrence on FP32 histories with heavy tails,
     outlier channels and positions on both sides of the kernel's 256-token
-    chunk boundaries -- normalized Q15.17 state, A14 words and E8M0 codes."""
+    chunk boundaries, and at position 4095, the reference's last -- normalized
+    Q15.17 state, A14 words and E8M0 codes;
+  - the reference's bound: positions at or past 4096 are refused.
+
+The kernel runs one of three launch shapes by batch size: four workgroups per
+(sequence, head) for batches 1-2, two for batches 3-8, one from batch 9.  The
+large-query, rescale-chain and saturation cases run in each shape."""
 import sys
 
 import numpy as np
 import pytest
 
 import oracle as O
-from gpu_cases import (H, assert_rows_equal, history, oracle_sequence, outlier_channels, prefill, rising_keys,
-                       rising_query)
+from gpu_cases import (H, assert_rows_equal, history, oracle_cache_synthetic, oracle_sequence, outlier_channels,
+                       prefill, rising_keys, rising_query)
 from helpers import f32_normal, kat_vector
 
 pytestmark = pytest.mark.gpu
@@ -101,8 +107,9 @@ def test_exact_matches_reference_decode(skv, ctx, lut4096, golden, case):
     ([1500, 77], "t3", True, False),
     ([300, 700], "wide", False, False),
     ([300, 700, 5, 257, 256, 511, 1, 0, 64], "wide", False, False),
-    ([300, 1030, 1], "normal", False, True),   # one workgroup per head
+    ([300, 1030, 1], "normal", False, True),   # two workgroups per head
     ([700], "t3", False, True),                # four workgroups per head
+    ([300, 1030, 1, 700, 5, 257, 256, 511, 64], "normal", False, True),   # one workgroup per head
 ])
 def test_exact_matches_oracle_integer_recurrence(skv, ctx, lut4096, rope_tables, positions, dist, q17, big_query):
     """big_query: queries past 64.0 in some heads (and saturated channels in
@@ -146,7 +153,7 @@ def test_exact_matches_oracle_integer_recurrence(skv, ctx, lut4096, rope_tables,
     kv.close()
 
 
-@pytest.mark.parametrize("batch", [1, 3])   # four workgroups per head, and one
+@pytest.mark.parametrize("batch", [1, 3, 9])   # four, two and one workgroups per head
 def test_exact_every_token_a_new_maximum(skv, ctx, lut4096, rope_tables, batch):
     """Keys that grow along the query's direction make most tokens a new
     running maximum (578 of 700: INT8 quantization makes some neighbours tie,
@@ -195,10 +202,12 @@ def saturation_cases(mag, batch):
     tokens (lead 0), or at token 968, 200 tokens into its 256-token chunk (the
     composed part there), with lead = (968 - 16384 / mag) / 2."""
     late = int(round((968 - 16384 / mag) / 2))
-    return [(1300, 0, 1000), (1250, late, 1100), (1100, 0, 900)][:batch]
+    cases = [(1300, 0, 1000), (1250, late, 1100), (1100, 0, 900)]
+    return [cases[b % len(cases)] for b in range(batch)]
 
 
-@pytest.mark.parametrize("mag,batch", [(31.0, 1), (31.0, 3), (40.0, 1), (40.0, 3)])
+# batch 1: four workgroups per head; 3: two; 9: one
+@pytest.mark.parametrize("mag,batch", [(31.0, 1), (31.0, 3), (31.0, 9), (40.0, 1), (40.0, 3), (40.0, 9)])
 def test_exact_y_saturates(skv, ctx, lut4096, rope_tables, mag, batch):
     """Y reaches INT32_MAX and INT32_MIN (alternate channels) early in a chunk
     (its ordered part) or late in one (its composed part), stays, and comes
@@ -234,7 +243,7 @@ def test_exact_y_saturates(skv, ctx, lut4096, rope_tables, mag, batch):
     kv.close()
 
 
-@pytest.mark.parametrize("seed,batch", [(99001, 1), (99004, 3)])
+@pytest.mark.parametrize("seed,batch", [(99001, 1), (99004, 3), (99009, 9)])
 def test_exact_y_saturates_mixed_shifts(skv, ctx, lut4096, rope_tables, seed, batch):
     """Y saturates while the V shifts change from token to token (magnitudes
     15 to 130 per token and 1024-channel block: shifts 14 to 18), so batches
@@ -297,6 +306,100 @@ def test_exact_batch_over_one_launch(skv, ctx, lut4096, rope_tables):
         q14, e8 = O.a14_q17(res["int"].reshape(128, 32))
         assert (asc[b] == e8).all() and (aq[b] == O.pack_a14(q14)).all(), f"seq {b}: A14"
     kv.close()
+
+
+@pytest.mark.parametrize("batch,dist,outliers,q17", [(1, 0, True, False), (4, 1, False, True), (12, 0, False, False)],
+                         ids=["batch1_four_workgroups", "batch4_two_workgroups_t3", "batch12_one_workgroup"])
+def test_exact_position4095_matches_oracle(skv, ctx, lut4096, rope_tables, batch, dist, outliers, q17):
+    """The integer-compatibility entry at the reference's last position, 4095
+    (16 chunks of 256 tokens per head), in each launch shape: four workgroups
+    per head (batch 1, K with 1% of channels x20), two (batch 4, Student-t(3),
+    Q15.17 inputs) and one (batch 12).  The device fills the cache from
+    synthetic streams through the append rule; the oracle rebuilds two sampled
+    sequences from the same streams and runs the integer recurrence over all
+    32 heads: every cached row, the appended row, the Q15.17 state, the A14
+    words and the E8M0 codes bit for bit."""
+    cos, sin = rope_tables
+    p = 4095
+    seed = 4700 + batch
+    _note(f"case: exact at position {p}, batch {batch}, dist {dist}, K outliers {outliers}, q17={q17}")
+    kv = skv.KVCache(ctx, layers=1, max_batch=batch, max_seq_len=p + 1)
+    kv.fill_synthetic(lut4096, ntok=p, seed=seed, dist=dist, k_outliers=outliers)
+    host = []
+    for i in range(3):
+        buf = ctx.alloc(batch * 4096 * 4)
+        ctx.fill_synthetic(buf, batch * 4096, seed + 1, 9300 + i, dist, outliers and i == 1)
+        host.append(buf.download(np.float32, (batch, 4096)))
+        buf.free()
+    q, k, v = host
+    qq, kq, vq = O.f2q17(q), O.f2q17(k), O.f2q17(v)
+    out, aq, asc = exact_step(skv, ctx, kv, lut4096, 0, [p] * batch, *((qq, kq, vq) if q17 else (q, k, v)), q17=q17)
+    for b in sorted({0, batch - 1}):
+        _note(f"  oracle check of slot {b}")
+        sc = oracle_cache_synthetic(skv, ctx, cos, sin, seed, b, 0, p, p + 1, dist=dist, k_outliers=outliers)
+        res = sc.step_q17(qq[b], kq[b], vq[b], p, cos[p], sin[p], fp=False, integer=True)
+        assert_rows_equal(kv, sc, b, 0, 0, p + 1)
+        ref = res["int"].reshape(4096)
+        diff = np.flatnonzero(out[b] != ref)
+        assert diff.size == 0, f"seq {b}: {diff.size} Q15.17 values differ (first {diff[:4]})"
+        q14, e8 = O.a14_q17(ref.reshape(128, 32))
+        assert (asc[b] == e8).all(), f"seq {b}: E8M0 codes"
+        assert (aq[b] == O.pack_a14(q14)).all(), f"seq {b}: A14 words"
+    kv.close()
+
+
+def test_exact_refuses_positions_past_the_reference_bound(skv, ctx):
+    """The integer-compatibility entry keeps the reference's bound (position
+    ap_uint<12>, SWIFTKV_MAX_SEQ_LEN = 4096): a call with any position at or
+    past 4096 returns SWIFTKV_ERANGE and enqueues nothing -- the output and
+    activation buffers keep their bytes and no row is appended, not even for a
+    sequence whose position is in range -- on a cache and RoPE table that hold
+    those positions, where the FP32 step accepts them; in host-memory I/O mode
+    too.  Position 4095 is accepted."""
+    _note("case: exact entry refuses positions >= 4096")
+    n = 4160
+    lut = skv.RopeLut.generate(ctx, n)
+    kv = skv.KVCache(ctx, layers=1, max_batch=2, max_seq_len=n)
+    kv.zero()
+    q, k, v = (f32_normal(4400 + i, (2, 4096)) for i in range(3))
+    dq, dk, dv = ctx.to_device(q), ctx.to_device(k), ctx.to_device(v)
+    sentinel = [np.full(2 * 4096, 0x5A5A5A5A, np.uint32).view(np.int32), np.full(2 * 128 * 56, 0x5A, np.uint8),
+                np.full(2 * 128, 0x5A, np.uint8)]
+    out, aq, asc = (ctx.to_device(x) for x in sentinel)
+    for positions in ([100, 4096], [4096, 4096], [3, 4100], [n - 1, n - 1]):
+        with pytest.raises(skv.SwiftKVError) as ei:
+            skv.swiftkv_attention_exact(ctx, dq, dk, dv, kv, lut, aq, asc, 0, positions, out)
+        assert ei.value.code == skv.ERANGE and "4096" in str(ei.value), str(ei.value)
+    hout = sentinel[0].copy()
+    ctx.set_host_io(True)
+    try:
+        with pytest.raises(skv.SwiftKVError) as ei:
+            skv.swiftkv_attention_exact(ctx, q, k, v, kv, lut, None, None, 0, [4096, 7], hout)
+        assert ei.value.code == skv.ERANGE
+    finally:
+        ctx.set_host_io(False)
+    ctx.synchronize()
+    assert (hout == sentinel[0]).all()
+    assert (out.download(np.int32, (2 * 4096,)) == sentinel[0]).all()
+    assert (aq.download(np.uint8, (2 * 128 * 56,)) == sentinel[1]).all()
+    assert (asc.download(np.uint8, (2 * 128,)) == sentinel[2]).all()
+    for seq in (0, 1):
+        for h in range(H):
+            kc, vc, ks, vs = kv.read(seq, 0, h, 0, n)
+            assert not kc.any() and not vc.any() and not ks.any() and not vs.any(), f"seq {seq} head {h}"
+    # the bound is the entry's own: the FP32 step accepts the same positions
+    fout = ctx.alloc(2 * 4096 * 4)
+    skv.swiftkv_attention(ctx, dq, dk, dv, kv, lut, None, None, 0, [4096, n - 1], fout)
+    ctx.synchronize()
+    assert kv.read(0, 0, 0, 4096, 1)[0].any() and kv.read(1, 0, 0, n - 1, 1)[0].any()
+    # and the exact entry accepts the last position below it
+    skv.swiftkv_attention_exact(ctx, dq, dk, dv, kv, lut, aq, asc, 0, [4095, 100], out)
+    ctx.synchronize()
+    assert kv.read(0, 0, 0, 4095, 1)[0].any() and kv.read(1, 0, 0, 100, 1)[0].any()
+    for buf in (dq, dk, dv, out, aq, asc, fout):
+        buf.free()
+    kv.close()
+    lut.close()
 
 
 def test_exact_and_fast_path_agree(skv, ctx, lut4096, rope_tables):

@@ -148,3 +148,98 @@ def test_two_contexts_interleaved(skv, ctx):
         kv.close()
         lut.close()
     other.close()
+
+
+@pytest.mark.parametrize("batch,split,noalloc", [(1, 0, False), (4, 256, False), (2, 0, True)],
+                         ids=["batch1_8splits_inline_merge", "batch4_16splits_looped_merge", "batch2_noalloc"])
+def test_merge_that_gives_up_is_reported(skv, ctx, batch, split, noalloc):
+    """A split merge whose wait for another split's partial runs out writes NaN
+    into its head's output and must be reported, not pass as success.  The
+    testing aid forces it from the host (every merge waits for a tag no
+    partial carries and gives up after one poll; every kernel exits
+    normally), through the inline merge (up to 8 splits), the looped one (16
+    splits) and the allocation-free entry:
+      - every merged head's output is NaN and the next synchronize returns
+        EHIP naming a cache slot and head, once;
+      - a step call issued after a faulting launch has ended returns EHIP and
+        enqueues nothing;
+      - with the aid off, the next launch gives the bits of a launch before
+        the fault: the split workspace stayed consistent."""
+    position = 4095
+    _note(f"case: merge give-up reported, batch {batch}, split_tokens {split or 'heuristic'}, noalloc={noalloc}")
+    lut = skv.RopeLut.generate(ctx, 4096)
+    kv = skv.KVCache(ctx, layers=1, max_batch=batch, max_seq_len=position + 1)
+    kv.fill_synthetic(lut, ntok=position, seed=990 + batch)
+    qkv = [ctx.alloc(batch * 4096 * 4) for _ in range(3)]
+    for i, b in enumerate(qkv):
+        ctx.fill_synthetic(b, batch * 4096, 991 + batch, 50 + i)
+    out, aq, asc = ctx.alloc(batch * 4096 * 4), ctx.alloc(batch * 128 * 56), ctx.alloc(batch * 128)
+    run = skv.swiftkv_attention_noalloc if noalloc else skv.swiftkv_attention
+    positions = np.full(batch, position, np.int32)
+
+    def enqueue():
+        run(ctx, qkv[0], qkv[1], qkv[2], kv, lut, aq, asc, 0, positions, out)
+
+    def result():
+        return (out.download(np.uint32, (batch * 4096,)), aq.download(np.uint8, (batch * 128 * 56,)),
+                asc.download(np.uint8, (batch * 128,)))
+
+    ctx.set_split_tokens(split)
+    try:
+        enqueue()
+        ctx.synchronize()
+        good = result()
+        assert np.isfinite(good[0].view(np.float32)).all()
+        ctx.debug_force_merge_timeout(True)
+        enqueue()
+        with pytest.raises(skv.SwiftKVError) as ei:
+            ctx.synchronize()
+        assert ei.value.code == skv.EHIP and "gave up" in str(ei.value) and "head" in str(ei.value), str(ei.value)
+        assert np.isnan(result()[0].view(np.float32)).all()
+        ctx.synchronize()                      # reported once
+        # a faulting launch that has ended, then a step call: refused, nothing enqueued
+        enqueue()
+        ctx.timer_record(60)
+        ctx.timer_elapsed_ms(60, 60)           # waits for the launch without looking for faults
+        sentinel = np.full(batch * 4096, 0x5A5A5A5A, np.uint32)
+        out.upload(sentinel)
+        with pytest.raises(skv.SwiftKVError) as ei:
+            enqueue()
+        assert ei.value.code == skv.EHIP
+        ctx.synchronize()
+        assert np.array_equal(out.download(np.uint32, (batch * 4096,)), sentinel)
+        ctx.debug_force_merge_timeout(False)
+        enqueue()
+        ctx.synchronize()
+        again = result()
+        assert all(np.array_equal(g, f) for g, f in zip(again, good)), "the launch after the fault differs"
+        if not noalloc and split == 0:
+            # a recorded graph whose merges give up: its replay is reported, and so
+            # is a graph launch after a faulting replay has ended
+            ctx.debug_force_merge_timeout(True)
+            ctx.capture_begin()
+            enqueue()
+            g = ctx.capture_end()
+            ctx.debug_force_merge_timeout(False)
+            g.launch()
+            with pytest.raises(skv.SwiftKVError) as ei:
+                ctx.synchronize()
+            assert ei.value.code == skv.EHIP
+            g.launch()
+            ctx.timer_record(61)
+            ctx.timer_elapsed_ms(61, 61)
+            with pytest.raises(skv.SwiftKVError) as ei:
+                g.launch()
+            assert ei.value.code == skv.EHIP
+            ctx.synchronize()
+            g.close()
+            enqueue()
+            ctx.synchronize()
+            assert all(np.array_equal(g_, f) for g_, f in zip(result(), good)), "the launch after the graph differs"
+    finally:
+        ctx.debug_force_merge_timeout(False)
+        ctx.set_split_tokens(0)
+    for b in qkv + [out, aq, asc]:
+        b.free()
+    kv.close()
+    lut.close()

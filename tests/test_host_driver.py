@@ -24,6 +24,8 @@ def test_help_and_argument_errors():
                         (["--steps", "x"], "--steps x"), (["--frobnicate"], "unknown option"),
                         (["--decode", "--graph"], "cannot advance"), (["--host-io", "--graph"], "cannot be recorded"),
                         (["--context", "32768", "--decode", "--steps", "2"], "beyond the cache limit"),
+                        (["--exact", "--context", "4097"], "--exact keeps the reference's bound"),
+                        (["--exact", "--context", "4096", "--decode", "--steps", "2"], "positions below 4096"),
                         (["--theta", "0.5"], "--theta"), (["--parts", "3"], "--parts must be"),
                         (["--parts", "4", "--q17"], "excludes --q17")):
         r = run(*bad)
