@@ -68,6 +68,7 @@ _SIGNATURES = {
     "swiftkv_set_split_tokens": (C.c_int, [_vp, _i32]),
     "swiftkv_debug_set_split_generation": (C.c_int, [_vp, C.c_uint32, _i32]),
     "swiftkv_debug_force_merge_timeout": (C.c_int, [_vp, _i32]),
+    "swiftkv_debug_set_step_shape": (C.c_int, [_vp, _i32, _i32]),
     "swiftkv_debug_step_plan": (C.c_int, [_i32, _i32, _i32, _vp, _i32, _vp, _vp, _vp, _vp]),
     "swiftkv_rope_lut_load": (C.c_int, [_vp, _vp, _sz, C.POINTER(_vp)]),
     "swiftkv_rope_lut_generate": (C.c_int, [_vp, _i32, C.c_double, C.POINTER(_vp)]),
@@ -234,6 +235,12 @@ class Context:
         launches gives up after one poll (NaN in the merged heads' outputs,
         SwiftKVError EHIP from the next synchronize, step or graph launch)."""
         _check(lib().swiftkv_debug_force_merge_timeout(self.handle, 1 if enable else 0))
+
+    def debug_set_step_shape(self, waves: int = 0, block_tokens: int = 0) -> None:
+        """Testing aid: force the step kernel's shape (waves per workgroup,
+        tokens per block: (4, 64) or (8, 32)) for later step launches;
+        waves = 0 returns to the launch plan's choice."""
+        _check(lib().swiftkv_debug_set_step_shape(self.handle, int(waves), int(block_tokens)))
 
     def set_host_io(self, enable: bool) -> None:
         """Host-memory I/O: step and append tensors are numpy arrays, staged

@@ -30,6 +30,11 @@ HIP_FLAGS = [
     "-shared",
     "-Wall",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # Atomics with a returned value stay single-lane operations whose result
+    # is waited for where it is used: the optimizer's wave-wide expansion
+    # broadcasts the result at once, so the issuing wave would stall on the
+    # round trip (the balanced scan's unit claims, the split arrival count).
+    "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
 ]
 SOURCES = ["swiftkv_kernels.hip", "swiftkv_synth.hip", "swiftkv_exact.hip", "swiftkv_capi.cpp"]
 HOST_SRC = os.path.join(PKG_DIR, "host", "swiftkv_host.cpp")

@@ -96,6 +96,7 @@ struct swiftkv_context {
     int step_per_cu = 3;        // 4-wave step workgroups one CU holds at once
     hipStream_t stream = nullptr;
     int32_t split_tokens = 0;   // 0: heuristic
+    StepShape forced_shape{0, 0};   // testing aid: waves 0 = the launch plan's shape
     // split-context workspace: [partial_rows][32] arrival words (kArrivalStride
     // apart), then [partial_rows][32][partial_slots][kSlotWords] tagged words,
     // zero-filled when allocated (generation 0; tag 0 is never current)
@@ -332,7 +333,7 @@ int upload_lut(swiftkv_context* ctx, std::vector<int2>&& host, int32_t positions
 }
 
 // Tokens per split.  A launch runs best when it fills one residency round:
-// one 16-wave workgroup per CU (step_shape picks 16 waves for such launches),
+// one 8-wave workgroup per CU (step_shape picks 8 waves for such launches),
 // or step_per_cu 4-wave workgroups per CU.  So
 //   batch x 32 heads <= CUs:  splits = CUs / heads (at most 8);
 //   otherwise:                splits = step_per_cu x CUs / heads (at least 1),
@@ -360,8 +361,11 @@ struct SplitPolicy {
     int32_t cus;
     int32_t step_per_cu;
     int32_t split_tokens;
+    StepShape forced_shape;   // waves 0: the heuristic's
 };
-SplitPolicy policy_of(const swiftkv_context* ctx) { return {ctx->cus, ctx->step_per_cu, ctx->split_tokens}; }
+SplitPolicy policy_of(const swiftkv_context* ctx) {
+    return {ctx->cus, ctx->step_per_cu, ctx->split_tokens, ctx->forced_shape};
+}
 
 int32_t choose_split(const SplitPolicy& pol, const int32_t* positions, int32_t batch) {
     if (pol.split_tokens > 0) return pol.split_tokens;
@@ -377,17 +381,19 @@ int32_t choose_split(const SplitPolicy& pol, const int32_t* positions, int32_t b
     return static_cast<int32_t>(std::min<int64_t>(quanta * kSplitQuantum, kMaxSeq));
 }
 
-// Launch shape.  A launch of at most one workgroup per CU whose
-// splits are whole multiples of 512 tokens runs 16 waves per workgroup on
-// 32-token blocks: four waves share a SIMD and each holds half a block, so
-// less math is left when the last data arrives (32 layers at context 4096:
-// batch 2 17.1 against 17.6 us/layer with 8 waves on 64-token blocks,
-// batch 8 50.6 against 51.0; batch 1 unchanged).  Larger launches fill the
-// machine either way and keep 4 waves, so more workgroups stay resident per CU.
-StepShape step_shape(const SplitPolicy& pol, int32_t grid_splits, int32_t batch, int32_t split_tokens) {
+// Launch shape.  A launch of at most one workgroup per CU runs 8 waves per
+// workgroup on 32-token blocks; larger launches run 4 waves on 64-token
+// blocks, so three workgroups stay resident per CU and overlap each other's
+// prologues.  32 layers, us/layer, in one process (8 waves on 32-token blocks
+// against the 16 waves on 32-token blocks and the 4 waves on 64-token blocks
+// used before): batch 1 at context 4096 10.75 against 11.25; batch 2 16.16
+// against 16.45; batch 4 26.85 against 27.55; batch 8 47.65 against 48.5;
+// batch 1 at context 2048 (256-token splits) 8.47 against 8.76.  At batch 16
+// and 64 every shape measured within 1%.
+StepShape step_shape(const SplitPolicy& pol, int32_t grid_splits, int32_t batch) {
+    if (pol.forced_shape.waves != 0) return pol.forced_shape;
     const int64_t workgroups = static_cast<int64_t>(grid_splits) * kHeads * batch;
-    const bool wide = workgroups <= pol.cus && split_tokens % kWideRoundTokens == 0;
-    return wide ? kWideShape : kNarrowShape;
+    return workgroups <= pol.cus ? kWideShape : kNarrowShape;
 }
 
 // Dispatch rows of one launch: (position, sequence) longest first, equal
@@ -541,7 +547,7 @@ int run_step(swiftkv_context* ctx, const void* q, const void* k, const void* v, 
         a.fault = ctx->fault_dev;
 
         ProfilePair* p = profile_begin(ctx, SWIFTKV_KERNEL_STEP);
-        SKV_HIP(launch_step(a, grid_splits, step_shape(policy_of(ctx), grid_splits, nb, a.split_tokens), in.format,
+        SKV_HIP(launch_step(a, grid_splits, step_shape(policy_of(ctx), grid_splits, nb), in.format,
                             ctx->stream));
         profile_end(ctx, p);
     }
@@ -777,6 +783,16 @@ int swiftkv_set_split_tokens(swiftkv_context* ctx, int32_t split_tokens) {
     return ok();
 }
 
+int swiftkv_debug_set_step_shape(swiftkv_context* ctx, int32_t waves, int32_t block_tokens) {
+    if (!ctx) return fail(SWIFTKV_EINVAL, "null context");
+    const StepShape shape{waves, block_tokens};
+    if (waves != 0 && !step_shape_compiled(shape))
+        return fail(SWIFTKV_EINVAL, "no step kernel is compiled for %d waves on %d-token blocks", waves,
+                    block_tokens);
+    ctx->forced_shape = waves != 0 ? shape : StepShape{0, 0};
+    return ok();
+}
+
 int swiftkv_debug_step_plan(int32_t cus, int32_t workgroups_per_cu, int32_t split_tokens, const int32_t* positions,
                             int32_t batch, int32_t* out_split_tokens, int32_t* out_grid_splits, int32_t* out_waves,
                             int32_t* out_rows) {
@@ -796,13 +812,13 @@ int swiftkv_debug_step_plan(int32_t cus, int32_t workgroups_per_cu, int32_t spli
             return fail(SWIFTKV_ERANGE, "position %d outside [0, %d)", positions[b], kMaxSeq);
         max_pos = std::max(max_pos, positions[b]);
     }
-    const SplitPolicy pol{cus, workgroups_per_cu, split_tokens};
+    const SplitPolicy pol{cus, workgroups_per_cu, split_tokens, StepShape{0, 0}};
     StepArgs a{};
     a.batch = batch;
     set_rows(a, positions);
     *out_split_tokens = choose_split(pol, positions, batch);
     *out_grid_splits = (max_pos + *out_split_tokens) / *out_split_tokens;
-    *out_waves = step_shape(pol, *out_grid_splits, batch, *out_split_tokens).waves;
+    *out_waves = step_shape(pol, *out_grid_splits, batch).waves;
     if (out_rows)
         for (int32_t z = 0; z < batch; ++z) out_rows[z] = static_cast<int32_t>(a.rows[z] & 0xffu);
     return ok();

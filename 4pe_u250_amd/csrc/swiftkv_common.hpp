@@ -28,14 +28,14 @@ constexpr int kA14WordBytes = 56;                // ap_uint<448>: 32 x 14-bit la
 // split_tokens tokens; each wave takes 64-token blocks round-robin.
 constexpr int kAttendWaves = 4;
 constexpr int kBlockTokens = 64;
-// Launches that fit one residency round of workgroups of one per CU, with
-// splits of a multiple of 512 tokens, use 16 waves on 32-token blocks: four
-// waves share a SIMD and each holds half a block, so less of the math is
-// left when the last data arrives (123 VGPRs, within the 128 that four
-// resident waves per SIMD allow).
-constexpr int kWideWaves = 16;
+// Launches of at most one workgroup per CU use 8 waves on 32-token blocks
+// (123 VGPRs): each wave holds half a block, so less math is left when the
+// last data arrives, and the CU keeps 8 waves' loads in flight (16 waves on
+// 32-token blocks, the same bytes per wave, measured slower: the CU then asks
+// for twice the data it can have in flight, and issues its waves' loads
+// oldest wave first, so its youngest waves start their scans last).
+constexpr int kWideWaves = 8;
 constexpr int kWideBlockTokens = 32;
-constexpr int kWideRoundTokens = kWideWaves * kWideBlockTokens;   // 512
 
 // A step launch's shape: waves per workgroup and tokens per block.
 struct StepShape {
@@ -45,6 +45,8 @@ struct StepShape {
 };
 constexpr StepShape kNarrowShape{kAttendWaves, kBlockTokens};
 constexpr StepShape kWideShape{kWideWaves, kWideBlockTokens};
+// Every shape the step kernel is compiled for, as X(waves, block_tokens).
+#define SWIFTKV_STEP_SHAPES(X) X(4, 64) X(8, 32)
 constexpr int kSplitQuantum = kAttendWaves * kBlockTokens;   // 256
 constexpr int kMaxSeq = 32768;                   // longest cache accepted (tokens per sequence)
 constexpr int kMaxSplits = kMaxSeq / kSplitQuantum;   // 128 partials per (sequence, head)
@@ -156,9 +158,9 @@ constexpr size_t kNoAllocPartialBytes =
 constexpr size_t kNoAllocScratchBytes = kNoAllocCounterBytes + kNoAllocPartialBytes;
 
 // Launchers (swiftkv_kernels.hip).
-// shape: kNarrowShape, or kWideShape when a.split_tokens is a multiple of
-// kWideRoundTokens.
+// shape: one of SWIFTKV_STEP_SHAPES (hipErrorInvalidValue otherwise).
 hipError_t launch_step(const StepArgs& a, int grid_splits, StepShape shape, InputFormat in, hipStream_t s);
+bool step_shape_compiled(StepShape shape);
 // Workgroups of the 4-wave step kernel one CU holds at once (0 on error).
 int step_workgroups_per_cu();
 hipError_t launch_append_bulk(const BulkArgs& a, bool q17, hipStream_t s);

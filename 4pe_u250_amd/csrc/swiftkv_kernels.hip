@@ -2,9 +2,9 @@
 // stage.
 //
 // step kernel (one launch per decode step and layer), grid (splits, 32 heads,
-// batch rows) of 4-wave workgroups on 64-token blocks (16 waves on 32-token
-// blocks when the launch has at most one workgroup per CU and
-// 512-token-multiple splits); workgroup (j, h, z) owns tokens
+// batch rows) of 4-wave workgroups on 64-token blocks (8 waves on 32-token
+// blocks when the launch has at most one workgroup per CU); workgroup
+// (j, h, z) owns tokens
 // [j*C, min((j+1)*C, position+1)) of head h of the sequence that row z names
 // (rows come longest first, so a ragged batch does not end on long heads):
 //   1. every lane loads its channel pair of the new row's q (and, in the one
@@ -18,7 +18,7 @@
 //      G32-quantizes the new K/V row, appends it to the cache, and forwards it
 //      into its own merge as one more partial -- the new token is written once
 //      and never read back (the reference does the same, hpp:37-41);
-//   3. the waves scan the cached tokens in 64-token (16 waves: 32-token)
+//   3. the waves scan the cached tokens in 64-token (8 waves: 32-token)
 //      blocks.  Lane = (chunk c = lane&7, row r = lane>>3): one nontemporal
 //      dwordx4 per lane reads a 16-channel chunk, so one wave instruction
 //      covers 8 full 128-B code rows.  K rows are dotted with the query limbs
@@ -444,83 +444,101 @@ __device__ __forceinline__ void report_merge_fault(uint32_t* fault, uint32_t cod
     __hip_atomic_store(fault, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
-// Log-sum-exp merge of a head's n split partials by the split `own`, which
-// holds its own (m, l, o) in registers; threads d < 128 get output channel d.
-// Up to kMergeInline splits every thread issues all of its reads at once --
-// each split's m and l (the same words in every lane) and its own channel of
-// each split's acc -- and needs no barrier.  More splits (only when a caller
-// forces small splits) take a second, looped pass with the statistics staged
+// Log-sum-exp merge of a head's n split partials; threads d < 128 get output
+// channel d.  Up to kMergeInline splits the merge is inline: every thread
+// reads all of its words at once -- each split's m and l (the same words in
+// every lane) and its own channel of each split's acc -- with no barrier, and
+// a split's own words stand in registers.  More splits (only when a caller
+// forces small splits) take a looped merge with the statistics staged
 // through LDS.  The terms are summed in split order whichever split merges,
 // so the result does not depend on the arrival order.
 constexpr int kMergeInline = 8;
 
-__device__ __forceinline__ float merge_partials(const uint64_t* slots, int n, int own, uint32_t tag, uint32_t polls,
-                                                float own_m, float own_l, float own_o, bool& gave_up) {
-    // Inline: called by waves 0-1 only.  Looped: by every wave (it stages the
-    // statistics through LDS behind a barrier); lanes past 127 read channel
-    // 127 and their result is unused.
+struct InlineWords {
+    uint64_t m[kMergeInline], l[kMergeInline], o[kMergeInline];
+};
+
+// First read of the other splits' words; the split's own words carry `tag`
+// (they are never read).  Threads past 127 read channel 127.
+__device__ __forceinline__ void fetch_inline(const uint64_t* slots, int n, int own, uint32_t tag, float own_m,
+                                             float own_l, float own_o, InlineWords& w) {
     const int d = min(static_cast<int>(threadIdx.x), kHeadDim - 1);
-    if (n <= kMergeInline) {
-        // Own words count as current (tag | own bits): they are never read.
-        const uint64_t own_tag = static_cast<uint64_t>(tag) << 32;
-        uint64_t wm[kMergeInline], wl[kMergeInline], wo[kMergeInline];
+    const uint64_t own_tag = static_cast<uint64_t>(tag) << 32;
 #pragma unroll
-        for (int j = 0; j < kMergeInline; ++j) {
-            wm[j] = own_tag | __float_as_uint(own_m);
-            wl[j] = own_tag | __float_as_uint(own_l);
-            wo[j] = own_tag | __float_as_uint(own_o);
-            if (j < n && j != own) {
-                const uint64_t* sl = slots + j * kSlotWords;
-                wm[j] = fetch_word(sl);
-                wl[j] = fetch_word(sl + 1);
-                wo[j] = fetch_word(sl + 2 + d);
-            }
+    for (int j = 0; j < kMergeInline; ++j) {
+        w.m[j] = own_tag | __float_as_uint(own_m);
+        w.l[j] = own_tag | __float_as_uint(own_l);
+        w.o[j] = own_tag | __float_as_uint(own_o);
+        if (j < n && j != own) {
+            const uint64_t* sl = slots + j * kSlotWords;
+            w.m[j] = fetch_word(sl);
+            w.l[j] = fetch_word(sl + 1);
+            w.o[j] = fetch_word(sl + 2 + d);
         }
-        // Words whose store had not landed yet are read again, all of them in
-        // one round trip per round.
-        for (uint32_t spin = 0;; ++spin) {
-            bool stale = false;
-#pragma unroll
-            for (int j = 0; j < kMergeInline; ++j)
-                stale |= !current(wm[j], tag) || !current(wl[j], tag) || !current(wo[j], tag);
-            if (!stale) break;
-            if (spin == polls) {
-#pragma unroll
-                for (int j = 0; j < kMergeInline; ++j) wo[j] = own_tag | 0x7fc00000u;   // NaN shows in the output
-                gave_up = true;
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-#pragma unroll
-            for (int j = 0; j < kMergeInline; ++j) {
-                const uint64_t* sl = slots + j * kSlotWords;
-                if (!current(wm[j], tag)) wm[j] = fetch_word(sl);
-                if (!current(wl[j], tag)) wl[j] = fetch_word(sl + 1);
-                if (!current(wo[j], tag)) wo[j] = fetch_word(sl + 2 + d);
-            }
-        }
-        float m[kMergeInline], l[kMergeInline], o[kMergeInline];
-#pragma unroll
-        for (int j = 0; j < kMergeInline; ++j) {
-            m[j] = __uint_as_float(static_cast<uint32_t>(wm[j]));
-            l[j] = __uint_as_float(static_cast<uint32_t>(wl[j]));
-            o[j] = __uint_as_float(static_cast<uint32_t>(wo[j]));
-        }
-        float mx = m[0];
-#pragma unroll
-        for (int j = 1; j < kMergeInline; ++j)
-            if (j < n) mx = fmaxf(mx, m[j]);
-        float den = 0.0f, num = 0.0f;
-#pragma unroll
-        for (int j = 0; j < kMergeInline; ++j) {
-            if (j < n) {
-                const float w = fast_exp2(m[j] - mx);
-                den += w * l[j];
-                num += w * o[j];
-            }
-        }
-        return num / den;
     }
+}
+
+__device__ __forceinline__ bool inline_stale(const InlineWords& w, uint32_t tag) {
+    bool stale = false;
+#pragma unroll
+    for (int j = 0; j < kMergeInline; ++j) stale |= !current(w.m[j], tag) || !current(w.l[j], tag) || !current(w.o[j], tag);
+    return stale;
+}
+
+// Inline merge of words first read by fetch_inline: words whose store had not
+// landed yet are read again, all of them in one round trip per round, for at
+// most `polls` rounds.
+__device__ __forceinline__ float merge_inline(const uint64_t* slots, int n, uint32_t tag, uint32_t polls,
+                                              InlineWords& w, bool& gave_up) {
+    const int d = min(static_cast<int>(threadIdx.x), kHeadDim - 1);
+    for (uint32_t spin = 0;; ++spin) {
+        if (!inline_stale(w, tag)) break;
+        if (spin == polls) {
+            const uint64_t nan_word = (static_cast<uint64_t>(tag) << 32) | 0x7fc00000u;   // NaN shows in the output
+#pragma unroll
+            for (int j = 0; j < kMergeInline; ++j) w.o[j] = nan_word;
+            gave_up = true;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int j = 0; j < kMergeInline; ++j) {
+            const uint64_t* sl = slots + j * kSlotWords;
+            if (!current(w.m[j], tag)) w.m[j] = fetch_word(sl);
+            if (!current(w.l[j], tag)) w.l[j] = fetch_word(sl + 1);
+            if (!current(w.o[j], tag)) w.o[j] = fetch_word(sl + 2 + d);
+        }
+    }
+    float m[kMergeInline], l[kMergeInline], o[kMergeInline];
+#pragma unroll
+    for (int j = 0; j < kMergeInline; ++j) {
+        m[j] = __uint_as_float(static_cast<uint32_t>(w.m[j]));
+        l[j] = __uint_as_float(static_cast<uint32_t>(w.l[j]));
+        o[j] = __uint_as_float(static_cast<uint32_t>(w.o[j]));
+    }
+    float mx = m[0];
+#pragma unroll
+    for (int j = 1; j < kMergeInline; ++j)
+        if (j < n) mx = fmaxf(mx, m[j]);
+    float den = 0.0f, num = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kMergeInline; ++j) {
+        if (j < n) {
+            const float wt = fast_exp2(m[j] - mx);
+            den += wt * l[j];
+            num += wt * o[j];
+        }
+    }
+    return num / den;
+}
+
+// Looped merge of n > kMergeInline partials by the split `own` (its (m, l, o)
+// in registers), called by every wave: it stages the statistics through LDS
+// behind a barrier.  Lanes past 127 read channel 127 and their result is
+// unused.  One poll budget serves every word the thread waits for.
+__device__ __forceinline__ float merge_looped(const uint64_t* slots, int n, int own, uint32_t tag, uint32_t polls,
+                                              float own_m, float own_l, float own_o, bool& gave_up) {
+    const int d = min(static_cast<int>(threadIdx.x), kHeadDim - 1);
     __shared__ float s_m[kMaxSplits], s_l[kMaxSplits];
     const int t = threadIdx.x;
     uint32_t budget = polls;
@@ -535,9 +553,9 @@ __device__ __forceinline__ float merge_partials(const uint64_t* slots, int n, in
     float den = 0.0f, num = 0.0f;
     for (int j = 0; j < n; ++j) {
         const uint64_t* sl = slots + j * kSlotWords + 2 + d;
-        const float w = fast_exp2(s_m[j] - mx);
-        den += w * s_l[j];
-        num += w * (j == own ? own_o : tagged_value(sl, fetch_word(sl), tag, budget, gave_up));
+        const float wt = fast_exp2(s_m[j] - mx);
+        den += wt * s_l[j];
+        num += wt * (j == own ? own_o : tagged_value(sl, fetch_word(sl), tag, budget, gave_up));
     }
     return num / den;
 }
@@ -662,10 +680,10 @@ __global__ __launch_bounds__(WAVES * 64) void step_kernel(StepArgs a) {
     __syncthreads();
     SKV_STAMP(2);
 
-    const int nparts = owner ? WAVES + 1 : WAVES;
     const int d = threadIdx.x;
     float o = 0.0f, l = 0.0f, mx = -INFINITY;
     if (d < kHeadDim) {
+        const int nparts = owner ? WAVES + 1 : WAVES;
         mx = s_m[0];
         for (int w = 1; w < nparts; ++w) mx = fmaxf(mx, s_m[w]);
         for (int w = 0; w < nparts; ++w) {
@@ -683,7 +701,13 @@ __global__ __launch_bounds__(WAVES * 64) void step_kernel(StepArgs a) {
 
     // Several splits: count this split's arrival, publish its partial as
     // tagged words without waiting for them to land, and let the split that
-    // arrives last merge the head's partials and finish the head.
+    // arrives last merge the head's partials and finish the head.  (Reading
+    // the other splits' words in the same round trip as the count, so that a
+    // split finding them all current could merge at once, measured 0.9-1.0 us
+    // slower at batch 1: every split then reads every other split's words at
+    // device scope, about 2.7 MB in one burst as the stream ends, and the
+    // splits of a head finish together, so the last one still finds some
+    // words stale.)
     // Both halves of the word stay in their registers until here: with the
     // low half dead early, the compiler reused its register in the prologue,
     // and a write to a register that a load is still filling waits for every
@@ -691,6 +715,7 @@ __global__ __launch_bounds__(WAVES * 64) void step_kernel(StepArgs a) {
     asm volatile("" ::"v"(arrival_word));
     const uint32_t tag = static_cast<uint32_t>(arrival_word >> 32) + 1u;
     uint64_t* slots = a.partials + head_row * static_cast<size_t>(a.slot_stride) * kSlotWords;
+    const bool inline_merge = nsplit <= kMergeInline;
     // The count goes out from thread 128, in a wave that publishes nothing,
     // so waiting for its result never waits for the stores of waves 0-1.
     constexpr unsigned kCountThread = kHeadDim;
@@ -713,15 +738,22 @@ __global__ __launch_bounds__(WAVES * 64) void step_kernel(StepArgs a) {
     // looped merge of more than kMergeInline splits needs every wave at its barrier.
     SKV_STAMP(3);
     SKV_STAMP_FLAG(2);
-    if (!s_last || (nsplit <= kMergeInline && d >= kHeadDim)) {
+    if (!s_last || (inline_merge && d >= kHeadDim)) {
         SKV_STAMP_FLUSH();
         return;
     }
-    // The merger waits for words tagged `tag` (a testing aid can make it wait
+    // The merger waits for words tagged `want` (a testing aid can make it wait
     // for a tag no word carries, so that the wait gives up).
+    const uint32_t want = tag + a.merge_tag_skew;
     bool gave_up = false;
-    const float merged = merge_partials(slots, nsplit, split, tag + a.merge_tag_skew, a.merge_polls, mx, l, o,
-                                        gave_up);
+    float merged;
+    if (inline_merge) {
+        InlineWords w;
+        fetch_inline(slots, nsplit, split, want, mx, l, o, w);
+        merged = merge_inline(slots, nsplit, want, a.merge_polls, w, gave_up);
+    } else {
+        merged = merge_looped(slots, nsplit, split, want, a.merge_polls, mx, l, o, gave_up);
+    }
     SKV_STAMP(4);
     if (gave_up) report_merge_fault(a.fault, static_cast<uint32_t>(a.slot0 + b) * kHeads + h + 1u);
     if (d >= kHeadDim) return;
@@ -1019,10 +1051,19 @@ int step_workgroups_per_cu() {
 
 hipError_t launch_step(const StepArgs& a, int grid_splits, StepShape shape, InputFormat in, hipStream_t s) {
     const dim3 grid(grid_splits, kHeads, a.batch);
-    if (shape == kNarrowShape) return launch_step_shape<kAttendWaves, kBlockTokens>(a, grid, in, s);
-    if (shape == kWideShape && a.split_tokens % kWideRoundTokens == 0)
-        return launch_step_shape<kWideWaves, kWideBlockTokens>(a, grid, in, s);
+#define SKV_LAUNCH_SHAPE(W, B) \
+    if (shape == StepShape{W, B}) return launch_step_shape<W, B>(a, grid, in, s);
+    SWIFTKV_STEP_SHAPES(SKV_LAUNCH_SHAPE)
+#undef SKV_LAUNCH_SHAPE
     return hipErrorInvalidValue;
+}
+
+bool step_shape_compiled(StepShape shape) {
+#define SKV_IS_SHAPE(W, B) \
+    if (shape == StepShape{W, B}) return true;
+    SWIFTKV_STEP_SHAPES(SKV_IS_SHAPE)
+#undef SKV_IS_SHAPE
+    return false;
 }
 
 hipError_t launch_append_bulk(const BulkArgs& a, bool q17, hipStream_t s) {

@@ -101,6 +101,14 @@ int swiftkv_synchronize(swiftkv_context* ctx);
 /* Tokens per split-context work item; 0 selects the built-in heuristic.
  * Must be 0 or a multiple of 256 in [256, 32768]. */
 int swiftkv_set_split_tokens(swiftkv_context* ctx, int32_t split_tokens);
+/* Testing aid with no counterpart in the reference: every later step launch
+ * of the context runs the step kernel of `waves` waves per workgroup on
+ * `block_tokens`-token blocks instead of the shape the launch plan picks;
+ * waves = 0 returns to the plan's choice.  The compiled shapes (waves,
+ * block_tokens) are (4, 64) and (8, 32); any other is refused
+ * (SWIFTKV_EINVAL).  Both compute the same function: tests force each one on
+ * every kind of launch. */
+int swiftkv_debug_set_step_shape(swiftkv_context* ctx, int32_t waves, int32_t block_tokens);
 /* Testing aid with no counterpart in the reference, host-only (no device or
  * context needed): the launch plan the step entries use for one launch of
  * batch <= 256 sequences at positions[batch], on a device of `cus` compute
@@ -108,10 +116,9 @@ int swiftkv_set_split_tokens(swiftkv_context* ctx, int32_t split_tokens);
  * takes both from the device), with split_tokens as swiftkv_set_split_tokens
  * sets it (0: the built-in heuristic).  Writes the tokens per split, the
  * splits of the longest sequence (the grid's split dimension), the waves per
- * workgroup (4, or 16 for launches of at most one workgroup per CU whose
- * splits are a multiple of 512 tokens) and, when out_rows is not null, the
- * sequence served by each grid row (longest first, equal positions in
- * sequence order). */
+ * workgroup (4, or 8 for launches of at most one workgroup per CU) and, when
+ * out_rows is not null, the sequence served by each grid row (longest first,
+ * equal positions in sequence order). */
 int swiftkv_debug_step_plan(int32_t cus, int32_t workgroups_per_cu, int32_t split_tokens, const int32_t* positions,
                             int32_t batch, int32_t* out_split_tokens, int32_t* out_grid_splits, int32_t* out_waves,
                             int32_t* out_rows);

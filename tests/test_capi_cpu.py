@@ -147,17 +147,18 @@ def test_host_arrays_need_host_io_mode(skv):
 
 
 @pytest.mark.parametrize("positions,split,want", [
-    ([4095], 0, (512, 8, 16)),                 # batch 1: 8 splits, one 16-wave workgroup per CU
-    ([4095] * 2, 0, (1024, 4, 16)),
-    ([4095] * 4, 0, (2048, 2, 16)),
-    ([4095] * 8, 0, (4096, 1, 16)),            # 256 workgroups: no split
+    ([4095], 0, (512, 8, 8)),                  # batch 1: 8 splits, one 8-wave workgroup per CU
+    ([2047], 0, (256, 8, 8)),                  # batch 1 at context 2048: 256-token splits
+    ([4095] * 2, 0, (1024, 4, 8)),
+    ([4095] * 4, 0, (2048, 2, 8)),
+    ([4095] * 8, 0, (4096, 1, 8)),             # 256 workgroups: no split
     ([4095] * 16, 0, (4096, 1, 4)),            # more than one workgroup per CU: 4 waves
     ([4095] * 64, 0, (4096, 1, 4)),            # the headline launch
     ([32767] * 16, 0, (8192, 4, 4)),           # no split longer than 8192 tokens
-    ([100, 700, 2047], 0, (1024, 2, 16)),
-    ([5, 100, 100, 3], 0, (256, 1, 4)),        # 256-token split: not a multiple of 512
+    ([100, 700, 2047], 0, (1024, 2, 8)),
+    ([5, 100, 100, 3], 0, (256, 1, 8)),
     ([4095] * 4, 256, (256, 16, 4)),           # forced splits
-    ([4095], 1536, (1536, 3, 16)),
+    ([4095], 1536, (1536, 3, 8)),
     ([4095] * 12, 512, (512, 8, 4)),           # 3,072 workgroups
 ])
 def test_step_plan(skv, positions, split, want):
@@ -185,7 +186,7 @@ def test_step_plan_argument_checks(skv):
         return L.swiftkv_debug_step_plan(cus, per_cu, split, positions, batch, C.byref(out[0]), C.byref(out[1]),
                                          C.byref(out[2]), None)
 
-    assert plan() == skv.OK and (out[0].value, out[1].value, out[2].value) == (256, 1, 4)
+    assert plan() == skv.OK and (out[0].value, out[1].value, out[2].value) == (256, 1, 8)
     assert plan(positions=None) == skv.EINVAL
     assert plan(cus=0) == skv.EINVAL
     assert plan(per_cu=0) == skv.EINVAL

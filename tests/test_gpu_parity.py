@@ -28,13 +28,16 @@ def lut4096(skv, ctx):
 
 
 def _scenario(skv, ctx, lut, rope_tables, positions, seed, layers=1, layer=0, cap=None, dist="normal",
-              outliers=None, split=0, q17=False):
-    """Prefill each sequence's history, run one step, compare everything."""
+              outliers=None, split=0, q17=False, shape=None):
+    """Prefill each sequence's history, run one step, compare everything.
+    shape: (waves, block_tokens) forced on the step kernel (None: the
+    launch plan's)."""
     cos, sin = rope_tables
     B = len(positions)
     cap = cap or (max(positions) + 1)
     kv = skv.KVCache(ctx, layers=layers, max_batch=B, max_seq_len=cap)
     ctx.set_split_tokens(split)
+    ctx.debug_set_step_shape(*(shape or (0, 0)))
     scs = []
     for b, p in enumerate(positions):
         kh, vh = history(seed + 10 * b, p, dist, outliers)
@@ -69,6 +72,7 @@ def _scenario(skv, ctx, lut, rope_tables, positions, seed, layers=1, layer=0, ca
         assert same_e.mean() > 0.95
         assert np.all(np.abs(q14.astype(np.int32) - q14r.astype(np.int32))[same_e] <= 1)
     ctx.set_split_tokens(0)
+    ctx.debug_set_step_shape(0, 0)
     kv.close()
     return max(errs)
 
@@ -81,7 +85,9 @@ def test_config1_batch1_position127(skv, ctx, lut4096, rope_tables):
 @pytest.mark.parametrize("split", [256, 4096])
 def test_batch_positions_edges(skv, ctx, lut4096, rope_tables, split):
     """Positions around block (64) and split (256) boundaries; with split 256
-    some heads finish in the step kernel and others go through the combine."""
+    some heads finish in the step kernel and others go through the combine.
+    Batch 8 at split 4096 is one workgroup per CU (8 waves on 32-token
+    blocks); at split 256 the launch has more (4 waves on 64-token blocks)."""
     _note(f"case: batch 8 positions [0,1,63,64,255,256,257,300], layer 1 of 3, split {split}")
     _scenario(skv, ctx, lut4096, rope_tables, [0, 1, 63, 64, 255, 256, 257, 300], seed=21, layers=3, layer=1,
               cap=320, split=split)
@@ -115,16 +121,15 @@ def test_randomized_configurations(skv, ctx, lut4096, rope_tables, case):
               dist=dist, outliers=outl, split=split, q17=q17)
 
 
-# Seeds whose shapes run the 16-wave launch (every one but 9501 and 9503,
+# Seeds whose shapes run the 8-wave launch (every one but 9501 and 9503,
 # which run 4-wave workgroups), with 1 to 8 splits per head.
 @pytest.mark.parametrize("seed", [9500, 9501, 9502, 9503, 9506, 9511, 9514, 9531])
 def test_randomized_small_batches(skv, ctx, lut4096, rope_tables, seed):
-    """Seeded random shapes for small launches (16 waves on 32-token blocks
-    when a launch has at most one workgroup per CU and its split is a
-    multiple of 512 tokens): batch 1..8, ragged positions up to 4095,
-    heuristic or forced split of 512 to 2048 tokens (or 768: 4 waves), FP32
-    or Q15.17 entry, N(0,1) or Student-t(3) data, with or without outlier
-    channels."""
+    """Seeded random shapes for small launches (8 waves on 32-token blocks
+    when a launch has at most one workgroup per CU, 4 waves on 64-token
+    blocks otherwise): batch 1..8, ragged positions up to 4095, heuristic or
+    forced split of 512 to 2048 tokens, FP32 or Q15.17 entry, N(0,1) or
+    Student-t(3) data, with or without outlier channels."""
     case = seed - 9500
     rng = np.random.default_rng(seed)
     B = int(rng.integers(1, 9))
@@ -137,6 +142,28 @@ def test_randomized_small_batches(skv, ctx, lut4096, rope_tables, seed):
           f"q17 {q17}")
     _scenario(skv, ctx, lut4096, rope_tables, positions, seed=9700 + 100 * case, dist=dist, outliers=outl,
               split=split, q17=q17)
+
+
+_EDGE_POSITIONS = [0, 1, 31, 32, 33, 63, 64, 65, 255, 256, 257, 300]
+
+
+@pytest.mark.parametrize("shape", [(4, 64), (8, 32)], ids=["4waves_64tok", "8waves_32tok"])
+@pytest.mark.parametrize("positions,split", [
+    ([4095], 0),                                        # 8 splits of 512 tokens, inline merge
+    ([2047], 0),                                        # 8 splits of 256 tokens
+    (_EDGE_POSITIONS, 256),                             # 32- and 64-token block and split edges
+    ([int(p) for p in np.random.default_rng(77).integers(0, 1200, 20)], 0),   # more workgroups than CUs
+    ([4095, 1000], 256),                                # 16 splits: looped merge
+], ids=["b1_pos4095", "b1_pos2047", "b12_edges_split256", "b20_ragged", "b2_16splits"])
+def test_forced_step_shapes(skv, ctx, lut4096, rope_tables, shape, positions, split):
+    """Each compiled shape of the step kernel (waves per workgroup, tokens per
+    block) forced on every kind of launch -- split heads (inline and looped
+    merges), unsplit heads, ranges ending on and next to block and split
+    edges, more workgroups than CUs -- against the oracle, whichever shape
+    the launch plan would pick."""
+    _note(f"case: forced shape {shape}, batch {len(positions)}, max position {max(positions)}, split {split}")
+    _scenario(skv, ctx, lut4096, rope_tables, positions, seed=8800 + len(positions), split=split, shape=shape,
+              dist="t3" if split else "normal")
 
 
 @pytest.mark.parametrize("split", [0, 256])
@@ -437,6 +464,10 @@ def test_error_codes(skv, ctx, lut4096):
     with pytest.raises(skv.SwiftKVError) as ei:
         ctx.set_split_tokens(300)
     assert ei.value.code == skv.EINVAL
+    for shape in ((16, 32), (8, 64), (4, 32), (-1, 64)):   # shapes no step kernel is compiled for
+        with pytest.raises(skv.SwiftKVError) as ei:
+            ctx.debug_set_step_shape(*shape)
+        assert ei.value.code == skv.EINVAL
     step()   # a valid call still works after the failures
     ctx.synchronize()
     small.close()
