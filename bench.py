@@ -50,6 +50,11 @@ STEP_SLOT0, STEP_SLOTS = 16, 48
 MIN_STEP_SAMPLES = 20
 METRIC = "decode-attn µs/layer + achieved HBM GB/s (% of peak), ctx 4096, batch 1/64"
 TOKEN_HEAD_BYTES = 288
+# Untimed warm-up of the main workload, in seconds, when its cache is large
+# (above SETTLE_MIN_BYTES): the stream runs slower for a second or more after
+# tens of GB have been allocated and filled (see Cache).
+SETTLE_S = 1.5
+SETTLE_MIN_BYTES = 8 << 30
 
 
 def step_bytes(position: int, parts: int = 1) -> int:
@@ -99,26 +104,50 @@ def profile_counters(vals):
     return {k: vals[k] for k in keys if k in vals} or None
 
 
-def run_gpu(skv, ctx, positions, layers, steps, warmup, seed, outliers=False, dist=0, exact_steps=0,
-            graph=True, advance=False, parts=0):
+class Cache:
+    """A KV cache and RoPE table filled on the device once, before any timed
+    region, and kept until the end of the run: a workload of `batch`
+    sequences uses slots 0 .. batch-1 and layers 0 .. layers-1.  Large
+    allocations and frees between timed workloads are avoided on purpose: on
+    MI355X the device streams about 4% slower for a second or more after
+    tens of GB are allocated or freed (batch 4: 26.9 us/layer settled, 28.1
+    right after a 77 GB cache was allocated and filled or freed, with no
+    attention kernel in between)."""
+
+    def __init__(self, skv, ctx, batch, layers, cap, seed, ntok=None, dist=0, outliers=False):
+        self.batch, self.layers, self.cap = batch, layers, cap
+        self.lut = skv.RopeLut.generate(ctx, max(cap, 4096))
+        self.kv = skv.KVCache(ctx, layers=layers, max_batch=batch, max_seq_len=cap)
+        t0 = time.time()
+        ntok = cap - 1 if ntok is None else ntok
+        self.kv.fill_synthetic(self.lut, ntok=ntok, seed=seed, dist=dist, k_outliers=outliers)
+        ctx.synchronize()
+        log(f"[bench] filled {self.kv.nbytes / 1e9:.1f} GB cache ({layers} layers x {batch} seq x {ntok} tokens) "
+            f"in {time.time() - t0:.1f} s")
+
+    def close(self):
+        self.kv.close()
+        self.lut.close()
+
+
+def run_gpu(skv, ctx, cache, positions, layers, steps, warmup, seed, outliers=False, dist=0, exact_steps=0,
+            graph=True, advance=False, parts=0, settle_s=0.0):
     """Time `steps` decode steps of `layers` calls each over sequences at `positions`.
 
-    The cache is filled on the device to max(positions) tokens per sequence;
-    q/k/v for every layer are resident before timing.  With advance=True step
-    s runs at positions + s (a decode run whose appends feed the next step);
-    otherwise every step repeats the same positions (the appended row is
-    rewritten with the same bits).
+    `cache` (a Cache) holds the sequences' rows up to max(positions) (its
+    fill); q/k/v for every layer are resident before timing (with outliers,
+    1% of k's channels scaled x20, as in the cache's own rows).  With
+    advance=True step s runs at positions + s (a decode run whose appends feed
+    the next step); otherwise every step repeats the same positions (the
+    appended row is rewritten with the same bits).  The untimed warm-up runs
+    `warmup` steps and, with settle_s, goes on until that much time has
+    passed.
     """
     positions = np.asarray(positions, np.int32)
     batch = positions.size
-    cap = int(positions.max()) + (steps if advance else 1)   # last written position + 1
-    lut = skv.RopeLut.generate(ctx, max(cap, 4096))
-    kv = skv.KVCache(ctx, layers=layers, max_batch=batch, max_seq_len=cap)
-    t0 = time.time()
-    kv.fill_synthetic(lut, ntok=int(positions.max()), seed=seed, dist=dist, k_outliers=outliers)
-    ctx.synchronize()
-    log(f"[bench] batch {batch}: filled {kv.nbytes / 1e9:.1f} GB cache ({layers} layers x {batch} seq x "
-        f"{int(positions.max())} tokens) in {time.time() - t0:.1f} s")
+    last = int(positions.max()) + (steps if advance else 1)   # last written position + 1
+    assert batch <= cache.batch and layers <= cache.layers and last <= cache.cap, "workload outside its cache"
+    kv, lut = cache.kv, cache.lut
     n_in = layers * batch * 4096
     qkv = [ctx.alloc(n_in * 4) for _ in range(3)]
     for i, buf in enumerate(qkv):
@@ -137,6 +166,10 @@ def run_gpu(skv, ctx, positions, layers, steps, warmup, seed, outliers=False, di
     for _ in range(0 if advance else warmup):
         one_step(positions)
     ctx.synchronize()
+    t_settle = time.time()
+    while not advance and time.time() - t_settle < settle_s:
+        one_step(positions)
+        ctx.synchronize()
     ctx.timer_record(0)
     for s in range(steps):
         one_step(positions + s if advance else positions)
@@ -230,8 +263,6 @@ def run_gpu(skv, ctx, positions, layers, steps, warmup, seed, outliers=False, di
                     "gbps": pbytes / (ms_parts / 1e3) / 1e9}
     for b in qkv + [out, aq, asc]:
         b.free()
-    kv.close()
-    lut.close()
     step_total = [sum(step_bytes(int(p) + (s if advance else 0)) for p in positions) for s in range(steps)]
     total_bytes = layers * sum(step_total)
     ms_step = ms / steps
@@ -291,6 +322,10 @@ def run_prefill(skv, ctx, tokens, layers, reps, seed, modes=("own", "shared")):
                 skv.swiftkv_append_tokens(ctx, ks[i], vs[i], kv, lut, layer, 0, 0, tokens)
         prompt()                              # warm-up pass
         ctx.synchronize()
+        t0 = time.time()                      # and untimed prompts while the fresh allocations settle (see Cache)
+        while time.time() - t0 < SETTLE_S:
+            prompt()
+            ctx.synchronize()
         ctx.timer_record(8)
         for _ in range(reps):
             prompt()
@@ -314,14 +349,12 @@ def run_prefill(skv, ctx, tokens, layers, reps, seed, modes=("own", "shared")):
     return res
 
 
-def run_host_io(skv, ctx, batch, context, reps, seed):
+def run_host_io(skv, ctx, cache, context, reps, seed):
     """The per-layer call with host-memory q/k/v/out/A14 (pageable numpy
-    arrays): copies in, step, copies out, wait -- the PCIe-inclusive rate."""
+    arrays): copies in, step, copies out, wait -- the PCIe-inclusive rate,
+    on layer 0 of every sequence of `cache`."""
     pos = context - 1
-    lut = skv.RopeLut.generate(ctx, max(context, 4096))
-    kv = skv.KVCache(ctx, layers=1, max_batch=batch, max_seq_len=context)
-    kv.fill_synthetic(lut, ntok=pos, seed=seed)
-    ctx.synchronize()
+    batch, kv, lut = cache.batch, cache.kv, cache.lut
     rng = np.random.default_rng(seed)
     q, k, v = (rng.standard_normal((batch, 4096)).astype(np.float32) for _ in range(3))
     out = np.empty((batch, 4096), np.float32)
@@ -337,8 +370,6 @@ def run_host_io(skv, ctx, batch, context, reps, seed):
                 times.append(time.perf_counter() - t0)
     finally:
         ctx.set_host_io(False)
-    kv.close()
-    lut.close()
     assert np.isfinite(out).all()
     t = float(np.median(times))
     return {"us_per_layer": round(t * 1e6, 1), "gbps": round(batch * step_bytes(pos) / t / 1e9, 1),
@@ -545,8 +576,18 @@ def main():
         main_positions = np.random.default_rng(4).integers(256, args.context + 1, args.batch) - 1
     else:
         main_positions = np.full(args.batch, args.context - 1)
-    main_res = run_gpu(skv, ctx, main_positions, args.layers, args.steps, args.warmup,
-                       seed=2026, exact_steps=args.exact_steps, parts=args.parts)
+    # Every cache of the run is allocated and filled here, before the first
+    # timed region, and freed at the end (see Cache).  The main cache also
+    # serves the secondary workloads of up to its batch and context.
+    main = Cache(skv, ctx, args.batch, args.layers, args.context, seed=2026, ntok=int(main_positions.max()))
+    b1_cache = (Cache(skv, ctx, 1, args.layers, args.context, seed=2027, outliers=True)
+                if not args.no_batch1 else None)
+    long_cache = (Cache(skv, ctx, 16, 1, 32768, seed=2031, ntok=32256, dist=skv.DIST_STUDENT_T3)
+                  if not args.no_configs else None)
+    main_res = run_gpu(skv, ctx, main, main_positions, args.layers, args.steps, args.warmup,
+                       seed=2026, exact_steps=args.exact_steps, parts=args.parts,
+                       settle_s=SETTLE_S if main.kv.nbytes + (long_cache.kv.nbytes if long_cache else 0) > SETTLE_MIN_BYTES
+                       else 0.0)
     log(f"[bench] batch {args.batch}: {main_res['us_per_layer']:.1f} us/layer, {main_res['gbps']:.0f} GB/s "
         f"(graph replay {main_res['graph']['us_per_layer']:.1f} us/layer)")
     if main_res["partials"]:
@@ -556,45 +597,54 @@ def main():
     extra = {}
     if not args.no_batch1:
         # batch-1 headline: 1% of K channels x20
-        b1 = run_gpu(skv, ctx, [args.context - 1], args.layers, max(args.steps, 20), args.warmup, seed=2027,
-                     outliers=True, parts=args.parts, exact_steps=min(args.exact_steps, 1) * 5)
+        b1 = run_gpu(skv, ctx, b1_cache, [args.context - 1], args.layers, max(args.steps, 20), args.warmup,
+                     seed=2027, outliers=True, parts=args.parts, exact_steps=min(args.exact_steps, 1) * 5)
         log(f"[bench] batch 1: {b1['us_per_layer']:.2f} us/layer, {b1['gbps']:.0f} GB/s "
             f"(graph replay {b1['graph']['us_per_layer']:.2f} us/layer)")
         if b1["partials"]:
             log(f"[bench] batch 1, {args.parts} split-K partials: {b1['partials']['us_per_layer']:.2f} us/layer")
     if not args.no_configs:
+        # The secondary workloads run on the main cache's slots 0 .. batch-1
+        # (every one fits its 64 sequences x 32 layers x 4096 tokens).
+        assert not args.ragged and args.batch >= 64 and args.layers >= 32 and args.context >= 4096, \
+            "the secondary workloads use the default main cache"
         # One launch per step: a graph of a single node would time hipGraphLaunch, not the kernel.
-        r = run_gpu(skv, ctx, [127], 1, 200, args.warmup, seed=2028, graph=False)
+        r = run_gpu(skv, ctx, main, [127], 1, 200, args.warmup, seed=2028, graph=False)
         extra["batch1_position127_1layer"] = summary(r, graph=False)
-        r = run_gpu(skv, ctx, [2047], 32, 20, args.warmup, seed=2029)
+        r = run_gpu(skv, ctx, main, [2047], 32, 20, args.warmup, seed=2029)
         extra["batch1_position2047_32layers"] = summary(r)
         # One layer repeated: its 37.8 MB stay resident in the 256 MB MALL, so
         # this is the cache-resident figure, reported apart from the sweep.
-        r = run_gpu(skv, ctx, [4095], 1, 200, args.warmup, seed=2033, graph=False)
+        r = run_gpu(skv, ctx, main, [4095], 1, 200, args.warmup, seed=2033, graph=False)
         extra["batch1_position4095_1layer_repeated_mall_resident"] = summary(r, graph=False)
         rng = np.random.default_rng(4)
         lengths = rng.integers(256, 4097, 64)
-        r = run_gpu(skv, ctx, lengths - 1, 32, args.steps, args.warmup, seed=2030)
+        r = run_gpu(skv, ctx, main, lengths - 1, 32, args.steps, args.warmup, seed=2030)
         extra["batch64_ragged_32layers"] = dict(summary(r), length_seed=4, sum_attended=r["sum_attended"],
                                                 lengths="U{256..4096}")
         # the same lengths, one layer timed on its own (its 1.3 GB exceeds the 256 MB MALL)
-        r = run_gpu(skv, ctx, lengths - 1, 1, 100, args.warmup, seed=2030, graph=False)
+        r = run_gpu(skv, ctx, main, lengths - 1, 1, 100, args.warmup, seed=2030, graph=False)
         extra["batch64_ragged_1layer"] = dict(summary(r, graph=False), length_seed=4, lengths="U{256..4096}")
         sweep = {}
         for b in (2, 4, 8, 16, 32):   # the batch sizes between the two headline ones, 32 layers at context 4096
-            r = run_gpu(skv, ctx, np.full(b, args.context - 1), 32, 5, 1, seed=2040 + b, graph=False)
+            r = run_gpu(skv, ctx, main, np.full(b, args.context - 1), 32, 5, 1, seed=2040 + b, graph=False)
             sweep[str(b)] = {"us_per_layer": round(r["us_per_layer"], 2), "gbps": round(r["gbps"], 1),
                              "pct_of_peak": round(r["pct_of_peak"], 2)}
         extra["batch_sweep_position4095_32layers"] = sweep
         log("[bench] batch sweep: " + ", ".join(f"{b}: {v['us_per_layer']:.1f} us" for b, v in sweep.items()))
-        r = run_gpu(skv, ctx, np.full(16, 32256), 1, 512, 0, seed=2031, dist=skv.DIST_STUDENT_T3, graph=False,
-                    advance=True)
+        r = run_gpu(skv, ctx, long_cache, np.full(16, 32256), 1, 512, 0, seed=2031, dist=skv.DIST_STUDENT_T3,
+                    graph=False, advance=True)
         extra["batch16_positions32256to32767_1layer_t3"] = dict(summary(r, graph=False),
                                                                  steps=512, ms_total=round(r["ms_per_step"] * 512, 2))
         for k, v in extra.items():
             if "us_per_layer" in v:
                 log(f"[bench] {k}: {v['us_per_layer']:.2f} us/layer, {v['gbps']:.0f} GB/s")
-        extra["batch64_position4095_host_io"] = run_host_io(skv, ctx, args.batch, args.context, 20, seed=2032)
+        extra["batch64_position4095_host_io"] = run_host_io(skv, ctx, main, args.context, 20, seed=2032)
+    for c in (main, b1_cache, long_cache):
+        if c is not None:
+            c.close()
+    if not args.no_configs:
+        # the prefill allocates its own cache and inputs, after the decode caches are freed
         extra["prefill_append_4096tokens_32layers"] = run_prefill(skv, ctx, 4096, 32, 5, seed=2034)
         log(f"[bench] prefill append, 4096 tokens: {extra['prefill_append_4096tokens_32layers']['us_per_layer']:.1f} "
             f"us/layer, {extra['prefill_append_4096tokens_32layers']['gbps']:.0f} GB/s")
