@@ -69,7 +69,7 @@ _SIGNATURES = {
     "swiftkv_debug_set_split_generation": (C.c_int, [_vp, C.c_uint32, _i32]),
     "swiftkv_debug_force_merge_timeout": (C.c_int, [_vp, _i32]),
     "swiftkv_debug_set_step_shape": (C.c_int, [_vp, _i32, _i32]),
-    "swiftkv_debug_step_plan": (C.c_int, [_i32, _i32, _i32, _vp, _i32, _vp, _vp, _vp, _vp]),
+    "swiftkv_debug_step_plan": (C.c_int, [_i32, _i32, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _vp]),
     "swiftkv_rope_lut_load": (C.c_int, [_vp, _vp, _sz, C.POINTER(_vp)]),
     "swiftkv_rope_lut_generate": (C.c_int, [_vp, _i32, C.c_double, C.POINTER(_vp)]),
     "swiftkv_rope_lut_destroy": (C.c_int, [_vp]),
@@ -238,7 +238,7 @@ class Context:
 
     def debug_set_step_shape(self, waves: int = 0, block_tokens: int = 0) -> None:
         """Testing aid: force the step kernel's shape (waves per workgroup,
-        tokens per block: (4, 64) or (8, 32)) for later step launches;
+        tokens per block: (4, 64), (8, 32) or (8, 64)) for later step launches;
         waves = 0 returns to the launch plan's choice."""
         _check(lib().swiftkv_debug_set_step_shape(self.handle, int(waves), int(block_tokens)))
 
@@ -489,14 +489,14 @@ NOALLOC_WORKSPACE_BYTES = 69206016   # 1 MiB of arrival words + 8 splits x 256 s
 def step_plan(positions, cus: int = 256, workgroups_per_cu: int = 3, split_tokens: int = 0):
     """The launch plan of one step launch (host-only, no device needed):
     (tokens per split, splits of the longest sequence, waves per workgroup,
-    sequence index per grid row)."""
+    tokens per block, sequence index per grid row)."""
     pos = np.ascontiguousarray(np.atleast_1d(np.asarray(positions, dtype=np.int32)))
-    split, grid, waves = C.c_int32(), C.c_int32(), C.c_int32()
+    split, grid, waves, block = C.c_int32(), C.c_int32(), C.c_int32(), C.c_int32()
     rows = np.zeros(pos.size, np.int32)
     _check(lib().swiftkv_debug_step_plan(int(cus), int(workgroups_per_cu), int(split_tokens), _host_ptr(pos),
                                          int(pos.size), C.byref(split), C.byref(grid), C.byref(waves),
-                                         _host_ptr(rows)))
-    return split.value, grid.value, waves.value, rows
+                                         C.byref(block), _host_ptr(rows)))
+    return split.value, grid.value, waves.value, block.value, rows
 
 
 def swiftkv_attention_noalloc(ctx: Context, q, k, v, kv_cache: KVCache, rope_lut: RopeLut,

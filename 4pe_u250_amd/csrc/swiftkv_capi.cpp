@@ -381,19 +381,27 @@ int32_t choose_split(const SplitPolicy& pol, const int32_t* positions, int32_t b
     return static_cast<int32_t>(std::min<int64_t>(quanta * kSplitQuantum, kMaxSeq));
 }
 
-// Launch shape.  A launch of at most one workgroup per CU runs 8 waves per
-// workgroup on 32-token blocks; larger launches run 4 waves on 64-token
-// blocks, so three workgroups stay resident per CU and overlap each other's
-// prologues.  32 layers, us/layer, in one process (8 waves on 32-token blocks
-// against the 16 waves on 32-token blocks and the 4 waves on 64-token blocks
-// used before): batch 1 at context 4096 10.75 against 11.25; batch 2 16.16
-// against 16.45; batch 4 26.85 against 27.55; batch 8 47.65 against 48.5;
-// batch 1 at context 2048 (256-token splits) 8.47 against 8.76.  At batch 16
-// and 64 every shape measured within 1%.
-StepShape step_shape(const SplitPolicy& pol, int32_t grid_splits, int32_t batch) {
+// Launch shape.  Up to one residency round of 4-wave workgroups (step_per_cu
+// per CU), a launch runs 8 waves per workgroup on 32-token blocks.  A larger
+// launch runs 8 waves on 64-token blocks, one workgroup per CU, when every
+// workgroup's range holds at least kLongRangeTokens (its shortest row's
+// length or the split, whichever is less); otherwise 4 waves on 64-token
+// blocks, three workgroups per CU overlapping each other's prologues.
+// 32 layers, us/layer, one process, interleaved rounds, against the 4-wave
+// shape: batch 1 to 8 at context 4096 10.75 / 16.16 / 26.85 / 47.65 against
+// 12.05 / 17.42 / 28.14 / 49.0 (and 11.25 / 16.45 / 27.55 / 48.5 with 16
+// waves on 32-token blocks); batch 1 at context 2048 8.47 against 8.76;
+// batch 12 (two splits) 72.6 against 73.55; batch 16 92.4 against 93.0;
+// with 8 waves on 64-token blocks batch 32 / 48 / 64 180.7 / 268.65 / 357.2
+// against 181.75 / 270.6 / 359.8, and batch 16 at context 32768 695.6
+// against 699.7 per layer; the ragged batch 64 (rows of 256 to 4096 tokens)
+// 216.35 with 4 waves against 216.8 with 8.
+StepShape step_shape(const SplitPolicy& pol, int32_t grid_splits, int32_t batch, int32_t split_tokens,
+                     int32_t min_len) {
     if (pol.forced_shape.waves != 0) return pol.forced_shape;
     const int64_t workgroups = static_cast<int64_t>(grid_splits) * kHeads * batch;
-    return workgroups <= pol.cus ? kWideShape : kNarrowShape;
+    if (workgroups <= static_cast<int64_t>(pol.cus) * pol.step_per_cu) return kWideShape;
+    return std::min(split_tokens, min_len) >= kLongRangeTokens ? kLongShape : kNarrowShape;
 }
 
 // Dispatch rows of one launch: (position, sequence) longest first, equal
@@ -518,8 +526,11 @@ int run_step(swiftkv_context* ctx, const void* q, const void* k, const void* v, 
         a.layer = layer;
         a.batch = nb;
         a.slot0 = b0;
-        int32_t max_pos = 0;
-        for (int32_t b = 0; b < nb; ++b) max_pos = std::max(max_pos, positions[b0 + b]);
+        int32_t max_pos = 0, min_pos = kMaxSeq;
+        for (int32_t b = 0; b < nb; ++b) {
+            max_pos = std::max(max_pos, positions[b0 + b]);
+            min_pos = std::min(min_pos, positions[b0 + b]);
+        }
         set_rows(a, positions + b0);
         a.split_tokens = choose_split(policy_of(ctx), positions + b0, nb);
         const int32_t grid_splits = (max_pos + 1 + a.split_tokens - 1) / a.split_tokens;
@@ -547,8 +558,8 @@ int run_step(swiftkv_context* ctx, const void* q, const void* k, const void* v, 
         a.fault = ctx->fault_dev;
 
         ProfilePair* p = profile_begin(ctx, SWIFTKV_KERNEL_STEP);
-        SKV_HIP(launch_step(a, grid_splits, step_shape(policy_of(ctx), grid_splits, nb), in.format,
-                            ctx->stream));
+        SKV_HIP(launch_step(a, grid_splits, step_shape(policy_of(ctx), grid_splits, nb, a.split_tokens, min_pos + 1),
+                            in.format, ctx->stream));
         profile_end(ctx, p);
     }
     return ok();
@@ -795,7 +806,7 @@ int swiftkv_debug_set_step_shape(swiftkv_context* ctx, int32_t waves, int32_t bl
 
 int swiftkv_debug_step_plan(int32_t cus, int32_t workgroups_per_cu, int32_t split_tokens, const int32_t* positions,
                             int32_t batch, int32_t* out_split_tokens, int32_t* out_grid_splits, int32_t* out_waves,
-                            int32_t* out_rows) {
+                            int32_t* out_block_tokens, int32_t* out_rows) {
     if (!positions || !out_split_tokens || !out_grid_splits || !out_waves)
         return fail(SWIFTKV_EINVAL, "null argument");
     if (cus < 1 || workgroups_per_cu < 1)
@@ -806,11 +817,12 @@ int swiftkv_debug_step_plan(int32_t cus, int32_t workgroups_per_cu, int32_t spli
         (split_tokens < kSplitQuantum || split_tokens > kMaxSplitTokens || split_tokens % kSplitQuantum != 0))
         return fail(SWIFTKV_EINVAL, "split_tokens %d must be 0 or a multiple of %d in [%d, %d]", split_tokens,
                     kSplitQuantum, kSplitQuantum, kMaxSplitTokens);
-    int32_t max_pos = 0;
+    int32_t max_pos = 0, min_pos = kMaxSeq;
     for (int32_t b = 0; b < batch; ++b) {
         if (positions[b] < 0 || positions[b] >= kMaxSeq)
             return fail(SWIFTKV_ERANGE, "position %d outside [0, %d)", positions[b], kMaxSeq);
         max_pos = std::max(max_pos, positions[b]);
+        min_pos = std::min(min_pos, positions[b]);
     }
     const SplitPolicy pol{cus, workgroups_per_cu, split_tokens, StepShape{0, 0}};
     StepArgs a{};
@@ -818,7 +830,9 @@ int swiftkv_debug_step_plan(int32_t cus, int32_t workgroups_per_cu, int32_t spli
     set_rows(a, positions);
     *out_split_tokens = choose_split(pol, positions, batch);
     *out_grid_splits = (max_pos + *out_split_tokens) / *out_split_tokens;
-    *out_waves = step_shape(pol, *out_grid_splits, batch).waves;
+    const StepShape shape = step_shape(pol, *out_grid_splits, batch, *out_split_tokens, min_pos + 1);
+    *out_waves = shape.waves;
+    if (out_block_tokens) *out_block_tokens = shape.block_tokens;
     if (out_rows)
         for (int32_t z = 0; z < batch; ++z) out_rows[z] = static_cast<int32_t>(a.rows[z] & 0xffu);
     return ok();

@@ -28,14 +28,19 @@ constexpr int kA14WordBytes = 56;                // ap_uint<448>: 32 x 14-bit la
 // split_tokens tokens; each wave takes 64-token blocks round-robin.
 constexpr int kAttendWaves = 4;
 constexpr int kBlockTokens = 64;
-// Launches of at most one workgroup per CU use 8 waves on 32-token blocks
-// (123 VGPRs): each wave holds half a block, so less math is left when the
-// last data arrives, and the CU keeps 8 waves' loads in flight (16 waves on
-// 32-token blocks, the same bytes per wave, measured slower: the CU then asks
-// for twice the data it can have in flight, and issues its waves' loads
-// oldest wave first, so its youngest waves start their scans last).
+// Launches of up to one residency round of 4-wave workgroups use 8 waves on
+// 32-token blocks (123 VGPRs): each wave holds half a block, so less math is
+// left when the last data arrives, and a CU keeps 8 or 16 waves' loads in
+// flight (16 waves on 32-token blocks, the same bytes per wave, measured
+// slower: the CU then asks for twice the data it can have in flight, and
+// issues its waves' loads oldest wave first, so its youngest waves start
+// their scans last).  Larger launches whose every workgroup holds at least
+// kLongRangeTokens run 8 waves on 64-token blocks, one workgroup per CU.
 constexpr int kWideWaves = 8;
 constexpr int kWideBlockTokens = 32;
+constexpr int kLongWaves = 8;
+constexpr int kLongBlockTokens = 64;
+constexpr int kLongRangeTokens = 2048;
 
 // A step launch's shape: waves per workgroup and tokens per block.
 struct StepShape {
@@ -45,8 +50,9 @@ struct StepShape {
 };
 constexpr StepShape kNarrowShape{kAttendWaves, kBlockTokens};
 constexpr StepShape kWideShape{kWideWaves, kWideBlockTokens};
+constexpr StepShape kLongShape{kLongWaves, kLongBlockTokens};
 // Every shape the step kernel is compiled for, as X(waves, block_tokens).
-#define SWIFTKV_STEP_SHAPES(X) X(4, 64) X(8, 32)
+#define SWIFTKV_STEP_SHAPES(X) X(4, 64) X(8, 32) X(8, 64)
 constexpr int kSplitQuantum = kAttendWaves * kBlockTokens;   // 256
 constexpr int kMaxSeq = 32768;                   // longest cache accepted (tokens per sequence)
 constexpr int kMaxSplits = kMaxSeq / kSplitQuantum;   // 128 partials per (sequence, head)

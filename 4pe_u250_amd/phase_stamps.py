@@ -148,7 +148,7 @@ def main():
         print(f"batch {batch}, position {pos}, {layers} layers{tag}: " + json.dumps(med), flush=True)
         if args.raw:
             os.makedirs(args.raw, exist_ok=True)
-            split, grid, waves, order = skv.step_plan(positions)
+            split, grid, waves, block, order = skv.step_plan(positions)
             np.savez_compressed(os.path.join(args.raw, f"stamps_batch{batch}.npz"),
                                 index=np.stack([r[0] for r in raw]), phase=np.stack([r[1] for r in raw]),
                                 wave=np.stack([r[2] for r in raw]), grid=np.array([grid, 32, batch]),

@@ -576,9 +576,12 @@ def main():
         main_positions = np.random.default_rng(4).integers(256, args.context + 1, args.batch) - 1
     else:
         main_positions = np.full(args.batch, args.context - 1)
-    # Every cache of the run is allocated and filled here, before the first
-    # timed region, and freed at the end (see Cache).  The main cache also
-    # serves the secondary workloads of up to its batch and context.
+    # The prefill allocates and frees its own cache and inputs, so it runs
+    # before the decode caches exist.
+    prefill = run_prefill(skv, ctx, 4096, 32, 5, seed=2034) if not args.no_configs else None
+    # Every decode cache of the run is allocated and filled here, before the
+    # first timed decode region, and freed at the end (see Cache).  The main
+    # cache also serves the secondary workloads of up to its batch and context.
     main = Cache(skv, ctx, args.batch, args.layers, args.context, seed=2026, ntok=int(main_positions.max()))
     b1_cache = (Cache(skv, ctx, 1, args.layers, args.context, seed=2027, outliers=True)
                 if not args.no_batch1 else None)
@@ -644,10 +647,8 @@ def main():
         if c is not None:
             c.close()
     if not args.no_configs:
-        # the prefill allocates its own cache and inputs, after the decode caches are freed
-        extra["prefill_append_4096tokens_32layers"] = run_prefill(skv, ctx, 4096, 32, 5, seed=2034)
-        log(f"[bench] prefill append, 4096 tokens: {extra['prefill_append_4096tokens_32layers']['us_per_layer']:.1f} "
-            f"us/layer, {extra['prefill_append_4096tokens_32layers']['gbps']:.0f} GB/s")
+        extra["prefill_append_4096tokens_32layers"] = prefill
+        log(f"[bench] prefill append, 4096 tokens: {prefill['us_per_layer']:.1f} us/layer, {prefill['gbps']:.0f} GB/s")
         log(f"[bench] host-memory I/O, batch {args.batch}: "
             f"{extra['batch64_position4095_host_io']['us_per_layer']:.1f} us/layer")
     ctx.close()

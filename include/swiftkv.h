@@ -105,8 +105,8 @@ int swiftkv_set_split_tokens(swiftkv_context* ctx, int32_t split_tokens);
  * of the context runs the step kernel of `waves` waves per workgroup on
  * `block_tokens`-token blocks instead of the shape the launch plan picks;
  * waves = 0 returns to the plan's choice.  The compiled shapes (waves,
- * block_tokens) are (4, 64) and (8, 32); any other is refused
- * (SWIFTKV_EINVAL).  Both compute the same function: tests force each one on
+ * block_tokens) are (4, 64), (8, 32) and (8, 64); any other is refused
+ * (SWIFTKV_EINVAL).  All compute the same function: tests force each one on
  * every kind of launch. */
 int swiftkv_debug_set_step_shape(swiftkv_context* ctx, int32_t waves, int32_t block_tokens);
 /* Testing aid with no counterpart in the reference, host-only (no device or
@@ -115,13 +115,15 @@ int swiftkv_debug_set_step_shape(swiftkv_context* ctx, int32_t waves, int32_t bl
  * units each holding `workgroups_per_cu` 4-wave step workgroups (a context
  * takes both from the device), with split_tokens as swiftkv_set_split_tokens
  * sets it (0: the built-in heuristic).  Writes the tokens per split, the
- * splits of the longest sequence (the grid's split dimension), the waves per
- * workgroup (4, or 8 for launches of at most one workgroup per CU) and, when
- * out_rows is not null, the sequence served by each grid row (longest first,
- * equal positions in sequence order). */
+ * splits of the longest sequence (the grid's split dimension), the shape --
+ * waves per workgroup and tokens per block: 8 on 32 up to cus x
+ * workgroups_per_cu workgroups; beyond that 8 on 64 when every workgroup's
+ * range holds at least 2048 tokens, else 4 on 64 -- (out_block_tokens may be
+ * null) and, when out_rows is not null, the sequence served by each grid row
+ * (longest first, equal positions in sequence order). */
 int swiftkv_debug_step_plan(int32_t cus, int32_t workgroups_per_cu, int32_t split_tokens, const int32_t* positions,
                             int32_t batch, int32_t* out_split_tokens, int32_t* out_grid_splits, int32_t* out_waves,
-                            int32_t* out_rows);
+                            int32_t* out_block_tokens, int32_t* out_rows);
 /* Testing aid with no counterpart in the reference.  A head split across
  * workgroups is merged inside the launch through 64-bit words tagged with the
  * (sequence row, head)'s generation + 1, which every launch that merges the

@@ -147,32 +147,39 @@ def test_host_arrays_need_host_io_mode(skv):
 
 
 @pytest.mark.parametrize("positions,split,want", [
-    ([4095], 0, (512, 8, 8)),                  # batch 1: 8 splits, one 8-wave workgroup per CU
-    ([2047], 0, (256, 8, 8)),                  # batch 1 at context 2048: 256-token splits
-    ([4095] * 2, 0, (1024, 4, 8)),
-    ([4095] * 4, 0, (2048, 2, 8)),
-    ([4095] * 8, 0, (4096, 1, 8)),             # 256 workgroups: no split
-    ([4095] * 16, 0, (4096, 1, 4)),            # more than one workgroup per CU: 4 waves
-    ([4095] * 64, 0, (4096, 1, 4)),            # the headline launch
-    ([32767] * 16, 0, (8192, 4, 4)),           # no split longer than 8192 tokens
-    ([100, 700, 2047], 0, (1024, 2, 8)),
-    ([5, 100, 100, 3], 0, (256, 1, 8)),
-    ([4095] * 4, 256, (256, 16, 4)),           # forced splits
-    ([4095], 1536, (1536, 3, 8)),
-    ([4095] * 12, 512, (512, 8, 4)),           # 3,072 workgroups
+    ([4095], 0, (512, 8, 8, 32)),              # batch 1: 8 splits, one 8-wave workgroup per CU
+    ([2047], 0, (256, 8, 8, 32)),              # batch 1 at context 2048: 256-token splits
+    ([4095] * 2, 0, (1024, 4, 8, 32)),
+    ([4095] * 4, 0, (2048, 2, 8, 32)),
+    ([4095] * 8, 0, (4096, 1, 8, 32)),         # 256 workgroups: no split
+    ([4095] * 12, 0, (2048, 2, 8, 32)),        # 768 workgroups: one round of three 4-wave workgroups per CU
+    ([4095] * 16, 0, (4096, 1, 8, 32)),
+    ([4095] * 24, 0, (4096, 1, 8, 32)),        # 768 workgroups
+    ([4095] * 25, 0, (4096, 1, 8, 64)),        # past one round, every range 4096 tokens: 8 waves, 64-token blocks
+    ([4095] * 64, 0, (4096, 1, 8, 64)),        # the headline launch
+    ([2047] * 32, 0, (2048, 1, 8, 64)),        # ranges of exactly 2048 tokens
+    ([2046] * 32, 0, (2048, 1, 4, 64)),        # 2047 tokens: 4 waves
+    ([255] + [4095] * 63, 0, (4096, 1, 4, 64)),   # a short row: 4 waves (the ragged batch)
+    ([32767] * 16, 0, (8192, 4, 8, 64)),       # no split longer than 8192 tokens
+    ([100, 700, 2047], 0, (1024, 2, 8, 32)),
+    ([5, 100, 100, 3], 0, (256, 1, 8, 32)),
+    ([4095] * 4, 256, (256, 16, 4, 64)),       # forced splits: 2,048 workgroups of 256 tokens
+    ([4095], 1536, (1536, 3, 8, 32)),
+    ([4095] * 12, 512, (512, 8, 4, 64)),       # 3,072 workgroups
+    ([4095] * 32, 2048, (2048, 2, 8, 64)),     # 2,048 workgroups of 2048 tokens
 ])
 def test_step_plan(skv, positions, split, want):
     """The launch plan on the reference device shape (256 CUs, three 4-wave
     step workgroups per CU): tokens per split, splits of the longest
-    sequence, waves per workgroup.  Host logic only."""
+    sequence, waves per workgroup, tokens per block.  Host logic only."""
     got = skv.step_plan(positions, split_tokens=split)
-    assert got[:3] == want
+    assert got[:4] == want
 
 
 def test_step_plan_orders_rows_longest_first(skv):
-    split, grid, waves, rows = skv.step_plan([5, 100, 100, 3, 4095, 0, 100])
+    split, grid, waves, block, rows = skv.step_plan([5, 100, 100, 3, 4095, 0, 100])
     assert rows.tolist() == [4, 1, 2, 6, 0, 3, 5]       # equal positions keep sequence order
-    _, _, _, rows = skv.step_plan(list(range(256)))
+    _, _, _, _, rows = skv.step_plan(list(range(256)))
     assert rows.tolist() == list(range(255, -1, -1))
 
 
@@ -184,7 +191,7 @@ def test_step_plan_argument_checks(skv):
 
     def plan(cus=256, per_cu=3, split=0, positions=p, batch=2):
         return L.swiftkv_debug_step_plan(cus, per_cu, split, positions, batch, C.byref(out[0]), C.byref(out[1]),
-                                         C.byref(out[2]), None)
+                                         C.byref(out[2]), None, None)
 
     assert plan() == skv.OK and (out[0].value, out[1].value, out[2].value) == (256, 1, 8)
     assert plan(positions=None) == skv.EINVAL

@@ -86,8 +86,8 @@ def test_config1_batch1_position127(skv, ctx, lut4096, rope_tables):
 def test_batch_positions_edges(skv, ctx, lut4096, rope_tables, split):
     """Positions around block (64) and split (256) boundaries; with split 256
     some heads finish in the step kernel and others go through the combine.
-    Batch 8 at split 4096 is one workgroup per CU (8 waves on 32-token
-    blocks); at split 256 the launch has more (4 waves on 64-token blocks)."""
+    Both launches run 8 waves on 32-token blocks (256 and 512 workgroups);
+    test_forced_step_shapes covers the other shapes on the same edges."""
     _note(f"case: batch 8 positions [0,1,63,64,255,256,257,300], layer 1 of 3, split {split}")
     _scenario(skv, ctx, lut4096, rope_tables, [0, 1, 63, 64, 255, 256, 257, 300], seed=21, layers=3, layer=1,
               cap=320, split=split)
@@ -121,15 +121,14 @@ def test_randomized_configurations(skv, ctx, lut4096, rope_tables, case):
               dist=dist, outliers=outl, split=split, q17=q17)
 
 
-# Seeds whose shapes run the 8-wave launch (every one but 9501 and 9503,
-# which run 4-wave workgroups), with 1 to 8 splits per head.
+# Seeds whose launches run 8 waves on 32-token blocks, with 1 to 8 splits
+# per head.
 @pytest.mark.parametrize("seed", [9500, 9501, 9502, 9503, 9506, 9511, 9514, 9531])
 def test_randomized_small_batches(skv, ctx, lut4096, rope_tables, seed):
-    """Seeded random shapes for small launches (8 waves on 32-token blocks
-    when a launch has at most one workgroup per CU, 4 waves on 64-token
-    blocks otherwise): batch 1..8, ragged positions up to 4095, heuristic or
-    forced split of 512 to 2048 tokens, FP32 or Q15.17 entry, N(0,1) or
-    Student-t(3) data, with or without outlier channels."""
+    """Seeded random shapes for small launches (8 waves on 32-token blocks):
+    batch 1..8, ragged positions up to 4095, heuristic or forced split of 512
+    to 2048 tokens, FP32 or Q15.17 entry, N(0,1) or Student-t(3) data, with
+    or without outlier channels."""
     case = seed - 9500
     rng = np.random.default_rng(seed)
     B = int(rng.integers(1, 9))
@@ -147,7 +146,7 @@ def test_randomized_small_batches(skv, ctx, lut4096, rope_tables, seed):
 _EDGE_POSITIONS = [0, 1, 31, 32, 33, 63, 64, 65, 255, 256, 257, 300]
 
 
-@pytest.mark.parametrize("shape", [(4, 64), (8, 32)], ids=["4waves_64tok", "8waves_32tok"])
+@pytest.mark.parametrize("shape", [(4, 64), (8, 32), (8, 64)], ids=["4waves_64tok", "8waves_32tok", "8waves_64tok"])
 @pytest.mark.parametrize("positions,split", [
     ([4095], 0),                                        # 8 splits of 512 tokens, inline merge
     ([2047], 0),                                        # 8 splits of 256 tokens
@@ -464,7 +463,7 @@ def test_error_codes(skv, ctx, lut4096):
     with pytest.raises(skv.SwiftKVError) as ei:
         ctx.set_split_tokens(300)
     assert ei.value.code == skv.EINVAL
-    for shape in ((16, 32), (8, 64), (4, 32), (-1, 64)):   # shapes no step kernel is compiled for
+    for shape in ((16, 32), (16, 64), (4, 32), (-1, 64)):   # shapes no step kernel is compiled for
         with pytest.raises(skv.SwiftKVError) as ei:
             ctx.debug_set_step_shape(*shape)
         assert ei.value.code == skv.EINVAL
