@@ -483,7 +483,7 @@ def swiftkv_attention(ctx: Context, q, k, v, kv_cache: KVCache, rope_lut: RopeLu
               _io_ptr(ctx, out, np.float32, True)))
 
 
-NOALLOC_WORKSPACE_BYTES = 69206016   # 1 MiB of arrival words + 8 splits x 256 sequences x 32 heads of partials
+NOALLOC_WORKSPACE_BYTES = 8650752   # 128 KiB of arrival words + 8 splits x 32 sequences x 32 heads of partials
 
 
 def step_plan(positions, cus: int = 256, workgroups_per_cu: int = 3, split_tokens: int = 0):

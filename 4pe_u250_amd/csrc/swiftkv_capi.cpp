@@ -488,16 +488,89 @@ void profile_end(swiftkv_context* ctx, ProfilePair* p) {
     if (p) (void)hipEventRecord(p->end, ctx->stream);
 }
 
-// noalloc: the split workspace is this device's fixed file-scope array
-// instead of the context's growable buffer; a launch that needs more than it
-// holds is refused (SWIFTKV_ERANGE) before anything is enqueued.
+// The arguments of one step call, for the launches it makes.
+struct StepCall {
+    const void* q;
+    const void* k;
+    const void* v;
+    StepInput in;
+    swiftkv_kv_cache* kv;
+    const swiftkv_rope_lut* lut;
+    uint8_t* act_q;
+    uint8_t* act_scale;
+    int32_t layer;
+    const int32_t* positions;
+    float* out;
+};
+
+// One step launch over the call's sequences [b0, b0 + nb) with the given
+// split and shape.  noalloc: the split workspace is this device's fixed
+// array (split launches of at most kNoAllocSplitRows sequences).
+int launch_rows(swiftkv_context* ctx, const StepCall& c, int32_t b0, int32_t nb, int32_t split_tokens,
+                StepShape shape, bool noalloc) {
+    constexpr size_t elem_bytes = 4;
+    StepArgs a;
+    std::memset(&a, 0, sizeof(a));
+    const size_t row0 = static_cast<size_t>(b0) * kModelDim;
+    a.q = static_cast<const char*>(c.q) + row0 * elem_bytes;
+    a.k = static_cast<const char*>(c.k) + row0 * elem_bytes;
+    a.v = static_cast<const char*>(c.v) + row0 * elem_bytes;
+    a.part_stride = c.in.part_stride;
+    a.kv = CacheView{c.kv->base, c.kv->page_bytes, c.kv->seq_cap, c.kv->layers};
+    a.lut = c.lut->table;
+    a.lut_positions = c.lut->positions;
+    a.layer = c.layer;
+    a.batch = nb;
+    a.slot0 = b0;
+    int32_t max_pos = 0;
+    for (int32_t b = 0; b < nb; ++b) max_pos = std::max(max_pos, c.positions[b0 + b]);
+    set_rows(a, c.positions + b0);
+    a.split_tokens = split_tokens;
+    const int32_t grid_splits = (max_pos + 1 + split_tokens - 1) / split_tokens;
+    int rc;
+    if (grid_splits > 1 && noalloc) {
+        a.arrivals = reinterpret_cast<uint64_t*>(ctx->scratch);
+        a.partials = reinterpret_cast<uint64_t*>(ctx->scratch + kNoAllocCounterBytes);
+        a.slot_stride = kFixedSlots;
+    } else if (grid_splits > 1) {
+        if ((rc = ensure_partials(ctx, nb, grid_splits))) return rc;
+        if (ctx->capturing) ctx->capture_uses_workspace = true;
+        a.arrivals = ctx->partials;
+        a.partials = ctx->partials + arrival_words(ctx->partial_rows);
+        a.slot_stride = ctx->partial_slots;
+    } else {
+        a.arrivals = ctx->arrivals;   // read, never written, by a launch that splits no head
+        a.partials = nullptr;
+        a.slot_stride = 0;
+    }
+    a.out = c.out + row0;
+    a.act_q = c.act_q ? c.act_q + static_cast<size_t>(b0) * kHeads * kGroupsPerHead * SWIFTKV_A14_WORD_BYTES
+                      : nullptr;
+    a.act_scale = c.act_scale ? c.act_scale + static_cast<size_t>(b0) * kHeads * kGroupsPerHead : nullptr;
+    a.merge_polls = ctx->merge_fault_test ? 1u : kMergePolls;
+    a.merge_tag_skew = ctx->merge_fault_test ? 1u : 0u;
+    a.fault = ctx->fault_dev;
+    ProfilePair* p = profile_begin(ctx, SWIFTKV_KERNEL_STEP);
+    SKV_HIP(launch_step(a, grid_splits, shape, c.in.format, ctx->stream));
+    profile_end(ctx, p);
+    return SWIFTKV_OK;
+}
+
+// The call runs one launch per kMaxBatchPerLaunch sequences, each planned
+// (split and shape) on its own sequences.  noalloc: the split workspace is
+// this device's fixed file-scope array instead of the context's growable
+// buffer.  It holds kFixedSlots splits per head of kNoAllocSplitRows
+// sequences: a plan that splits heads more ways is refused (SWIFTKV_ERANGE)
+// before anything is enqueued, and a split launch of more sequences runs as
+// launches of kNoAllocSplitRows sequences with the same plan, so every head
+// sees the same split and shape, and gives the same bits, as in the
+// allocating entry.
 int run_step(swiftkv_context* ctx, const void* q, const void* k, const void* v, StepInput in,
              swiftkv_kv_cache* kv, const swiftkv_rope_lut* lut, uint8_t* act_q, uint8_t* act_scale,
              int32_t layer, const int32_t* positions, int32_t batch, float* out, bool noalloc = false) {
     int rc = validate_step(ctx, q, k, v, kv, lut, act_q, act_scale, layer, positions, batch, out);
     if (rc) return rc;
     if ((rc = set_device(ctx))) return rc;
-    const size_t elem_bytes = 4;
     if (noalloc) {   // check every launch first, so a refused call enqueues nothing
         for (int32_t b0 = 0; b0 < batch; b0 += kMaxBatchPerLaunch) {
             const int32_t nb = std::min<int32_t>(kMaxBatchPerLaunch, batch - b0);
@@ -511,56 +584,20 @@ int run_step(swiftkv_context* ctx, const void* q, const void* k, const void* v, 
                             split, max_pos + 1, kFixedSlots);
         }
     }
+    const StepCall call{q, k, v, in, kv, lut, act_q, act_scale, layer, positions, out};
     for (int32_t b0 = 0; b0 < batch; b0 += kMaxBatchPerLaunch) {
         const int32_t nb = std::min<int32_t>(kMaxBatchPerLaunch, batch - b0);
-        StepArgs a;
-        std::memset(&a, 0, sizeof(a));
-        const size_t row0 = static_cast<size_t>(b0) * kModelDim;
-        a.q = static_cast<const char*>(q) + row0 * elem_bytes;
-        a.k = static_cast<const char*>(k) + row0 * elem_bytes;
-        a.v = static_cast<const char*>(v) + row0 * elem_bytes;
-        a.part_stride = in.part_stride;
-        a.kv = CacheView{kv->base, kv->page_bytes, kv->seq_cap, kv->layers};
-        a.lut = lut->table;
-        a.lut_positions = lut->positions;
-        a.layer = layer;
-        a.batch = nb;
-        a.slot0 = b0;
         int32_t max_pos = 0, min_pos = kMaxSeq;
         for (int32_t b = 0; b < nb; ++b) {
             max_pos = std::max(max_pos, positions[b0 + b]);
             min_pos = std::min(min_pos, positions[b0 + b]);
         }
-        set_rows(a, positions + b0);
-        a.split_tokens = choose_split(policy_of(ctx), positions + b0, nb);
-        const int32_t grid_splits = (max_pos + 1 + a.split_tokens - 1) / a.split_tokens;
-        if (noalloc) {
-            a.arrivals = reinterpret_cast<uint64_t*>(ctx->scratch);
-            a.partials = reinterpret_cast<uint64_t*>(ctx->scratch + kNoAllocCounterBytes);
-            a.slot_stride = kFixedSlots;
-        } else if (grid_splits > 1) {
-            if ((rc = ensure_partials(ctx, nb, grid_splits))) return rc;
-            if (ctx->capturing) ctx->capture_uses_workspace = true;
-            a.arrivals = ctx->partials;
-            a.partials = ctx->partials + arrival_words(ctx->partial_rows);
-            a.slot_stride = ctx->partial_slots;
-        } else {
-            a.arrivals = ctx->arrivals;
-            a.partials = nullptr;   // no head of the launch is split
-            a.slot_stride = 0;
-        }
-        a.out = out + row0;
-        a.act_q = act_q ? act_q + static_cast<size_t>(b0) * kHeads * kGroupsPerHead * SWIFTKV_A14_WORD_BYTES
-                        : nullptr;
-        a.act_scale = act_scale ? act_scale + static_cast<size_t>(b0) * kHeads * kGroupsPerHead : nullptr;
-        a.merge_polls = ctx->merge_fault_test ? 1u : kMergePolls;
-        a.merge_tag_skew = ctx->merge_fault_test ? 1u : 0u;
-        a.fault = ctx->fault_dev;
-
-        ProfilePair* p = profile_begin(ctx, SWIFTKV_KERNEL_STEP);
-        SKV_HIP(launch_step(a, grid_splits, step_shape(policy_of(ctx), grid_splits, nb, a.split_tokens, min_pos + 1),
-                            in.format, ctx->stream));
-        profile_end(ctx, p);
+        const int32_t split = choose_split(policy_of(ctx), positions + b0, nb);
+        const int32_t grid_splits = (max_pos + split) / split;
+        const StepShape shape = step_shape(policy_of(ctx), grid_splits, nb, split, min_pos + 1);
+        const int32_t rows = noalloc && grid_splits > 1 ? kNoAllocSplitRows : nb;
+        for (int32_t s0 = 0; s0 < nb; s0 += rows)
+            if ((rc = launch_rows(ctx, call, b0 + s0, std::min(rows, nb - s0), split, shape, noalloc))) return rc;
     }
     return ok();
 }
@@ -850,7 +887,7 @@ int swiftkv_debug_set_split_generation(swiftkv_context* ctx, uint32_t generation
     int32_t rows = 0, slots = 0;
     if (noalloc) {
         base = reinterpret_cast<uint64_t*>(ctx->scratch);
-        rows = kMaxBatchPerLaunch;
+        rows = kNoAllocSplitRows;
         slots = kFixedSlots;
     } else {
         base = ctx->partials;

@@ -157,10 +157,15 @@ struct BulkArgs {
 
 // Workspace of the allocation-free step entry: one file-scope device array
 // per GPU (swiftkv_kernels.hip), the split-arrival counters first, then the
-// split partials.  Bound once per device by bind_noalloc_scratch.
-constexpr size_t kNoAllocCounterBytes = sizeof(uint64_t) * kMaxBatchPerLaunch * kHeads * kArrivalStride;
+// split partials, for kFixedSlots splits per head of kNoAllocSplitRows
+// sequences per launch (the launch plan splits heads only in launches of
+// fewer than 32 sequences at 256 CUs; a caller's forced split of more runs
+// as launches of kNoAllocSplitRows).  Bound once per device by
+// bind_noalloc_scratch.
+constexpr int kNoAllocSplitRows = 32;
+constexpr size_t kNoAllocCounterBytes = sizeof(uint64_t) * kNoAllocSplitRows * kHeads * kArrivalStride;
 constexpr size_t kNoAllocPartialBytes =
-    sizeof(uint64_t) * kMaxBatchPerLaunch * kHeads * kFixedSlots * kSlotWords;
+    sizeof(uint64_t) * kNoAllocSplitRows * kHeads * kFixedSlots * kSlotWords;
 constexpr size_t kNoAllocScratchBytes = kNoAllocCounterBytes + kNoAllocPartialBytes;
 
 // Launchers (swiftkv_kernels.hip).

@@ -227,20 +227,24 @@ int swiftkv_attention_q17(swiftkv_context* ctx, const int32_t* q, const int32_t*
  * Same arguments, kernels and results as swiftkv_attention_f32, but the split
  * workspace (per-head arrival words and the split partials) is a fixed
  * file-scope device array that every GPU the library runs on holds until the
- * process ends (SWIFTKV_NOALLOC_WORKSPACE_BYTES, 66 MiB: 1 MiB of arrival
- * words, 65 MiB of partials for up to 8 splits per head of 256 sequences per
- * launch), bound once per device when the first context on it is created.
- * The call allocates nothing, host or device.
+ * process ends (SWIFTKV_NOALLOC_WORKSPACE_BYTES, 8.25 MiB: 128 KiB of
+ * arrival words and 8.1 MiB of partials, for up to 8 splits per head of 32
+ * sequences per launch), bound once per device when the first context on it
+ * is created.  The call allocates nothing, host or device.
  *   - A call that would split a head more than 8 ways (only a forced split,
  *     swiftkv_set_split_tokens, does) returns SWIFTKV_ERANGE before any work
  *     is enqueued; the built-in heuristic never does.
+ *   - A launch whose plan splits the heads of more than 32 sequences (only a
+ *     forced split does; the heuristic splits heads only for fewer) runs as
+ *     launches of 32 sequences with that plan, so the outputs are still
+ *     those of swiftkv_attention_f32, bit for bit.
  *   - Every call on one GPU shares that GPU's array: calls that overlap in
  *     time on one GPU (two contexts, or two streams) race and must not be
  *     issued.  Calls in order on one context are safe; the kernels leave the
  *     arrival counts at zero.
  *   - Host-memory I/O mode is refused (SWIFTKV_ESTATE): it stages through an
  *     allocated buffer. */
-#define SWIFTKV_NOALLOC_WORKSPACE_BYTES 69206016u
+#define SWIFTKV_NOALLOC_WORKSPACE_BYTES 8650752u
 int swiftkv_attention_f32_noalloc(swiftkv_context* ctx, const float* q, const float* k, const float* v,
                                   swiftkv_kv_cache* kv_cache, const swiftkv_rope_lut* rope_lut,
                                   uint8_t* activation_q, uint8_t* activation_scale, int32_t layer_index,

@@ -203,9 +203,12 @@ def test_batch300_split_across_two_launches(skv, ctx, rope_tables, entry):
     """300 sequences at ragged positions 300..1400 with forced 256-token
     splits: two launches (256 rows, then 44) whose split heads reuse the same
     workspace rows (the second launch's tags follow the first's), through the
-    regular entry and through the allocation-free one (its fixed workspace).
-    Every sequence's appended row bit-exact; the outputs of sequences on both
-    sides of the launch boundary checked in full against the oracle."""
+    regular entry and through the allocation-free one, whose fixed workspace
+    holds the split slots of 32 sequences, so it runs them as 10 launches of
+    at most 32 sequences with the same plan: its outputs must equal the
+    regular entry's bit for bit.  Every sequence's appended row bit-exact;
+    the outputs of sequences on both sides of the launch boundaries checked
+    in full against the oracle."""
     cos, sin = rope_tables
     batch, seed = 300, 7300
     rng = np.random.default_rng(seed)
@@ -235,9 +238,19 @@ def test_batch300_split_across_two_launches(skv, ctx, rope_tables, entry):
     words = aq.download(np.uint8, (batch, 128, 56))
     codes = asc.download(np.uint8, (batch, 128))
     assert np.isfinite(o).all()
+    if entry == "noalloc":
+        ctx.set_split_tokens(256)
+        try:
+            skv.swiftkv_attention(ctx, bufs[0], bufs[1], bufs[2], kv, lut, aq, asc, 0, positions, out)
+            ctx.synchronize()
+        finally:
+            ctx.set_split_tokens(0)
+        assert np.array_equal(out.download(np.float32, (batch, 4096)).view(np.uint32), o.view(np.uint32))
+        assert np.array_equal(aq.download(np.uint8, (batch, 128, 56)), words)
+        assert np.array_equal(asc.download(np.uint8, (batch, 128)), codes)
     for b in range(batch):
         _appended_rows_match(kv, b, 0, int(positions[b]), k[b], v[b], cos, sin)
-    for b in (0, 255, 256, 299, int(np.argmax(positions))):
+    for b in (0, 31, 32, 255, 256, 299, int(np.argmax(positions))):
         p = int(positions[b])
         _note(f"  oracle check of sequence {b}, position {p}")
         sc = _oracle_cache(skv, ctx, cos, sin, seed, b, 0, p, p + 1)
