@@ -20,7 +20,9 @@ from the first workgroup's start, medians over the repetitions:
   - epilogue:    FP32 row and A14/E8M0 words written;
   - launch:      the event-timed time per layer minus the span from the first
                  workgroup's start to the last one's end (dispatch, completion
-                 and the gap to the next launch).
+                 and the gap to the next launch);
+  - per XCD:     workgroups, their median span from entry to end, and the
+                 XCD's last workgroup end.
 With --parts N (2 or 4) the steps go through swiftkv_attention_partials, fed
 N split-K FP32 partials of q, k and v.
 Diagnostics only: nothing here is the product path, and the product library
@@ -70,6 +72,13 @@ def launch_phases(ph, wv, nwg):
                   "last_lds_to_end": float(np.max(end) - np.nanmax(lds))})
     else:
         d.update({"epilogue_p50": pct(done - lds, 50), "last_lds_to_end": float(np.max(end) - np.nanmax(lds))})
+    # Per XCD (slot 7's low half): workgroups, their mean span from entry to
+    # end, and the XCD's last workgroup end.
+    xcd = ph[:, 7] & 0xFFFFFFFF
+    d["xcd_workgroups"] = [int((xcd == x).sum()) for x in range(8)]
+    d["xcd_workgroup_us_p50"] = [pct((end - entry)[xcd == x], 50) if (xcd == x).any() else float("nan")
+                                  for x in range(8)]
+    d["xcd_done"] = [float(np.max(end[xcd == x])) if (xcd == x).any() else float("nan") for x in range(8)]
     return d
 
 
@@ -142,7 +151,8 @@ def main():
             d["launch"] = us_layer - d["span"]
             d["workgroups"] = nwg
             rows.append(d)
-        med = {k: round(float(np.median([r[k] for r in rows])), 3) for k in rows[0]}
+        med = {k: (np.round(np.median([r[k] for r in rows], axis=0), 3).tolist() if isinstance(rows[0][k], list)
+                   else round(float(np.median([r[k] for r in rows])), 3)) for k in rows[0]}
         tag = f", {parts} partials" if parts else ""
         out[f"batch{batch}_position{pos}" + (f"_parts{parts}" if parts else "")] = med
         print(f"batch {batch}, position {pos}, {layers} layers{tag}: " + json.dumps(med), flush=True)
