@@ -35,6 +35,12 @@ HIP_FLAGS = [
     # broadcasts the result at once, so the issuing wave would stall on the
     # round trip (the balanced scan's unit claims, the split arrival count).
     "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
+    # The leading kernel arguments (the step kernel's first eight: everything
+    # its first loads depend on) are preloaded into SGPRs by the dispatcher,
+    # so a wave issues its first vector loads without waiting on scalar loads
+    # of the argument block.  Kernels whose first argument is a struct
+    # preload nothing.
+    "-mllvm", "-amdgpu-kernarg-preload-count=8",
 ]
 SOURCES = ["swiftkv_kernels.hip", "swiftkv_synth.hip", "swiftkv_exact.hip", "swiftkv_capi.cpp"]
 HOST_SRC = os.path.join(PKG_DIR, "host", "swiftkv_host.cpp")

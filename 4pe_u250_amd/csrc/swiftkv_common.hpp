@@ -142,6 +142,23 @@ __host__ __device__ inline uint32_t pack_row(int seq, int pos) {
     return (static_cast<uint32_t>(pos) << 8) | static_cast<uint32_t>(seq);
 }
 
+// The step kernel's leading arguments, preloaded into SGPRs (12 of the 14
+// user SGPRs left beside the argument-block pointer): everything its first
+// loads depend on, derived from a StepArgs by the launcher.
+//   layer_pages: the page of (sequence 0 of the launch, layer, head 0);
+//                page (b, h) = layer_pages + (b * layers * 32 + h) * seq_cap * 288
+//   geometry:    seq_cap (bits 0-15) | layers (bits 16-31)
+//   dispatch:    the launch's common position, or kRowsListed when its
+//                positions differ (rows[] then names each row's) (bits
+//                0-15) | split_tokens / kSplitQuantum (bits 16-31)
+struct StepPreload {
+    static constexpr uint32_t kRowsListed = 0xffffu;
+    const int8_t* layer_pages;
+    uint32_t geometry;
+    uint32_t dispatch;
+};
+static_assert(kMaxSeq <= 0x8000 && kMaxSeq / kSplitQuantum <= 0xffff, "StepPreload packs positions and splits in 16 bits");
+
 // Bulk append of n tokens of one sequence (prefill).
 struct BulkArgs {
     const void* k;            // [n][4096]

@@ -340,7 +340,23 @@ __device__ __forceinline__ float readlane_f(float x, int lane) {
 // so the group maximum (DPP within 16-lane rows, then the two rows of the
 // half) and the packing of the 14-bit lanes (lane-to-lane reads) stay inside
 // the wave, with no LDS and no barrier.
-__device__ __forceinline__ void finalize_head(const StepArgs& a, int b, int h, float o) {
+// The argument-block fields the end of a step uses: its outputs and the split
+// exchange.  The step kernel loads them into SGPRs while its first loads are
+// in flight; loaded where they are used, each was a scalar round trip ahead
+// of the merge or the output stores.
+struct StepTail {
+    float* out;
+    uint8_t* act_q;
+    uint8_t* act_scale;
+    uint64_t* partials;
+    uint32_t* fault;
+    int32_t slot_stride;
+    uint32_t merge_tag_skew;
+    uint32_t merge_polls;
+    int32_t slot0;
+};
+
+__device__ __forceinline__ void finalize_head(const StepTail& a, int b, int h, float o) {
     const int d = threadIdx.x;
     a.out[static_cast<size_t>(b) * kModelDim + h * kHeadDim + d] = o;
     if (a.act_q == nullptr) return;
@@ -564,16 +580,33 @@ __device__ __forceinline__ float merge_looped(const uint64_t* slots, int n, int 
 
 // Grid (splits, 32 heads, batch) of WAVES-wave workgroups scanning blocks of
 // 8 * NI tokens (NI rows per lane); grid row z serves rows[z].
+//
+// The arguments every first load depends on come first and travel in SGPRs:
+// the library is compiled with kernarg preloading (-amdgpu-kernarg-preload-
+// count), so the dispatcher writes them into each wave's user SGPRs and no
+// wave waits on a scalar load of the argument block before its first vector
+// loads (a wave that had to load them chained three scalar round trips ahead
+// of its first cache block).  Firmware without the feature runs the code
+// object's own prologue, which loads the same SGPRs.  StepPreload (host and
+// kernel) packs them; the rest of the arguments stay in StepArgs.
 template <int IN, int WAVES, int NI>
-__global__ __launch_bounds__(WAVES * 64) void step_kernel(StepArgs a) {
+__global__ __launch_bounds__(WAVES * 64) void step_kernel(const int8_t* layer_pages, uint32_t geometry,
+                                                          uint32_t dispatch, const void* q_in, const void* k_in,
+                                                          const void* v_in, const int2* lut, uint64_t* arrivals,
+                                                          StepArgs a) {
     constexpr int kBlk = 8 * NI;
     SKV_STAMP_DECL;
     SKV_STAMP(0);
-    const uint32_t row = a.rows[blockIdx.z];
+    // A launch whose sequences all stand at one position names it in
+    // `dispatch` and its rows are the identity (set_rows keeps equal positions
+    // in sequence order); only other launches read rows[].
+    const uint32_t uniform_pos = dispatch & StepPreload::kRowsListed;
+    const uint32_t row = uniform_pos != StepPreload::kRowsListed ? pack_row(blockIdx.z, uniform_pos)
+                                                                 : a.rows[blockIdx.z];
     const int split = blockIdx.x, h = blockIdx.y, b = static_cast<int>(row & 0xffu);
     const int pos = static_cast<int>(row >> 8);
     const int len = pos + 1;
-    const int C = a.split_tokens;
+    const int C = static_cast<int>(dispatch >> 16) * kSplitQuantum;
     const int t_begin = split * C;
     if (t_begin >= len) {
         SKV_STAMP_FLUSH();
@@ -588,8 +621,10 @@ __global__ __launch_bounds__(WAVES * 64) void step_kernel(StepArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int lane = threadIdx.x & 63;
     const int c = lane & 7, r = lane >> 3;
-    int8_t* page = page_ptr(a.kv, a.slot0 + b, a.layer, h);
-    const int64_t cap = a.kv.seq_cap;
+    const int64_t cap = geometry & 0xffffu;
+    const int64_t page_bytes = cap * kTokenBytes;
+    int8_t* page = const_cast<int8_t*>(layer_pages) +
+                   (static_cast<int64_t>(b) * (geometry >> 16) * kHeads + h) * page_bytes;
 
     __shared__ float s_acc[WAVES + 1][kHeadDim];
     __shared__ float s_m[WAVES + 1], s_l[WAVES + 1];
@@ -607,12 +642,12 @@ __global__ __launch_bounds__(WAVES * 64) void step_kernel(StepArgs a) {
     // at batch 1: 12.5-12.9 against 11.7-11.9 us/layer.)
     const size_t row_elem = static_cast<size_t>(b) * kModelDim + h * kHeadDim + 2 * lane;
     const bool appends = owner && wave == 0;       // this wave writes and forwards the new row
-    const int2 row_cs = a.lut[static_cast<size_t>(pos) * kRopePairs + lane];
-    const InPair<IN> row_q = load_in<IN>(a.q, row_elem, a.part_stride);
+    const int2 row_cs = lut[static_cast<size_t>(pos) * kRopePairs + lane];
+    const InPair<IN> row_q = load_in<IN>(q_in, row_elem, a.part_stride);
     InPair<IN> row_k{}, row_v{};
     if (appends) {
-        row_k = load_in<IN>(a.k, row_elem, a.part_stride);
-        row_v = load_in<IN>(a.v, row_elem, a.part_stride);
+        row_k = load_in<IN>(k_in, row_elem, a.part_stride);
+        row_v = load_in<IN>(v_in, row_elem, a.part_stride);
     }
     const PageReader pr = make_reader(page, cap, c, r);
     const int t_first = t_begin + wave * kBlk;
@@ -625,8 +660,11 @@ __global__ __launch_bounds__(WAVES * 64) void step_kernel(StepArgs a) {
     // on every path (unused by a head held by one split): a load under a
     // branch would make the compiler wait for the block at the join.
     const size_t head_row = static_cast<size_t>(b) * kHeads + h;
-    uint64_t* arrival = a.arrivals + head_row * kArrivalStride;
+    uint64_t* arrival = arrivals + head_row * kArrivalStride;
     const uint64_t arrival_word = fetch_word(arrival);
+    const StepTail tail{a.out,         a.act_q,          a.act_scale,  a.partials, a.fault,
+                        a.slot_stride, a.merge_tag_skew, a.merge_polls, a.slot0};
+    __builtin_amdgcn_sched_barrier(0);   // issue their loads here, not at the first wait
 
     // Query: each lane converts and rotates its own pair and splits it into
     // byte limbs; each lane then gathers the limbs of its chunk c.  The new
@@ -646,6 +684,10 @@ __global__ __launch_bounds__(WAVES * 64) void step_kernel(StepArgs a) {
     const int2 ki = in_to_q17<IN>(row_k), vi = in_to_q17<IN>(row_v);
     int32_t k0, k1;
     rope_pair(ki.x, ki.y, row_cs, k0, k1);
+    // The tail's fields are in SGPRs from here on (the wait for them, if any,
+    // falls in the wait for the first block).
+    asm volatile("" ::"s"(tail.out), "s"(tail.act_q), "s"(tail.act_scale), "s"(tail.partials), "s"(tail.fault),
+                 "s"(tail.slot_stride), "s"(tail.merge_tag_skew), "s"(tail.merge_polls), "s"(tail.slot0));
 
     float m_run, l_run, acc[16];
     scan_range<NI>(pr, bl, Q, t_first, t_stop, WAVES * kBlk, r, m_run, l_run, acc);
@@ -658,7 +700,7 @@ __global__ __launch_bounds__(WAVES * 64) void step_kernel(StepArgs a) {
     // one more partial.
     if (appends) {
         float kh0, kh1, vh0, vh1;
-        append_row_dequant(page, a.kv.seq_cap, pos, lane, k0, k1, vi.x, vi.y, kh0, kh1, vh0, vh1);
+        append_row_dequant(page, static_cast<int>(cap), pos, lane, k0, k1, vi.x, vi.y, kh0, kh1, vh0, vh1);
         float sp = qs0 * kh0 + qs1 * kh1;
 #pragma unroll
         for (int s = 1; s < 64; s <<= 1) sp += __shfl_xor(sp, s);
@@ -693,7 +735,7 @@ __global__ __launch_bounds__(WAVES * 64) void step_kernel(StepArgs a) {
         }
     }
     if (nsplit == 1) {
-        if (d < kHeadDim) finalize_head(a, b, h, o / l);
+        if (d < kHeadDim) finalize_head(tail, b, h, o / l);
         SKV_STAMP(5);
         SKV_STAMP_FLUSH();
         return;
@@ -714,7 +756,7 @@ __global__ __launch_bounds__(WAVES * 64) void step_kernel(StepArgs a) {
     // load in flight, the first cache block included.
     asm volatile("" ::"v"(arrival_word));
     const uint32_t tag = static_cast<uint32_t>(arrival_word >> 32) + 1u;
-    uint64_t* slots = a.partials + head_row * static_cast<size_t>(a.slot_stride) * kSlotWords;
+    uint64_t* slots = tail.partials + head_row * static_cast<size_t>(tail.slot_stride) * kSlotWords;
     const bool inline_merge = nsplit <= kMergeInline;
     // The count goes out from thread 128, in a wave that publishes nothing,
     // so waiting for its result never waits for the stores of waves 0-1.
@@ -744,20 +786,20 @@ __global__ __launch_bounds__(WAVES * 64) void step_kernel(StepArgs a) {
     }
     // The merger waits for words tagged `want` (a testing aid can make it wait
     // for a tag no word carries, so that the wait gives up).
-    const uint32_t want = tag + a.merge_tag_skew;
+    const uint32_t want = tag + tail.merge_tag_skew;
     bool gave_up = false;
     float merged;
     if (inline_merge) {
         InlineWords w;
         fetch_inline(slots, nsplit, split, want, mx, l, o, w);
-        merged = merge_inline(slots, nsplit, want, a.merge_polls, w, gave_up);
+        merged = merge_inline(slots, nsplit, want, tail.merge_polls, w, gave_up);
     } else {
-        merged = merge_looped(slots, nsplit, split, want, a.merge_polls, mx, l, o, gave_up);
+        merged = merge_looped(slots, nsplit, split, want, tail.merge_polls, mx, l, o, gave_up);
     }
     SKV_STAMP(4);
-    if (gave_up) report_merge_fault(a.fault, static_cast<uint32_t>(a.slot0 + b) * kHeads + h + 1u);
+    if (gave_up) report_merge_fault(tail.fault, static_cast<uint32_t>(tail.slot0 + b) * kHeads + h + 1u);
     if (d >= kHeadDim) return;
-    finalize_head(a, b, h, merged);
+    finalize_head(tail, b, h, merged);
     SKV_STAMP(5);
     SKV_STAMP_FLAG(1);
     SKV_STAMP_FLUSH();
@@ -767,7 +809,7 @@ __global__ __launch_bounds__(WAVES * 64) void step_kernel(StepArgs a) {
     // (tag 0 is never current), so no word left from 2^32-1 launches ago can
     // pass for a current one.
     if (tag == 0xffffffffu) {
-        for (int i = d; i < a.slot_stride * kSlotWords; i += kHeadDim)
+        for (int i = d; i < tail.slot_stride * kSlotWords; i += kHeadDim)
             __hip_atomic_store(slots + i, uint64_t(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     if (d == 0)
@@ -1028,17 +1070,35 @@ hipError_t launch_fill_u64(uint64_t* p, size_t n, uint64_t value, hipStream_t s)
 }
 
 template <int WAVES, int BLOCK>
-hipError_t launch_step_shape(const StepArgs& a, dim3 grid, InputFormat in, hipStream_t s) {
+hipError_t launch_step_shape(const StepArgs& a, const StepPreload& p, dim3 grid, InputFormat in, hipStream_t s) {
     constexpr int NI = BLOCK / 8;
     const dim3 block(WAVES * 64);
+#define SKV_STEP_ARGS p.layer_pages, p.geometry, p.dispatch, a.q, a.k, a.v, a.lut, a.arrivals, a
     switch (in) {
-    case kInF32: step_kernel<kInF32, WAVES, NI><<<grid, block, 0, s>>>(a); break;
-    case kInQ17: step_kernel<kInQ17, WAVES, NI><<<grid, block, 0, s>>>(a); break;
-    case kInParts2: step_kernel<kInParts2, WAVES, NI><<<grid, block, 0, s>>>(a); break;
-    case kInParts4: step_kernel<kInParts4, WAVES, NI><<<grid, block, 0, s>>>(a); break;
+    case kInF32: step_kernel<kInF32, WAVES, NI><<<grid, block, 0, s>>>(SKV_STEP_ARGS); break;
+    case kInQ17: step_kernel<kInQ17, WAVES, NI><<<grid, block, 0, s>>>(SKV_STEP_ARGS); break;
+    case kInParts2: step_kernel<kInParts2, WAVES, NI><<<grid, block, 0, s>>>(SKV_STEP_ARGS); break;
+    case kInParts4: step_kernel<kInParts4, WAVES, NI><<<grid, block, 0, s>>>(SKV_STEP_ARGS); break;
     default: return hipErrorInvalidValue;
     }
+#undef SKV_STEP_ARGS
     return hipGetLastError();
+}
+
+// The preloaded arguments of a launch (StepPreload); launch_step has checked
+// that its geometry and split fit the packing.
+StepPreload step_preload(const StepArgs& a) {
+    StepPreload p;
+    p.layer_pages = page_ptr(a.kv, a.slot0, a.layer, 0);
+    p.geometry = static_cast<uint32_t>(a.kv.seq_cap) | (static_cast<uint32_t>(a.kv.layers) << 16);
+    uint32_t common = StepPreload::kRowsListed;
+    if (a.batch > 0) {
+        common = a.rows[0] >> 8;
+        for (int z = 0; z < a.batch; ++z)
+            if (a.rows[z] != pack_row(z, static_cast<int>(common))) common = StepPreload::kRowsListed;
+    }
+    p.dispatch = common | (static_cast<uint32_t>(a.split_tokens / kSplitQuantum) << 16);
+    return p;
 }
 
 int step_workgroups_per_cu() {
@@ -1051,8 +1111,12 @@ int step_workgroups_per_cu() {
 
 hipError_t launch_step(const StepArgs& a, int grid_splits, StepShape shape, InputFormat in, hipStream_t s) {
     const dim3 grid(grid_splits, kHeads, a.batch);
+    if (a.split_tokens <= 0 || a.split_tokens % kSplitQuantum != 0 || a.split_tokens > kMaxSeq ||
+        a.kv.seq_cap > kMaxSeq || a.kv.layers > 0xffff)
+        return hipErrorInvalidValue;   // outside what StepPreload packs
+    const StepPreload p = step_preload(a);
 #define SKV_LAUNCH_SHAPE(W, B) \
-    if (shape == StepShape{W, B}) return launch_step_shape<W, B>(a, grid, in, s);
+    if (shape == StepShape{W, B}) return launch_step_shape<W, B>(a, p, grid, in, s);
     SWIFTKV_STEP_SHAPES(SKV_LAUNCH_SHAPE)
 #undef SKV_LAUNCH_SHAPE
     return hipErrorInvalidValue;
