@@ -52,9 +52,11 @@ METRIC = "decode-attn µs/layer + achieved HBM GB/s (% of peak), ctx 4096, batch
 TOKEN_HEAD_BYTES = 288
 # Untimed warm-up of the main workload, in seconds, when its cache is large
 # (above SETTLE_MIN_BYTES): the stream runs slower for a second or more after
-# tens of GB have been allocated and filled (see Cache).
+# gigabytes have been allocated and filled (see Cache; a 4.8 GB cache of 16
+# sequences at context 32768 timed right after its fill measured 714 us per
+# launch against 693 settled).
 SETTLE_S = 1.5
-SETTLE_MIN_BYTES = 8 << 30
+SETTLE_MIN_BYTES = 4 << 30
 
 
 def step_bytes(position: int, parts: int = 1) -> int:
