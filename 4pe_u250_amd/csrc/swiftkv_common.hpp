@@ -142,9 +142,10 @@ __host__ __device__ inline uint32_t pack_row(int seq, int pos) {
     return (static_cast<uint32_t>(pos) << 8) | static_cast<uint32_t>(seq);
 }
 
-// The step kernel's leading arguments, preloaded into SGPRs (12 of the 14
-// user SGPRs left beside the argument-block pointer): everything its first
-// loads depend on, derived from a StepArgs by the launcher.
+// The packed leading arguments of the step kernel, derived from a StepArgs
+// by the launcher.  With q, k, v, the RoPE table and the arrival words they
+// fill the 14 user SGPRs left beside the argument-block pointer, preloaded
+// by the dispatcher: everything the kernel's first loads depend on.
 //   layer_pages: the page of (sequence 0 of the launch, layer, head 0);
 //                page (b, h) = layer_pages + (b * layers * 32 + h) * seq_cap * 288
 //   geometry:    seq_cap (bits 0-15) | layers (bits 16-31)
