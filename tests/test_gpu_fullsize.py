@@ -199,21 +199,27 @@ def test_batch64_32layer_arena(skv, ctx, rope_tables, ragged):
 
 
 @pytest.mark.parametrize("entry", ["regular", "noalloc"])
-def test_batch300_split_across_two_launches(skv, ctx, rope_tables, entry):
-    """300 sequences at ragged positions 300..1400 with forced 256-token
-    splits: two launches (256 rows, then 44) whose split heads reuse the same
-    workspace rows (the second launch's tags follow the first's), through the
-    regular entry and through the allocation-free one, whose fixed workspace
-    holds the split slots of 32 sequences, so it runs them as 10 launches of
-    at most 32 sequences with the same plan: its outputs must equal the
-    regular entry's bit for bit.  Every sequence's appended row bit-exact;
-    the outputs of sequences on both sides of the launch boundaries checked
-    in full against the oracle."""
+@pytest.mark.parametrize("kind", ["ragged", "uniform"])
+def test_batch300_split_across_two_launches(skv, ctx, rope_tables, entry, kind):
+    """300 sequences at ragged positions 300..1400 (or all at position 1400)
+    with forced 256-token splits: two launches (256 rows, then 44) whose split
+    heads reuse the same workspace rows (the second launch's tags follow the
+    first's), through the regular entry and through the allocation-free one,
+    whose fixed workspace holds the split slots of 32 sequences, so it runs
+    them as 10 launches of at most 32 sequences with the same plan: its
+    outputs must equal the regular entry's bit for bit.  A launch whose
+    sequences share one position computes its rows in the kernel instead of
+    reading them (the uniform case, whose launches start at cache slots 0,
+    32, ..., 256).  Every sequence's appended row bit-exact; the outputs of
+    sequences on both sides of the launch boundaries checked in full against
+    the oracle."""
     cos, sin = rope_tables
     batch, seed = 300, 7300
     rng = np.random.default_rng(seed)
     positions = rng.integers(300, 1401, batch).astype(np.int32)
-    _note(f"case: batch {batch}, positions 300..1400, 256-token splits, {entry} entry")
+    if kind == "uniform":
+        positions[:] = 1400
+    _note(f"case: batch {batch}, {kind} positions up to 1400, 256-token splits, {entry} entry")
     lut = skv.RopeLut.generate(ctx, 4096)
     kv = skv.KVCache(ctx, layers=1, max_batch=batch, max_seq_len=1408)
     kv.fill_synthetic(lut, ntok=1400, seed=seed)

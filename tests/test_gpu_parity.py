@@ -143,6 +143,28 @@ def test_randomized_small_batches(skv, ctx, lut4096, rope_tables, seed):
               split=split, q17=q17)
 
 
+# A launch whose sequences all stand at one position computes its rows in the
+# kernel; the others read them from the argument block.
+@pytest.mark.parametrize("batch,pos,split,shape,layers,layer,cap,q17", [
+    (3, 1000, 0, None, 3, 2, None, False),
+    (5, 4095, 1024, (8, 64), 1, 0, None, True),
+    (9, 2047, 0, (4, 64), 1, 0, None, False),
+    (2, 3000, 0, None, 2, 1, 8192, False),
+    (17, 300, 256, None, 1, 0, None, True),
+    (260, 40, 0, None, 1, 0, None, False),
+], ids=["b3_layer2of3", "b5_split1024_8x64_q17", "b9_4x64", "b2_cap8192_layer1of2", "b17_split256_q17",
+        "b260_two_launches"])
+def test_uniform_batches(skv, ctx, lut4096, rope_tables, batch, pos, split, shape, layers, layer, cap, q17):
+    """Batches whose sequences share one position (rows computed in the
+    kernel): split and unsplit heads, every compiled shape, a cache of
+    8192-token pages, a layer past the first, and 260 sequences over two
+    launches (the second starting at cache slot 256)."""
+    _note(f"case: uniform batch {batch} at position {pos}, split {split}, shape {shape}, layer {layer} of {layers}, "
+          f"cap {cap}, q17 {q17}")
+    _scenario(skv, ctx, lut4096, rope_tables, [pos] * batch, seed=9900 + batch, layers=layers, layer=layer,
+              cap=cap, split=split, q17=q17, shape=shape)
+
+
 _EDGE_POSITIONS = [0, 1, 31, 32, 33, 63, 64, 65, 255, 256, 257, 300]
 
 
