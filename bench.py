@@ -631,8 +631,10 @@ def main():
         r = run_gpu(skv, ctx, main, lengths - 1, 1, 100, args.warmup, seed=2030, graph=False)
         extra["batch64_ragged_1layer"] = dict(summary(r, graph=False), length_seed=4, lengths="U{256..4096}")
         sweep = {}
-        for b in (2, 4, 8, 16, 32):   # the batch sizes between the two headline ones, 32 layers at context 4096
-            r = run_gpu(skv, ctx, main, np.full(b, args.context - 1), 32, 5, 1, seed=2040 + b, graph=False)
+        # The batch sizes between the two headline ones, 32 layers at context 4096.  Three warm-up steps: the
+        # first steps after a workload of another batch size run 0.1-0.4 us/layer slower.
+        for b in (2, 4, 8, 16, 32):
+            r = run_gpu(skv, ctx, main, np.full(b, args.context - 1), 32, 20, 3, seed=2040 + b, graph=False)
             sweep[str(b)] = {"us_per_layer": round(r["us_per_layer"], 2), "gbps": round(r["gbps"], 1),
                              "pct_of_peak": round(r["pct_of_peak"], 2)}
         extra["batch_sweep_position4095_32layers"] = sweep
