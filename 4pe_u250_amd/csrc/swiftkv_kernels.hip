@@ -588,12 +588,23 @@ __device__ __forceinline__ float merge_looped(const uint64_t* slots, int n, int 
 // loads (a wave that had to load them chained three scalar round trips ahead
 // of its first cache block).  Firmware without the feature runs the code
 // object's own prologue, which loads the same SGPRs.  StepPreload (host and
-// kernel) packs them; the rest of the arguments stay in StepArgs.
+// kernel) packs them; the rest of the arguments stay in StepArgs.  `aux` is
+// the arrival words' address, except for the split-K partial formats, whose
+// q/k/v loads need the stride between partials first: for them it carries
+// part_stride as a pointer-sized integer and the arrival words come from
+// StepArgs (their load is not waited for until the end).  It stays a
+// pointer parameter so that the compiler knows the arrival words are global
+// memory: a generic pointer made from an integer is read with a flat load,
+// which counts against both wait counters and made the query conversion wait
+// for the whole first block.
 template <int IN, int WAVES, int NI>
 __global__ __launch_bounds__(WAVES * 64) void step_kernel(const int8_t* layer_pages, uint32_t geometry,
                                                           uint32_t dispatch, const void* q_in, const void* k_in,
-                                                          const void* v_in, const int2* lut, uint64_t* arrivals,
+                                                          const void* v_in, const int2* lut, const void* aux,
                                                           StepArgs a) {
+    constexpr bool kParts = IN >= kInParts2;
+    const int64_t part_stride = kParts ? static_cast<int64_t>(reinterpret_cast<uintptr_t>(aux)) : 0;
+    uint64_t* const arrivals = kParts ? a.arrivals : static_cast<uint64_t*>(const_cast<void*>(aux));
     constexpr int kBlk = 8 * NI;
     SKV_STAMP_DECL;
     SKV_STAMP(0);
@@ -643,11 +654,11 @@ __global__ __launch_bounds__(WAVES * 64) void step_kernel(const int8_t* layer_pa
     const size_t row_elem = static_cast<size_t>(b) * kModelDim + h * kHeadDim + 2 * lane;
     const bool appends = owner && wave == 0;       // this wave writes and forwards the new row
     const int2 row_cs = lut[static_cast<size_t>(pos) * kRopePairs + lane];
-    const InPair<IN> row_q = load_in<IN>(q_in, row_elem, a.part_stride);
+    const InPair<IN> row_q = load_in<IN>(q_in, row_elem, part_stride);
     InPair<IN> row_k{}, row_v{};
     if (appends) {
-        row_k = load_in<IN>(k_in, row_elem, a.part_stride);
-        row_v = load_in<IN>(v_in, row_elem, a.part_stride);
+        row_k = load_in<IN>(k_in, row_elem, part_stride);
+        row_v = load_in<IN>(v_in, row_elem, part_stride);
     }
     const PageReader pr = make_reader(page, cap, c, r);
     const int t_first = t_begin + wave * kBlk;
@@ -1073,12 +1084,14 @@ template <int WAVES, int BLOCK>
 hipError_t launch_step_shape(const StepArgs& a, const StepPreload& p, dim3 grid, InputFormat in, hipStream_t s) {
     constexpr int NI = BLOCK / 8;
     const dim3 block(WAVES * 64);
-#define SKV_STEP_ARGS p.layer_pages, p.geometry, p.dispatch, a.q, a.k, a.v, a.lut, a.arrivals, a
+    const void* arrivals = a.arrivals;
+    const void* part_stride = reinterpret_cast<const void*>(static_cast<uintptr_t>(a.part_stride));
+#define SKV_STEP_ARGS(AUX) p.layer_pages, p.geometry, p.dispatch, a.q, a.k, a.v, a.lut, AUX, a
     switch (in) {
-    case kInF32: step_kernel<kInF32, WAVES, NI><<<grid, block, 0, s>>>(SKV_STEP_ARGS); break;
-    case kInQ17: step_kernel<kInQ17, WAVES, NI><<<grid, block, 0, s>>>(SKV_STEP_ARGS); break;
-    case kInParts2: step_kernel<kInParts2, WAVES, NI><<<grid, block, 0, s>>>(SKV_STEP_ARGS); break;
-    case kInParts4: step_kernel<kInParts4, WAVES, NI><<<grid, block, 0, s>>>(SKV_STEP_ARGS); break;
+    case kInF32: step_kernel<kInF32, WAVES, NI><<<grid, block, 0, s>>>(SKV_STEP_ARGS(arrivals)); break;
+    case kInQ17: step_kernel<kInQ17, WAVES, NI><<<grid, block, 0, s>>>(SKV_STEP_ARGS(arrivals)); break;
+    case kInParts2: step_kernel<kInParts2, WAVES, NI><<<grid, block, 0, s>>>(SKV_STEP_ARGS(part_stride)); break;
+    case kInParts4: step_kernel<kInParts4, WAVES, NI><<<grid, block, 0, s>>>(SKV_STEP_ARGS(part_stride)); break;
     default: return hipErrorInvalidValue;
     }
 #undef SKV_STEP_ARGS
