@@ -152,13 +152,16 @@ def test_randomized_small_batches(skv, ctx, lut4096, rope_tables, seed):
     (2, 3000, 0, None, 2, 1, 8192, False),
     (17, 300, 256, None, 1, 0, None, True),
     (260, 40, 0, None, 1, 0, None, False),
+    (2, 4095, 256, None, 1, 0, None, False),
+    (4, 0, 0, None, 1, 0, None, False),
 ], ids=["b3_layer2of3", "b5_split1024_8x64_q17", "b9_4x64", "b2_cap8192_layer1of2", "b17_split256_q17",
-        "b260_two_launches"])
+        "b260_two_launches", "b2_16splits_looped_merge", "b4_position0"])
 def test_uniform_batches(skv, ctx, lut4096, rope_tables, batch, pos, split, shape, layers, layer, cap, q17):
     """Batches whose sequences share one position (rows computed in the
-    kernel): split and unsplit heads, every compiled shape, a cache of
-    8192-token pages, a layer past the first, and 260 sequences over two
-    launches (the second starting at cache slot 256)."""
+    kernel): split and unsplit heads (16 splits: the looped merge), every
+    compiled shape, a cache of 8192-token pages, a layer past the first, 260
+    sequences over two launches (the second starting at cache slot 256), and
+    position 0 (only the forwarded new row)."""
     _note(f"case: uniform batch {batch} at position {pos}, split {split}, shape {shape}, layer {layer} of {layers}, "
           f"cap {cap}, q17 {q17}")
     _scenario(skv, ctx, lut4096, rope_tables, [pos] * batch, seed=9900 + batch, layers=layers, layer=layer,
