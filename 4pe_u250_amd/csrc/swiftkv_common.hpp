@@ -143,9 +143,10 @@ __host__ __device__ inline uint32_t pack_row(int seq, int pos) {
 }
 
 // The packed leading arguments of the step kernel, derived from a StepArgs
-// by the launcher.  With q, k, v, the RoPE table and the arrival words they
-// fill the 14 user SGPRs left beside the argument-block pointer, preloaded
-// by the dispatcher: everything the kernel's first loads depend on.
+// by the launcher.  With q, k, v, the RoPE table and the arrival words (or,
+// for the split-K partial formats, the part stride) they fill the 14 user
+// SGPRs left beside the argument-block pointer, preloaded by the dispatcher:
+// everything the kernel's first loads depend on.
 //   layer_pages: the page of (sequence 0 of the launch, layer, head 0);
 //                page (b, h) = layer_pages + (b * layers * 32 + h) * seq_cap * 288
 //   geometry:    seq_cap (bits 0-15) | layers (bits 16-31)
