@@ -90,3 +90,66 @@ def test_noalloc_entry_matches_the_allocating_entry(skv, ctx):
     for kv in caches:
         kv.close()
     lut.close()
+
+
+def test_noalloc_entry_under_graph_capture(skv, ctx):
+    """The allocation-free entry recorded into a HIP graph (its purpose: a
+    caller under capture cannot allocate): every layer of a 3-sequence step
+    at position 2047 (two splits per head, so every head goes through the
+    per-GPU workspace), replayed three times with eager calls between the
+    replays that advance the workspace's generations (an eager batch-1 call
+    with eight splits per head, on the same workspace rows).  Every replay
+    must equal the eager step bit for bit."""
+    layers, batch, pos = 4, 3, 2047
+    _note(f"case: allocation-free entry in a graph, {layers} layers x batch {batch} at position {pos}")
+    lut = skv.RopeLut.generate(ctx, 4096)
+    kv = skv.KVCache(ctx, layers=layers, max_batch=batch, max_seq_len=2048)
+    kv.fill_synthetic(lut, ntok=pos, seed=521)
+    n = layers * batch * 4096
+    bufs = [ctx.alloc(n * 4) for _ in range(3)]
+    for i, b in enumerate(bufs):
+        ctx.fill_synthetic(b, n, 522, 60 + i)
+    outs = [ctx.alloc(batch * 4096 * 4) for _ in range(layers)]
+    aqs = [ctx.alloc(batch * 128 * 56) for _ in range(layers)]
+    ass = [ctx.alloc(batch * 128) for _ in range(layers)]
+    positions = np.full(batch, pos, np.int32)
+    stride = batch * 4096 * 4
+
+    def step():
+        for layer in range(layers):
+            q, k, v = (b.ptr + layer * stride for b in bufs)
+            skv.swiftkv_attention_noalloc(ctx, q, k, v, kv, lut, aqs[layer], ass[layer], layer, positions,
+                                          outs[layer])
+
+    def snapshot():
+        ctx.synchronize()
+        return [(o.download(np.uint32, (batch, 4096)), a.download(np.uint8, (batch, 128, 56)),
+                 s.download(np.uint8, (batch, 128))) for o, a, s in zip(outs, aqs, ass)]
+
+    step()
+    ref = snapshot()
+    for r in ref:
+        assert np.isfinite(r[0].view(np.float32)).all()
+    extra = ctx.alloc(4096 * 4)
+    ctx.capture_begin()
+    step()
+    g = ctx.capture_end()
+    try:
+        for rep in range(3):
+            for o in outs:
+                o.zero()
+            ctx.synchronize()
+            g.launch()
+            got = snapshot()
+            for layer in range(layers):
+                for x, y in zip(ref[layer], got[layer]):
+                    assert np.array_equal(x, y), f"replay {rep}, layer {layer}"
+            # eager work between the replays on the same workspace rows
+            skv.swiftkv_attention_noalloc(ctx, bufs[0], bufs[1], bufs[2], kv, lut, None, None, 0, [pos], extra)
+            ctx.synchronize()
+    finally:
+        g.close()
+    for x in bufs + outs + aqs + ass + [extra]:
+        x.free()
+    kv.close()
+    lut.close()
