@@ -148,6 +148,23 @@ def _host_ptr(a: np.ndarray):
     return a.ctypes.data_as(C.c_void_p)
 
 
+_INT32_MIN, _INT32_MAX = -(1 << 31), (1 << 31) - 1
+
+
+def _positions(ctx: "Context", position):
+    """(address, count, owner) of a step's positions as int32, `owner` keeping
+    the memory alive across the call.  A single position (the latency-bound
+    batch-1 step) goes through the context's one-element buffer: building a
+    numpy array and its ctypes view cost several microseconds per call, more
+    than a short step takes on the GPU."""
+    if isinstance(position, (int, np.integer)) and _INT32_MIN <= position <= _INT32_MAX:
+        buf = ctx._one_position
+        buf[0] = int(position)
+        return C.addressof(buf), 1, buf
+    pos = np.ascontiguousarray(np.atleast_1d(np.asarray(position, dtype=np.int32)))
+    return pos.ctypes.data, int(pos.size), pos
+
+
 class DeviceBuffer:
     """A device allocation with numpy-style upload/download (no framework needed)."""
 
@@ -206,6 +223,7 @@ class Context:
         self.handle = h.value
         self.device = device
         self.host_io = False
+        self._one_position = (C.c_int32 * 1)()
 
     def close(self) -> None:
         if self.handle:
@@ -473,13 +491,13 @@ def swiftkv_attention(ctx: Context, q, k, v, kv_cache: KVCache, rope_lut: RopeLu
     device [batch][128][56] bytes and [batch][128] E8M0 codes, or None.
     Asynchronous on the context stream.
     """
-    pos = np.ascontiguousarray(np.atleast_1d(np.asarray(position, dtype=np.int32)))
+    pos, batch, _keep = _positions(ctx, position)
     fn = lib().swiftkv_attention_q17 if q17 else lib().swiftkv_attention_f32
-    _check_io_sizes(ctx, pos.size, q, k, v, out, activation_q, activation_scale)
+    _check_io_sizes(ctx, batch, q, k, v, out, activation_q, activation_scale)
     it = np.int32 if q17 else np.float32
     _check(fn(ctx.handle, _io_ptr(ctx, q, it), _io_ptr(ctx, k, it), _io_ptr(ctx, v, it), kv_cache.handle,
               rope_lut.handle, _io_ptr(ctx, activation_q, np.uint8, True),
-              _io_ptr(ctx, activation_scale, np.uint8, True), int(layer_index), _host_ptr(pos), int(pos.size),
+              _io_ptr(ctx, activation_scale, np.uint8, True), int(layer_index), pos, batch,
               _io_ptr(ctx, out, np.float32, True)))
 
 
@@ -505,10 +523,10 @@ def swiftkv_attention_noalloc(ctx: Context, q, k, v, kv_cache: KVCache, rope_lut
     split workspace is the library's fixed per-GPU array, so the call never
     allocates device memory.  Calls that overlap in time on one GPU race.
     Device pointers only (host-memory I/O mode is refused)."""
-    pos = np.ascontiguousarray(np.atleast_1d(np.asarray(position, dtype=np.int32)))
+    pos, batch, _keep = _positions(ctx, position)
     _check(lib().swiftkv_attention_f32_noalloc(ctx.handle, _ptr(q), _ptr(k), _ptr(v), kv_cache.handle,
                                                rope_lut.handle, _ptr(activation_q), _ptr(activation_scale),
-                                               int(layer_index), _host_ptr(pos), int(pos.size), _ptr(out)))
+                                               int(layer_index), pos, batch, _ptr(out)))
 
 
 def swiftkv_attention_partials(ctx: Context, q, k, v, parts: int, kv_cache: KVCache, rope_lut: RopeLut,
@@ -523,8 +541,7 @@ def swiftkv_attention_partials(ctx: Context, q, k, v, parts: int, kv_cache: KVCa
     1655-1667, 1089-1118) -- then converts to Q15.17 and proceeds as
     swiftkv_attention.  Asynchronous on the context stream.
     """
-    pos = np.ascontiguousarray(np.atleast_1d(np.asarray(position, dtype=np.int32)))
-    batch = int(pos.size)
+    pos, batch, _keep = _positions(ctx, position)
     stride = batch * 4096 if part_stride is None else int(part_stride)
     _check_io_sizes(ctx, batch, q, k, v, out, activation_q, activation_scale,
                     in_elems=(int(parts) - 1) * stride + batch * 4096 if int(parts) > 1 else None)
@@ -533,7 +550,7 @@ def swiftkv_attention_partials(ctx: Context, q, k, v, parts: int, kv_cache: KVCa
                                             int(parts), stride, kv_cache.handle, rope_lut.handle,
                                             _io_ptr(ctx, activation_q, np.uint8, True),
                                             _io_ptr(ctx, activation_scale, np.uint8, True), int(layer_index),
-                                            _host_ptr(pos), batch, _io_ptr(ctx, out, np.float32, True)))
+                                            pos, batch, _io_ptr(ctx, out, np.float32, True)))
 
 
 def swiftkv_attention_exact(ctx: Context, q, k, v, kv_cache: KVCache, rope_lut: RopeLut,
@@ -550,14 +567,14 @@ def swiftkv_attention_exact(ctx: Context, q, k, v, kv_cache: KVCache, rope_lut: 
     position must be below 4096, the reference's bound (SwiftKVError ERANGE
     otherwise, with nothing enqueued).
     """
-    pos = np.ascontiguousarray(np.atleast_1d(np.asarray(position, dtype=np.int32)))
-    _check_io_sizes(ctx, pos.size, q, k, v, out_q17, activation_q, activation_scale)
+    pos, batch, _keep = _positions(ctx, position)
+    _check_io_sizes(ctx, batch, q, k, v, out_q17, activation_q, activation_scale)
     it = np.int32 if q17 else np.float32
     _check(lib().swiftkv_attention_exact(ctx.handle, _io_ptr(ctx, q, it), _io_ptr(ctx, k, it),
                                          _io_ptr(ctx, v, it), 1 if q17 else 0, kv_cache.handle, rope_lut.handle,
                                          _io_ptr(ctx, activation_q, np.uint8, True),
                                          _io_ptr(ctx, activation_scale, np.uint8, True), int(layer_index),
-                                         _host_ptr(pos), int(pos.size), _io_ptr(ctx, out_q17, np.int32, True)))
+                                         pos, batch, _io_ptr(ctx, out_q17, np.int32, True)))
 
 
 def swiftkv_append_tokens(ctx: Context, k, v, kv_cache: KVCache, rope_lut: RopeLut, layer_index: int,
