@@ -22,7 +22,12 @@ from the first workgroup's start, medians over the repetitions:
                  workgroup's start to the last one's end (dispatch, completion
                  and the gap to the next launch);
   - per XCD:     workgroups, their median span from entry to end, and the
-                 XCD's last workgroup end.
+                 XCD's last workgroup end;
+  - per wave:    each wave slot's mean first-block arrival and scan end, and
+                 the median first-block spread inside a workgroup;
+  - merges:      split heads' mergers, and how many sit on odd XCDs;
+  - dispatch:    the XCD of grid index i is (i + offset) mod 8 when one offset
+                 holds for the whole launch.
 With --parts N (2 or 4) the steps go through swiftkv_attention_partials, fed
 N split-K FP32 partials of q, k and v.
 Diagnostics only: nothing here is the product path, and the product library
@@ -50,8 +55,9 @@ def pct(x, q):
     return float(np.percentile(x, q)) if x.size else float("nan")
 
 
-def launch_phases(ph, wv, nwg):
-    """Phase times (us) of one launch from its stamps."""
+def launch_phases(ph, wv, nwg, index=None):
+    """Phase times (us) of one launch from its stamps; `index`: the live
+    workgroups' linear grid indices (for the dispatch order)."""
     ph = ph[:nwg].astype(np.int64)
     wv = wv[:nwg].astype(np.int64)
     t0 = ph[:, 0].min()
@@ -79,6 +85,20 @@ def launch_phases(ph, wv, nwg):
     d["xcd_workgroup_us_p50"] = [pct((end - entry)[xcd == x], 50) if (xcd == x).any() else float("nan")
                                   for x in range(8)]
     d["xcd_done"] = [float(np.max(end[xcd == x])) if (xcd == x).any() else float("nan") for x in range(8)]
+    # Per wave slot (waves that stamped): mean first-block arrival and scan
+    # end, and the median spread of first-block arrivals inside a workgroup.
+    waves = int(np.max(np.sum(wv[:, :, 0] > 0, axis=1)))
+    d["wave_first_block_mean"] = [float(np.nanmean(wd[:, w])) for w in range(waves)]
+    d["wave_scan_end_mean"] = [float(np.nanmean(we[:, w])) for w in range(waves)]
+    d["first_block_spread_p50"] = pct(np.nanmax(wd[:, :waves], axis=1) - np.nanmin(wd[:, :waves], axis=1), 50)
+    # The split that counted last and merged: how many sit on odd XCDs.
+    d["mergers"] = int(merger.sum())
+    d["mergers_on_odd_xcd"] = int((merger & (xcd % 2 == 1)).sum())
+    # Dispatch order: XCD minus linear grid index, mod 8, when one value
+    # holds for every workgroup of the launch (-1 otherwise).
+    if index is not None:
+        offs = np.unique((xcd - np.asarray(index, np.int64)) % 8)
+        d["dispatch_xcd_offset"] = int(offs[0]) if offs.size == 1 else -1
     return d
 
 
@@ -146,7 +166,7 @@ def main():
             nwg = int(live.sum())
             if args.raw:
                 raw.append((np.flatnonzero(live), ph[live].copy(), wv[live].copy()))
-            d = launch_phases(ph[live], wv[live], nwg)
+            d = launch_phases(ph[live], wv[live], nwg, index=np.flatnonzero(live))
             d["us_per_layer"] = us_layer
             d["launch"] = us_layer - d["span"]
             d["workgroups"] = nwg
