@@ -337,14 +337,14 @@ int upload_lut(swiftkv_context* ctx, std::vector<int2>&& host, int32_t positions
 // or step_per_cu 4-wave workgroups per CU.  So
 //   batch x 32 heads <= CUs:  splits = CUs / heads (at most 8);
 //   otherwise:                splits = step_per_cu x CUs / heads (at least 1),
-// rounded to whole 256-token quanta.  Measured at context 4096 on 256 CUs
-// (3 workgroups per CU), us/layer with this rule against other splits:
-//   batch 1: 8 splits (12.0); batch 2: 4 (18.1; 19.2 with 8);
-//   batch 3 and 4: 2 (23.3 and 29.0; 24.4 and 32.8 with 8);
-//   batch 5 to 8: none (35.2 to 52.0; 38.2 to 55.0 with more);
-//   batch 12: 2 (76.9; 81.2 with none); batch 16 and 32: none (98.4 and
-//   189.8; 101.2 and 192.1 with 4 and 2); batch 64: none (361; 377 with 2);
-//   batch 16 at context 32K: none (715.5; 722.9 with 4).
+// rounded to whole 256-token quanta.  Measured on 256 CUs, 32 layers,
+// us/layer with this rule's split against forced ones:
+//   batch 1, context 4096: 512 tokens (8 splits) 10.44-10.47; 768 10.72,
+//   1024 11.8-12.1;  context 2048: 256 (8 splits) 7.94-7.98; 512 8.45-8.72;
+//   batch 2: 1024 (4 splits) 15.79-15.89; 512 16.5-16.7, 1280 16.3-16.4;
+//   batch 3 and 4: 2048 (2 splits) 21.4 and 26.6; 1024 23.9 and 27.8;
+//   batch 8: none 47.4; 2048 49.6-49.9.  Earlier builds: batch 16, 32 and
+//   64 unsplit (98.4, 189.8, 361 against 101.2, 192.1, 377 with 4, 2, 2).
 // No split is longer than kMaxSplitTokensHeuristic: on long contexts a
 // split's exchange is small against its scan and finer work balances better
 // (batch 16 decoding from position 32256: 698 us/step with 8192-token splits
@@ -388,7 +388,9 @@ int32_t choose_split(const SplitPolicy& pol, const int32_t* positions, int32_t b
 // length or the split, whichever is less); otherwise 4 waves on 64-token
 // blocks, three workgroups per CU overlapping each other's prologues.
 // 32 layers, us/layer, one process, interleaved rounds, against the 4-wave
-// shape: batch 1 to 8 at context 4096 10.75 / 16.16 / 26.85 / 47.65 against
+// shape (measured before the leading kernel arguments were preloaded, which
+// took about 0.4 us off every small launch in every shape): batch 1 to 8 at
+// context 4096 10.75 / 16.16 / 26.85 / 47.65 against
 // 12.05 / 17.42 / 28.14 / 49.0 (and 11.25 / 16.45 / 27.55 / 48.5 with 16
 // waves on 32-token blocks); batch 1 at context 2048 8.47 against 8.76;
 // batch 12 (two splits) 72.6 against 73.55; batch 16 92.4 against 93.0;
