@@ -2,9 +2,11 @@
 // stage.
 //
 // step kernel (one launch per decode step and layer), grid (splits, 32 heads,
-// batch rows) of 4-wave workgroups on 64-token blocks (8 waves on 32-token
-// blocks when the launch has at most one workgroup per CU); workgroup
-// (j, h, z) owns tokens
+// batch rows) of workgroups in one of three shapes, chosen by the host per
+// launch: 8 waves on 32-token blocks for launches of up to one residency round
+// of 4-wave workgroups, 8 waves on 64-token blocks for larger launches whose
+// every range holds at least 2048 tokens, 4 waves on 64-token blocks for the
+// rest; workgroup (j, h, z) owns tokens
 // [j*C, min((j+1)*C, position+1)) of head h of the sequence that row z names
 // (rows come longest first, so a ragged batch does not end on long heads):
 //   1. every lane loads its channel pair of the new row's q (and, in the one
@@ -18,8 +20,8 @@
 //      G32-quantizes the new K/V row, appends it to the cache, and forwards it
 //      into its own merge as one more partial -- the new token is written once
 //      and never read back (the reference does the same, hpp:37-41);
-//   3. the waves scan the cached tokens in 64-token (8 waves: 32-token)
-//      blocks.  Lane = (chunk c = lane&7, row r = lane>>3): one nontemporal
+//   3. the waves scan the cached tokens in blocks taken round-robin.
+//      Lane = (chunk c = lane&7, row r = lane>>3): one nontemporal
 //      dwordx4 per lane reads a 16-channel chunk, so one wave instruction
 //      covers 8 full 128-B code rows.  K rows are dotted with the query limbs
 //      by v_dot4 on the int8 codes, V codes are dequantized in VGPRs, partial
