@@ -159,3 +159,39 @@ def test_every_entry_on_one_workload(skv, ctx, lut4096, rope_tables, case):
         ctx.set_split_tokens(0)
         ctx.debug_set_step_shape(0, 0)
         kv.close()
+
+
+@pytest.mark.parametrize("layers,layer,batch,positions_hi,cap", [
+    (64, 63, 3, 300, 320),        # the most layers a cache holds, its last layer
+    (1, 0, 4096, 63, 64),         # the most sequences a cache holds, one call: 16 launches, slots up to 4095
+])
+def test_extreme_cache_geometry(skv, ctx, lut4096, rope_tables, layers, layer, batch, positions_hi, cap):
+    """The step at the cache's limits: pages addressed through every layer of a
+    64-layer cache, and a 4096-sequence call whose later launches start at
+    high cache slots (page offsets past 2^31 bytes).  Sampled sequences against
+    the oracle: every cached and appended row bit-exact, the FP32 output
+    within tolerance."""
+    cos, sin = rope_tables
+    seed = 65000 + batch + layers
+    rng = np.random.default_rng(seed)
+    positions = [int(p) for p in rng.integers(0, positions_hi + 1, batch)]
+    positions[-1] = positions_hi
+    _note(f"case: {layers} layers (layer {layer}), batch {batch}, positions up to {positions_hi}, cap {cap}")
+    kv = skv.KVCache(ctx, layers=layers, max_batch=batch, max_seq_len=cap)
+    bufs = []
+    try:
+        kv.fill_synthetic(lut4096, ntok=positions_hi, seed=seed, layer0=layer, nlayers=1)
+        q, k, v = (np.random.default_rng(seed + i).standard_normal((batch, 4096)).astype(np.float32) for i in range(3))
+        bufs = [ctx.to_device(x) for x in (q, k, v)]
+        out = _step(skv, ctx, "f32", batch, *bufs, kv, lut4096, layer, positions)[0].view(np.float32)
+        qq, kq, vq = O.f2q17(q), O.f2q17(k), O.f2q17(v)
+        for b in sorted({0, batch // 2, batch - 1}):
+            p = positions[b]
+            sc = oracle_cache_synthetic(skv, ctx, cos, sin, seed, b, layer, p, p + 1)
+            res = sc.step_q17(qq[b], kq[b], vq[b], p, cos[p], sin[p], fp=True)
+            assert_rows_equal(kv, sc, b, layer, 0, p + 1)
+            assert_close(out[b].reshape(H, 128), res["fp"], f"seq {b} position {p}")
+    finally:
+        for x in bufs:
+            x.free()
+        kv.close()
