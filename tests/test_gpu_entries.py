@@ -195,3 +195,40 @@ def test_extreme_cache_geometry(skv, ctx, lut4096, rope_tables, layers, layer, b
         for x in bufs:
             x.free()
         kv.close()
+
+
+def test_long_context_entries_agree(skv, ctx, rope_tables):
+    """Contexts of 20001 and 32768 tokens (4 splits of 8192 per head): the
+    FP32, Q15.17, allocation-free and 4-part split-K entries give the same
+    bits (outputs, A14/E8M0 words, appended rows).  The FP32 entry at these
+    lengths is checked against the oracle by the long-context decode test."""
+    _note("case: batch 2 at positions 32767 and 20000, cap 32768, every fast entry")
+    lut = skv.RopeLut.generate(ctx, 32768)
+    kv = skv.KVCache(ctx, layers=1, max_batch=2, max_seq_len=32768)
+    positions = [32767, 20000]
+    bufs = []
+    try:
+        kv.fill_synthetic(lut, ntok=32767, seed=66001, dist=skv.DIST_STUDENT_T3)
+        parts = np.stack([np.random.default_rng(66002 + j).standard_normal((3, 2, 4096)).astype(np.float32)
+                          for j in range(4)], axis=1)   # [tensor][part][batch][4096]
+        red = [O.reduce_partials(parts[i]) for i in range(3)]
+        dparts = [ctx.to_device(parts[i].reshape(-1)) for i in range(3)]
+        dred = [ctx.to_device(x) for x in red]
+        dq17 = [ctx.to_device(O.f2q17(x)) for x in red]
+        bufs = dparts + dred + dq17
+        ref = _step(skv, ctx, "f32", 2, *dred, kv, lut, 0, positions)
+        ref_rows = _new_rows(kv, positions, 0, [0, 1])
+        for entry, args, extra in (("q17", dq17, {}), ("noalloc", dred, {}),
+                                   ("parts", dparts, {"parts": 4, "stride": 2 * 4096})):
+            got = _step(skv, ctx, entry, 2, *args, kv, lut, 0, positions, **extra)
+            for a, b_, what in zip(got, ref, ("FP32 output", "A14 words", "E8M0 codes")):
+                assert (a == b_).all(), f"{entry}: {what} differ from the f32 entry"
+            for x, y in zip(_new_rows(kv, positions, 0, [0, 1]), ref_rows):
+                for u, w in zip(x, y):
+                    assert (u.view(np.uint8) == w.view(np.uint8)).all(), f"{entry}: appended row differs"
+        assert np.isfinite(ref[0].view(np.float32)).all()
+    finally:
+        for x in bufs:
+            x.free()
+        kv.close()
+        lut.close()
