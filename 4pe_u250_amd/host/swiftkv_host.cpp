@@ -20,6 +20,7 @@
 //   swiftkv_host --decode --batch 16 --context 32257 --steps 512 --layers 1 --t3
 //   swiftkv_host --exact --batch 4 --context 1024 --rope-lut rope_lut.bin
 //   swiftkv_host --batch 64 --parts 4
+//   swiftkv_host --batch 1 --noalloc --graph
 //   swiftkv_host --batch 3 --layers 2 --context 700 --steps 2 --dump /tmp/run
 #include "swiftkv.h"
 
@@ -124,6 +125,7 @@ struct Config {
     bool q17 = false;         // Q15.17 inputs (swiftkv_attention_q17)
     bool exact = false;       // integer-compatibility entry
     int parts = 1;            // split-K FP32 partials per input (swiftkv_attention_partials) when 2 or 4
+    bool noalloc = false;     // the allocation-free entry (swiftkv_attention_f32_noalloc)
     bool decode = false;      // step s runs at position context-1+s, appending as it goes
     bool graph = false;       // record one step as a HIP graph and replay it
     bool host_io = false;     // host-memory q/k/v and outputs
@@ -149,6 +151,8 @@ void print_usage(const char* program) {
         << "  --exact          the integer-compatibility entry (bit-exact A14 words)\n"
         << "  --parts N        inputs as N = 2 or 4 split-K FP32 partial sums (swiftkv_attention_partials;\n"
         << "                   with --exact they are finalized once by swiftkv_convert_partials_q17)\n"
+        << "  --noalloc        the allocation-free entry (swiftkv_attention_f32_noalloc: FP32 device inputs,\n"
+        << "                   split workspace in the library's fixed per-GPU array)\n"
         << "  --decode         advance the position every step (a real decode run)\n"
         << "  --graph          record one step as a HIP graph and time its replays\n"
         << "  --host-io        inputs and outputs in host memory (PCIe included)\n"
@@ -214,6 +218,8 @@ Config parse_args(int argc, char** argv, bool* help) {
         } else if (a == "--parts") {
             c.parts = static_cast<int>(parse_integer(a, value(), 1, 4));
             if (c.parts == 3) throw std::runtime_error("--parts must be 1, 2 or 4");
+        } else if (a == "--noalloc") {
+            c.noalloc = true;
         } else if (a == "--decode") {
             c.decode = true;
         } else if (a == "--graph") {
@@ -236,6 +242,8 @@ Config parse_args(int argc, char** argv, bool* help) {
         throw std::runtime_error("--graph replays the recorded positions; it cannot advance them (--decode)");
     if (c.host_io && c.graph) throw std::runtime_error("--host-io calls synchronize; they cannot be recorded (--graph)");
     if (c.parts > 1 && c.q17) throw std::runtime_error("--parts gives FP32 partial sums; it excludes --q17");
+    if (c.noalloc && (c.q17 || c.exact || c.parts > 1 || c.host_io))
+        throw std::runtime_error("--noalloc takes FP32 device inputs; it excludes --q17, --exact, --parts and --host-io");
     const long long last = static_cast<long long>(c.context) - 1 + (c.decode ? c.steps - 1 : 0);
     if (last >= SWIFTKV_MAX_SEQ) {
         std::ostringstream msg;
@@ -392,6 +400,11 @@ int run(const Config& cfg) {
                                                  static_cast<std::int64_t>(all_elems), kv.p, lut.p, aq, as, layer,
                                                  positions.data(), cfg.batch, static_cast<float*>(o)),
                       "swiftkv_attention_partials");
+            } else if (cfg.noalloc) {
+                check(swiftkv_attention_f32_noalloc(ctx.p, static_cast<const float*>(q), static_cast<const float*>(k),
+                                                    static_cast<const float*>(v), kv.p, lut.p, aq, as, layer,
+                                                    positions.data(), cfg.batch, static_cast<float*>(o)),
+                      "swiftkv_attention_f32_noalloc");
             } else if (cfg.q17) {
                 check(swiftkv_attention_q17(ctx.p, static_cast<const std::int32_t*>(q),
                                             static_cast<const std::int32_t*>(k), static_cast<const std::int32_t*>(v),
@@ -498,6 +511,7 @@ int run(const Config& cfg) {
              << ", \"distribution\": " << dist << ", \"outliers\": " << (cfg.outliers ? "true" : "false")
              << ", \"parts\": " << cfg.parts << ", \"q17\": " << (cfg.q17 ? "true" : "false")
              << ", \"exact\": " << (cfg.exact ? "true" : "false")
+             << ", \"noalloc\": " << (cfg.noalloc ? "true" : "false")
              << ", \"input_layout\": \"[part][layer][batch][4096] FP32\""
              << ", \"output\": \"" << (cfg.exact ? "int32 Q15.17" : "float32") << " [batch][4096]\""
              << ", \"appended\": \"records [batch][layer][head][320] of token position\"}\n";
@@ -519,6 +533,7 @@ int run(const Config& cfg) {
               << "  batch " << cfg.batch << ", " << cfg.layers << " layers, position " << p0
               << (cfg.decode ? " advancing" : "") << ", " << cfg.steps << " steps"
               << (cfg.exact ? ", integer-compatibility entry" : (cfg.q17 ? ", Q15.17 inputs" : ", FP32 inputs"))
+              << (cfg.noalloc ? ", allocation-free entry" : "")
               << (cfg.parts > 1 ? ", " + std::to_string(cfg.parts) + " split-K partials per input" : std::string())
               << (cfg.graph ? ", graph replay" : "") << (cfg.host_io ? ", host-memory I/O" : "") << "\n"
               << "  setup " << setup_ms << " ms; timed " << ms << " ms (" << (cfg.host_io ? "wall" : "device")

@@ -27,7 +27,9 @@ def test_help_and_argument_errors():
                         (["--exact", "--context", "4097"], "--exact keeps the reference's bound"),
                         (["--exact", "--context", "4096", "--decode", "--steps", "2"], "positions below 4096"),
                         (["--theta", "0.5"], "--theta"), (["--parts", "3"], "--parts must be"),
-                        (["--parts", "4", "--q17"], "excludes --q17")):
+                        (["--parts", "4", "--q17"], "excludes --q17"),
+                        (["--noalloc", "--q17"], "--noalloc takes FP32 device inputs"),
+                        (["--noalloc", "--host-io"], "--noalloc takes FP32 device inputs")):
         r = run(*bad)
         assert r.returncode == 1, bad
         assert needle in r.stderr, (bad, r.stderr)
@@ -53,7 +55,7 @@ def _result(r):
 @pytest.mark.gpu
 @pytest.mark.parametrize("mode", [[], ["--q17"], ["--exact"], ["--graph"], ["--host-io"],
                                   ["--decode", "--t3", "--outliers"], ["--parts", "4"], ["--parts", "2", "--host-io"],
-                                  ["--parts", "4", "--exact"]])
+                                  ["--parts", "4", "--exact"], ["--noalloc"], ["--noalloc", "--graph"]])
 def test_host_driver_modes(mode):
     print(f"case: swiftkv_host {' '.join(mode)}", flush=True)
     sys.stdout.flush()
@@ -95,7 +97,7 @@ def _dump_inputs(skv, ctx, meta):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("mode", [[], ["--q17"], ["--parts", "4"], ["--exact"], ["--parts", "4", "--exact"],
-                                  ["--decode", "--t3", "--outliers"], ["--graph"], ["--host-io"]])
+                                  ["--decode", "--t3", "--outliers"], ["--graph"], ["--host-io"], ["--noalloc"]])
 def test_host_driver_dump_matches_the_oracle(skv, ctx, rope_tables, tmp_path, mode):
     """The native host driver's own outputs, dumped with --dump, against the
     oracle on the inputs it generated (the reference host dumps and compares
