@@ -44,47 +44,7 @@
 // once per device and the entry passes that address.
 static __device__ __align__(256) unsigned char scratch[swiftkv::kNoAllocScratchBytes];
 
-// Phase stamps (the instrumented build libswiftkv_stamps.so only, compiled
-// with SWIFTKV_PHASE_STAMPS): per workgroup of the step kernel, thread 0
-// records s_memrealtime (100 MHz) at entry, when wave 0's first loads have
-// all arrived (an added wait for them), after the workgroup's LDS merge,
-// when the arrival count is known, after the merge and after the epilogue;
-// lane 0 of every wave records when its first loads arrived and when its
-// scan ended; slot 7 holds the workgroup's XCD (low half) and HW_ID register
-// (high half: CU, shader array and engine).  The product library compiles
-// every stamp away.
-#ifdef SWIFTKV_PHASE_STAMPS
-constexpr int kStampWorkgroups = 8192;
-constexpr int kStampSlots = 8;   // entry, first loads, LDS merge, arrival, merge, epilogue, flags, XCD + HW_ID
-__device__ unsigned long long g_phase_stamps[kStampWorkgroups * kStampSlots];
-__device__ unsigned long long g_wave_stamps[kStampWorkgroups * 16 * 2];
-#define SKV_STAMP_DECL unsigned long long skv_st[kStampSlots] = {0, 0, 0, 0, 0, 0, 0, 0}
-#define SKV_STAMP(i) do { if (threadIdx.x == 0) skv_st[i] = __builtin_amdgcn_s_memrealtime(); } while (0)
-#define SKV_STAMP_FLAG(f) do { skv_st[6] |= (f); } while (0)
-#define SKV_STAMP_WAIT() __builtin_amdgcn_s_waitcnt(0)
-#define SKV_WAVE_STAMP(k, t) do {                                                                   \
-        const size_t wg_ = (static_cast<size_t>(blockIdx.z) * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x; \
-        if ((threadIdx.x & 63) == 0 && wg_ < kStampWorkgroups)                                      \
-            g_wave_stamps[(wg_ * 16 + (threadIdx.x >> 6)) * 2 + (k)] = (t);                         \
-    } while (0)
-#define SKV_STAMP_FLUSH() do {                                                                      \
-        const size_t wg_ = (static_cast<size_t>(blockIdx.z) * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x; \
-        if (threadIdx.x == 0 && wg_ < kStampWorkgroups) {                                           \
-            unsigned xcc_, hw_;                                                                     \
-            asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc_));                    \
-            asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw_));                      \
-            skv_st[7] = xcc_ | (static_cast<unsigned long long>(hw_) << 32);                        \
-            for (int i_ = 0; i_ < kStampSlots; ++i_) g_phase_stamps[wg_ * kStampSlots + i_] = skv_st[i_]; \
-        }                                                                                           \
-    } while (0)
-#else
-#define SKV_STAMP_DECL do {} while (0)
-#define SKV_STAMP(i) do {} while (0)
-#define SKV_STAMP_FLAG(f) do {} while (0)
-#define SKV_STAMP_WAIT() do {} while (0)
-#define SKV_WAVE_STAMP(k, t) do {} while (0)
-#define SKV_STAMP_FLUSH() do {} while (0)
-#endif
+#include "swiftkv_stamps.hpp"
 
 namespace swiftkv {
 namespace {
@@ -685,9 +645,7 @@ __global__ __launch_bounds__(WAVES * 64) void step_kernel(const int8_t* layer_pa
     // registers before the scan.
     SKV_STAMP_WAIT();
     SKV_STAMP(1);
-#ifdef SWIFTKV_PHASE_STAMPS
-    const unsigned long long skv_first = __builtin_amdgcn_s_memrealtime();
-#endif
+    SKV_WAVE_FIRST_LOADS();
     const int2 qi = in_to_q17<IN>(row_q);
     int32_t q0, q1;
     rope_pair(qi.x, qi.y, row_cs, q0, q1);
@@ -704,10 +662,7 @@ __global__ __launch_bounds__(WAVES * 64) void step_kernel(const int8_t* layer_pa
 
     float m_run, l_run, acc[16];
     scan_range<NI>(pr, bl, Q, t_first, t_stop, WAVES * kBlk, r, m_run, l_run, acc);
-#ifdef SWIFTKV_PHASE_STAMPS
-    SKV_WAVE_STAMP(0, skv_first);
-    SKV_WAVE_STAMP(1, __builtin_amdgcn_s_memrealtime());
-#endif
+    SKV_WAVE_SCAN_DONE();
 
     // The new row: quantize, append; forward (k^ . q', v^) into the merge as
     // one more partial.
@@ -1047,20 +1002,6 @@ __global__ __launch_bounds__(256) void fill_u64_kernel(uint64_t* __restrict__ p,
 
 // ---------------------------------------------------------------- launchers
 
-#ifdef SWIFTKV_PHASE_STAMPS
-// Copies the stamps of the last step launch (workgroups [0, 8192)): phase
-// [8192][8] then wave [8192][16][2] 64-bit words (instrumented build only,
-// not part of the C ABI).
-extern "C" int swiftkv_debug_phase_stamps(unsigned long long* phase, unsigned long long* wave) {
-    if (hipMemcpyFromSymbol(phase, HIP_SYMBOL(g_phase_stamps), sizeof(g_phase_stamps), 0, hipMemcpyDeviceToHost) !=
-        hipSuccess)
-        return -3;
-    return hipMemcpyFromSymbol(wave, HIP_SYMBOL(g_wave_stamps), sizeof(g_wave_stamps), 0, hipMemcpyDeviceToHost) ==
-                   hipSuccess
-               ? 0
-               : -3;
-}
-#endif
 
 hipError_t bind_noalloc_scratch(hipStream_t s, void** device_ptr) {
     static_assert(kNoAllocScratchBytes % 4 == 0 && kNoAllocCounterBytes % 256 == 0, "workspace layout");
