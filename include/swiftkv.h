@@ -26,8 +26,9 @@
  *     no C++ exception crosses the boundary; swiftkv_last_error() describes
  *     the most recent failure of the calling thread;
  *   - tensors passed to the step functions are DEVICE pointers (allocate with
- *     swiftkv_device_alloc or any HIP allocator); position/length arrays are
- *     HOST pointers;
+ *     swiftkv_device_alloc or any HIP allocator), or host pointers in a
+ *     context switched to host-memory I/O (swiftkv_set_host_io);
+ *     position/length arrays are HOST pointers;
  *   - work is issued asynchronously on the context's HIP stream; call
  *     swiftkv_synchronize() before reading results on the host;
  *   - a failure found on the device is reported by the next call that looks
